@@ -1,0 +1,91 @@
+/*
+ * iris_oracle.h - CPU f32 restatement of the reference denoiser forward.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker and the CPU
+ * baseline: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. The product (iris.c_amd/) never links or calls it.
+ *
+ * It restates the reference's `make blas` path (all weights widened bf16->f32,
+ * linears through cblas_sgemm, per-head sgemm/softmax/sgemm attention) with the
+ * same operation order. Each function cites the reference file:line it follows.
+ * sgemm is OpenBLAS when orc_set_blas() bound one, else a plain loop nest.
+ */
+#ifndef IRIS_ORACLE_H
+#define IRIS_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+typedef struct orc_flux orc_flux_t;
+typedef struct orc_zi orc_zi_t;
+
+typedef struct {
+    const float *latent;
+    int h, w;
+    int t_offset;
+} orc_ref_t;
+
+/* BLAS binding: path of a shared library exporting <prefix>cblas_sgemm. */
+int orc_set_blas(const char *so_path, const char *prefix, int threads);
+const char *orc_blas_info(void);
+
+/* fast_expf of iris_kernels.h:21-35 */
+float orc_fast_expf(float x);
+
+/* --- Flux.2-Klein --- */
+orc_flux_t *orc_flux_load(const char *model_dir);
+orc_flux_t *orc_flux_create_synth(int hidden, int heads, int n_double, int n_single,
+                                  int text_dim, int latent_ch, float mlp_ratio,
+                                  float rope_theta, uint64_t seed);
+void orc_flux_free(orc_flux_t *m);
+int orc_flux_dims(const orc_flux_t *m, int *out8);
+
+float *orc_flux_forward(orc_flux_t *m, const float *latent, int h, int w,
+                        const float *txt, int txt_seq, float t);
+float *orc_flux_forward_refs(orc_flux_t *m, const float *latent, int h, int w,
+                             const orc_ref_t *refs, int n_refs,
+                             const float *txt, int txt_seq, float t);
+void orc_free(void *p);
+
+/* Pieces, for block- and table-level parity. */
+void orc_rope_img(float *cos_out, float *sin_out, int ph, int pw, int axis_dim,
+                  float theta, int t_offset);
+void orc_rope_txt(float *cos_out, float *sin_out, int txt_seq, int axis_dim, float theta);
+void orc_timestep_sincos(float *out, float t, int dim, float max_period);
+void orc_flux_time_embed(orc_flux_t *m, float t, float *t_emb);
+/* mod outputs: dimg[6h], dtxt[6h], single[3h], final[2h] (any may be NULL) */
+void orc_flux_modulation(orc_flux_t *m, const float *t_emb, float *dimg, float *dtxt,
+                         float *single, float *final_mod);
+void orc_flux_double_block(orc_flux_t *m, int idx, float *img, float *txt,
+                           const float *img_mod, const float *txt_mod,
+                           const float *img_cos, const float *img_sin,
+                           const float *txt_cos, const float *txt_sin,
+                           int img_seq, int txt_seq);
+void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
+                           const float *img_cos, const float *img_sin,
+                           const float *txt_cos, const float *txt_sin,
+                           int seq, int img_offset);
+
+/* --- Z-Image S3-DiT --- */
+orc_zi_t *orc_zi_load(const char *model_dir, int dim, int heads, int layers, int refiners,
+                      int cap_dim, int in_ch, int ps, float theta, const int *axes);
+orc_zi_t *orc_zi_create_synth(int dim, int heads, int layers, int refiners, int cap_dim,
+                              int in_ch, int ps, float theta, const int *axes, int ffn_dim,
+                              int t_mid, uint64_t seed);
+void orc_zi_free(orc_zi_t *m);
+/* 1: reproduce the reference CPU path's in-place attention output projection. */
+void orc_zi_set_reference_aliasing(int on);
+float *orc_zi_forward(orc_zi_t *m, const float *latent, int lh, int lw, float t,
+                      const float *cap, int cap_len);
+void orc_zi_rope_tables(orc_zi_t *m, float *cos_out, float *sin_out, int axis);
+void orc_zi_patchify(float *out, const float *latent, int in_ch, int H, int W, int ps);
+void orc_zi_t_embed(orc_zi_t *m, float t, float *out);
+void orc_zi_block(orc_zi_t *m, int kind, int idx, float *x, const int *pos, const int *mask,
+                  const float *t_emb, int seq);
+
+/* --- sampler pieces --- */
+float *orc_official_schedule(int n, int image_seq_len);
+float *orc_zimage_schedule(int n, float shift);
+float *orc_init_noise(int batch, int ch, int h, int w, int64_t seed);
+
+#endif

@@ -1,0 +1,258 @@
+"""Shared helpers for the tests: library loading, synthetic model writers, metrics.
+
+The synthetic models are random-init bf16 safetensors directories in the
+reference's on-disk layout (tensor names of iris_transformer_flux.c:5349-5497 and
+iris_transformer_zimage.c:2024-2395). Values come from the seeded generator of
+include/iris_synth.h, so the reference build, the oracle and the HIP library all
+see identical weights.
+"""
+import ctypes
+import hashlib
+import json
+import os
+import struct
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libiris_ref.so")
+HIP_SO = os.path.join(ROOT, "iris.c_amd", "libiris_hip.so")
+
+FP = ctypes.POINTER(ctypes.c_float)
+IP = ctypes.POINTER(ctypes.c_int)
+U16P = ctypes.POINTER(ctypes.c_uint16)
+
+_libs = {}
+
+
+def oracle():
+    """The CPU checker (test infrastructure)."""
+    if "oracle" not in _libs:
+        lib = ctypes.CDLL(ORACLE_SO)
+        lib.orc_flux_load.restype = ctypes.c_void_p
+        lib.orc_flux_create_synth.restype = ctypes.c_void_p
+        lib.orc_flux_create_synth.argtypes = [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_float, ctypes.c_uint64]
+        lib.orc_flux_forward.restype = ctypes.c_void_p
+        lib.orc_flux_forward_refs.restype = ctypes.c_void_p
+        lib.orc_zi_load.restype = ctypes.c_void_p
+        lib.orc_zi_create_synth.restype = ctypes.c_void_p
+        lib.orc_zi_forward.restype = ctypes.c_void_p
+        lib.orc_official_schedule.restype = ctypes.c_void_p
+        lib.orc_zimage_schedule.restype = ctypes.c_void_p
+        lib.orc_init_noise.restype = ctypes.c_void_p
+        lib.orc_blas_info.restype = ctypes.c_char_p
+        lib.iris_synth_seed.restype = ctypes.c_uint64
+        lib.iris_synth_seed.argtypes = [ctypes.c_uint64, ctypes.c_char_p]
+        lib.iris_synth_fill_bf16.argtypes = [U16P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
+                                             ctypes.c_float, ctypes.c_float]
+        lib.iris_synth_fill_f32.argtypes = [FP, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
+                                            ctypes.c_float, ctypes.c_float]
+        _libs["oracle"] = lib
+        bind_blas(lib)
+    return _libs["oracle"]
+
+
+def find_openblas():
+    """The OpenBLAS bundled with scipy (same image on every machine)."""
+    try:
+        import scipy
+        d = os.path.join(os.path.dirname(os.path.dirname(scipy.__file__)), "scipy.libs")
+        for f in sorted(os.listdir(d)):
+            if f.startswith("libscipy_openblas") and f.endswith(".so"):
+                return os.path.join(d, f), "scipy_"
+    except Exception:
+        pass
+    return None, None
+
+
+def bind_blas(lib, threads=None):
+    path, prefix = find_openblas()
+    if path:
+        n = threads or int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+        lib.orc_set_blas(path.encode(), prefix.encode(), n)
+
+
+def ref():
+    """The reference build (only where the reference tree exists)."""
+    if "ref" not in _libs:
+        lib = ctypes.CDLL(REF_SO)
+        lib.iris_transformer_load_safetensors.restype = ctypes.c_void_p
+        lib.iris_transformer_forward.restype = ctypes.c_void_p
+        lib.iris_transformer_forward_with_multi_refs.restype = ctypes.c_void_p
+        lib.zi_transformer_load_safetensors.restype = ctypes.c_void_p
+        lib.zi_transformer_forward.restype = ctypes.c_void_p
+        lib.iris_official_schedule.restype = ctypes.c_void_p
+        lib.iris_zimage_schedule.restype = ctypes.c_void_p
+        lib.iris_init_noise.restype = ctypes.c_void_p
+        lib.iris_sample_euler.restype = ctypes.c_void_p
+        _libs["ref"] = lib
+    return _libs["ref"]
+
+
+def fptr(a):
+    return a.ctypes.data_as(FP)
+
+
+def take_f32(lib, ptr, n):
+    """Copies a malloc'd float array returned by a C library and frees it."""
+    out = np.ctypeslib.as_array(ctypes.cast(ptr, FP), shape=(n,)).copy()
+    lib_free = getattr(lib, "orc_free", None)
+    if lib_free is not None:
+        lib_free(ctypes.c_void_p(ptr))
+    else:
+        ctypes.CDLL(None).free(ctypes.c_void_p(ptr))
+    return out
+
+
+def synth_f32(shape, seed, mean=0.0, std=1.0):
+    n = int(np.prod(shape))
+    a = np.empty(n, np.float32)
+    oracle().iris_synth_fill_f32(fptr(a), n, seed, 0, mean, std)
+    return a.reshape(shape)
+
+
+def synth_bf16(name, shape, model_seed, mean=0.0, std=0.02):
+    lib = oracle()
+    n = int(np.prod(shape))
+    a = np.empty(n, np.uint16)
+    lib.iris_synth_fill_bf16(a.ctypes.data_as(U16P), n, lib.iris_synth_seed(model_seed, name.encode()), 0,
+                             mean, std)
+    return a.reshape(shape)
+
+
+def bf16_to_f32(a):
+    return (a.astype(np.uint32) << 16).view(np.float32)
+
+
+def write_safetensors(path, tensors):
+    """tensors: list of (name, uint16 array) written as BF16."""
+    header, off, blobs = {}, 0, []
+    for name, arr in tensors:
+        b = np.ascontiguousarray(arr).tobytes()
+        header[name] = {"dtype": "BF16", "shape": list(arr.shape), "data_offsets": [off, off + len(b)]}
+        off += len(b)
+        blobs.append(b)
+    h = json.dumps(header).encode()
+    h += b" " * ((8 - len(h) % 8) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def flux_tensor_list(cfg):
+    """(name, shape, is_norm) of a Flux.2-Klein transformer, reference naming."""
+    h = cfg["heads"] * 128
+    mlp = int(h * cfg.get("mlp_ratio", 3.0))
+    C, td = cfg.get("latent_ch", 128), cfg["text_dim"]
+    t = [("x_embedder.weight", (h, C), 0), ("context_embedder.weight", (h, td), 0),
+         ("time_guidance_embed.timestep_embedder.linear_1.weight", (h, 256), 0),
+         ("time_guidance_embed.timestep_embedder.linear_2.weight", (h, h), 0),
+         ("double_stream_modulation_img.linear.weight", (6 * h, h), 0),
+         ("double_stream_modulation_txt.linear.weight", (6 * h, h), 0),
+         ("single_stream_modulation.linear.weight", (3 * h, h), 0)]
+    for i in range(cfg["n_double"]):
+        p = f"transformer_blocks.{i}."
+        t += [(p + "attn.norm_q.weight", (128,), 1), (p + "attn.norm_k.weight", (128,), 1),
+              (p + "attn.to_q.weight", (h, h), 0), (p + "attn.to_k.weight", (h, h), 0),
+              (p + "attn.to_v.weight", (h, h), 0), (p + "attn.to_out.0.weight", (h, h), 0),
+              (p + "ff.linear_in.weight", (2 * mlp, h), 0), (p + "ff.linear_out.weight", (h, mlp), 0),
+              (p + "attn.norm_added_q.weight", (128,), 1), (p + "attn.norm_added_k.weight", (128,), 1),
+              (p + "attn.add_q_proj.weight", (h, h), 0), (p + "attn.add_k_proj.weight", (h, h), 0),
+              (p + "attn.add_v_proj.weight", (h, h), 0), (p + "attn.to_add_out.weight", (h, h), 0),
+              (p + "ff_context.linear_in.weight", (2 * mlp, h), 0),
+              (p + "ff_context.linear_out.weight", (h, mlp), 0)]
+    for i in range(cfg["n_single"]):
+        p = f"single_transformer_blocks.{i}."
+        t += [(p + "attn.norm_q.weight", (128,), 1), (p + "attn.norm_k.weight", (128,), 1),
+              (p + "attn.to_qkv_mlp_proj.weight", (3 * h + 2 * mlp, h), 0),
+              (p + "attn.to_out.weight", (h, h + mlp), 0)]
+    t += [("norm_out.linear.weight", (2 * h, h), 0), ("proj_out.weight", (C, h), 0)]
+    return t
+
+
+def write_flux_model(d, cfg, seed):
+    os.makedirs(os.path.join(d, "transformer"), exist_ok=True)
+    conf = {"num_attention_heads": cfg["heads"], "attention_head_dim": 128,
+            "num_layers": cfg["n_double"], "num_single_layers": cfg["n_single"],
+            "joint_attention_dim": cfg["text_dim"], "in_channels": cfg.get("latent_ch", 128),
+            "mlp_ratio": cfg.get("mlp_ratio", 3.0), "rope_theta": cfg.get("theta", 2000.0)}
+    with open(os.path.join(d, "transformer", "config.json"), "w") as f:
+        json.dump(conf, f)
+    tensors = [(n, synth_bf16(n, s, seed, 1.0 if norm else 0.0, 0.02))
+               for n, s, norm in flux_tensor_list(cfg)]
+    write_safetensors(os.path.join(d, "transformer", "diffusion_pytorch_model.safetensors"), tensors)
+
+
+def zimage_tensor_list(cfg):
+    """(name, shape, mean, std) of a Z-Image transformer, reference naming."""
+    d, hd, ps, C = cfg["dim"], 128, cfg.get("ps", 2), cfg.get("in_ch", 16)
+    ffn, tmid, cap = cfg["ffn"], cfg["t_mid"], cfg["cap_dim"]
+    ad = min(d, 256)
+    pf = ps * ps * C
+    t = [("t_embedder.mlp.0.weight", (tmid, 256), 0.0, 0.02), ("t_embedder.mlp.0.bias", (tmid,), 0.0, 0.02),
+         ("t_embedder.mlp.2.weight", (ad, tmid), 0.0, 0.02), ("t_embedder.mlp.2.bias", (ad,), 0.0, 0.02),
+         ("cap_embedder.0.weight", (cap,), 1.0, 0.02), ("cap_embedder.1.weight", (d, cap), 0.0, 0.02),
+         ("cap_embedder.1.bias", (d,), 0.0, 0.02),
+         (f"all_x_embedder.{ps}-1.weight", (d, pf), 0.0, 0.02), (f"all_x_embedder.{ps}-1.bias", (d,), 0.0, 0.02),
+         ("x_pad_token", (d,), 0.0, 1.0), ("cap_pad_token", (d,), 0.0, 1.0)]
+
+    def block(pre, mod):
+        b = [(pre + ".attention.to_q.weight", (d, d), 0.0, 0.02), (pre + ".attention.to_k.weight", (d, d), 0.0, 0.02),
+             (pre + ".attention.to_v.weight", (d, d), 0.0, 0.02),
+             (pre + ".attention.to_out.0.weight", (d, d), 0.0, 0.02),
+             (pre + ".attention.norm_q.weight", (hd,), 1.0, 0.02), (pre + ".attention.norm_k.weight", (hd,), 1.0, 0.02),
+             (pre + ".attention_norm1.weight", (d,), 1.0, 0.02), (pre + ".attention_norm2.weight", (d,), 1.0, 0.02),
+             (pre + ".feed_forward.w1.weight", (ffn, d), 0.0, 0.02),
+             (pre + ".feed_forward.w2.weight", (d, ffn), 0.0, 0.02),
+             (pre + ".feed_forward.w3.weight", (ffn, d), 0.0, 0.02),
+             (pre + ".ffn_norm1.weight", (d,), 1.0, 0.02), (pre + ".ffn_norm2.weight", (d,), 1.0, 0.02)]
+        if mod:
+            b += [(pre + ".adaLN_modulation.0.weight", (4 * d, ad), 0.0, 0.02),
+                  (pre + ".adaLN_modulation.0.bias", (4 * d,), 0.0, 0.02)]
+        return b
+    for i in range(cfg["refiners"]):
+        t += block(f"noise_refiner.{i}", True)
+        t += block(f"context_refiner.{i}", False)
+    for i in range(cfg["layers"]):
+        t += block(f"layers.{i}", True)
+    t += [(f"all_final_layer.{ps}-1.adaLN_modulation.1.weight", (d, ad), 0.0, 0.02),
+          (f"all_final_layer.{ps}-1.adaLN_modulation.1.bias", (d,), 0.0, 0.02),
+          (f"all_final_layer.{ps}-1.linear.weight", (pf, d), 0.0, 0.02),
+          (f"all_final_layer.{ps}-1.linear.bias", (pf,), 0.0, 0.02)]
+    return t
+
+
+def write_zimage_model(d, cfg, seed):
+    os.makedirs(os.path.join(d, "transformer"), exist_ok=True)
+    tensors = [(n, synth_bf16(n, s, seed, m, sd)) for n, s, m, sd in zimage_tensor_list(cfg)]
+    write_safetensors(os.path.join(d, "transformer", "diffusion_pytorch_model.safetensors"), tensors)
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def cosine(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    return float(a @ b / max(np.linalg.norm(a) * np.linalg.norm(b), 1e-30))
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def fingerprint(x, stride=97):
+    """Compact golden of a large array: strided subsample plus moments."""
+    x = np.asarray(x, np.float32).ravel()
+    return {"sub": x[::stride].copy(), "sum": np.float64(x.astype(np.float64).sum()),
+            "sumsq": np.float64((x.astype(np.float64) ** 2).sum())}
