@@ -1,0 +1,151 @@
+/*
+ * iris_hip.h - C ABI of the MI355X (gfx950) HIP layer.
+ *
+ * Plain pointers and sizes only; every pointer named d_* is device memory
+ * returned by iris_hip_malloc (or any hipMalloc'd pointer of this process).
+ * All launches are asynchronous on the library's one stream; iris_hip_sync()
+ * waits. Functions return 0 on success and a negative value on error, with a
+ * message in iris_hip_last_error(), which mirrors the reference's "0 means
+ * the caller falls back" convention (iris_metal.h:23-60) without a fallback:
+ * the host code reports the error and returns NULL.
+ *
+ * This layer takes the place the Metal runtime has in the reference
+ * (iris_metal.h: device init :23-40, weight cache keyed by host pointer
+ * :710-730, batch/command buffers :315-320, GPU tensors :158-223, kernels of
+ * iris_shaders.metal). Coarse per-step entry points live in
+ * iris_transformer.h; the kernel-level exports below serve the host code and
+ * the parity tests.
+ */
+#ifndef IRIS_HIP_H
+#define IRIS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- device, memory, stream (cf. iris_metal_init / iris_metal_available) ---- */
+int iris_hip_init(int device);
+int iris_hip_available(void);
+const char *iris_hip_last_error(void);
+const char *iris_hip_device_name(void);
+void *iris_hip_malloc(size_t bytes);                 /* NULL on failure */
+void iris_hip_free(void *d_ptr);
+int iris_hip_memcpy_h2d(void *d_dst, const void *src, size_t bytes);   /* on the stream */
+int iris_hip_memcpy_d2h(void *dst, const void *d_src, size_t bytes);   /* synchronous */
+int iris_hip_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes); /* on the stream */
+int iris_hip_memset(void *d_dst, int value, size_t bytes);             /* not for captured work */
+int iris_hip_sync(void);
+size_t iris_hip_mem_in_use(void);
+
+/* ---- timing: events recorded on the library stream ---- */
+int iris_hip_event_record(int slot);                 /* slot 0..63 */
+float iris_hip_event_elapsed_ms(int slot_start, int slot_end);
+
+/* ---- graph capture of the library stream (cf. iris_gpu_batch_begin/end) ---- */
+int iris_hip_graph_begin(void);
+void *iris_hip_graph_end(void);                      /* instantiated graph, NULL on error */
+int iris_hip_graph_launch(void *graph);
+void iris_hip_graph_destroy(void *graph);
+
+/* ---- bf16 MFMA GEMM: out = A[M,K] . W[N,K]^T with a fused epilogue ---- */
+enum {
+    IRIS_EPI_F32 = 0,        /* out f32[M,ldo] = acc (+ vec[n] bias)                 */
+    IRIS_EPI_BF16 = 1,       /* out bf16[M,ldo] = acc (+ vec[n] bias)                */
+    IRIS_EPI_GATED_ADD = 2,  /* out f32[M,ldo] += vec[n] * acc  (vec NULL: += acc)   */
+    IRIS_EPI_SWIGLU = 3,     /* W rows interleaved in 64-row gate/up groups:
+                                out bf16[M,ldo] col j = silu(gate_j) * up_j         */
+    IRIS_EPI_F32_T = 4       /* out f32[n*ldo + m] = acc (+ vec[n] bias): transposed */
+};
+
+typedef struct {
+    const uint16_t *A;   /* bf16 [M][lda]                           */
+    const uint16_t *W;   /* bf16 [N][ldw] (row n = output feature)  */
+    void *out;
+    const float *vec;    /* bias / gate per output column, or NULL  */
+    int M, N, K;         /* K % 64 == 0                             */
+    int lda, ldw, ldo;
+    int epi;
+} iris_gemm_problem_t;
+
+/* Up to 4 independent problems in one launch (e.g. the txt and img streams). */
+int iris_hip_gemm(const iris_gemm_problem_t *problems, int n_problems);
+
+/* y[n] = act_out( sum_k W[n][k] * act_in(x[k]) + bias[n] ), W bf16 [N][K], x f32.
+ * act_in: 0 none, 1 SiLU (expf). Used for the timestep MLP and modulation. */
+int iris_hip_gemv(float *d_y, const uint16_t *d_W, const float *d_x, const float *d_bias,
+                  int N, int K, int act_in);
+
+/* ---- row normalisations (one row of `cols` per block) ---- */
+enum {
+    IRIS_NORM_LN_MOD = 0,    /* LayerNorm (no affine) then (1 + scale) * n + shift     */
+    IRIS_NORM_LN_SCALE = 1,  /* LayerNorm (no affine) then n * scale                   */
+    IRIS_NORM_RMS = 2,       /* x * rsqrt(mean(x^2) + eps) * w, then * scale if given  */
+};
+typedef struct {
+    const float *x; int ldx;          /* f32 input rows */
+    void *out; int ldo; int out_bf16; /* output rows    */
+    int rows, cols, mode;
+    float eps;
+    int split;                        /* (row % period) < split: set A, else set B */
+    int period;                       /* 0: no period (row itself)                 */
+    const float *shiftA, *scaleA, *wA;
+    const float *shiftB, *scaleB, *wB;
+} iris_norm_args_t;
+int iris_hip_rownorm(const iris_norm_args_t *a);
+
+/* Z-Image gated residual: x[r,:] += gate[:] * RMSNorm(y[r,:]) * w[:]  (gate NULL: 1). */
+int iris_hip_rms_gated_add(float *d_x, const float *d_y, const float *d_w, const float *d_gate,
+                           int rows, int cols, float eps);
+
+/* ---- attention pieces ---- */
+/* Per (row, head) RMSNorm of Q and K (x w_q / w_k, rows < split use set A) and
+ * rotary embedding from per-row cos/sin tables [rows][128] (pairs 2i, 2i+1).
+ * qkv: bf16 rows holding Q at column 0, K at col_k, V at col_v (ld_qkv).
+ * Writes Q', K' as bf16 [rows][heads*128] and V transposed to
+ * vt[head][d][ld_vt] (columns rows..ld_vt-1 zero-filled). */
+typedef struct {
+    const uint16_t *qkv; int ld_qkv, col_k, col_v;
+    uint16_t *q_out, *k_out, *vt_out; int ld_vt;
+    int rows, heads;
+    const float *wqA, *wkA, *wqB, *wkB; int split;
+    const float *cos_t, *sin_t;       /* [rows][128]; NULL = no rotation */
+    int period;                       /* 0: none; else split and table row use row % period */
+    float eps;
+} iris_qkprep_args_t;
+int iris_hip_qk_prepare(const iris_qkprep_args_t *a);
+
+/* Flash attention over head_dim 128: O = softmax(Q K^T * scale) V per head.
+ * Q [sq][ld_q], K [sk][ld_k] (head h at column h*128), Vt [h][128][ld_vt],
+ * O [sq][ld_o]. Keys outside [kv_lo0, kv_hi0) U [kv_lo1, kv_hi1) are masked
+ * (pass 0, sk, 0, 0 for none). batch / *_bstride run independent sequences. */
+typedef struct {
+    const uint16_t *q; const uint16_t *k; const uint16_t *vt; uint16_t *o;
+    int ld_q, ld_k, ld_vt, ld_o;
+    int sq, sk, heads, batch;
+    long long q_bstride, k_bstride, vt_bstride, o_bstride;
+    float scale;
+    int kv_lo0, kv_hi0, kv_lo1, kv_hi1;
+} iris_attn_args_t;
+int iris_hip_attention(const iris_attn_args_t *a);
+
+/* ---- layout and conversion ---- */
+/* NCHW f32 latent [C][hw] -> token rows bf16 out[row0 + p][C] (ld = C) */
+int iris_hip_nchw_to_tokens(uint16_t *d_out, const float *d_latent, int C, int hw);
+int iris_hip_f32_to_bf16(uint16_t *d_out, const float *d_in, size_t n);
+int iris_hip_bf16_to_f32(float *d_out, const uint16_t *d_in, size_t n);
+/* z += dt * v  (sign -1: z += dt * (-v)); with v2: v = v + g * (v2 - v) first (CFG) */
+int iris_hip_euler(float *d_z, const float *d_v, const float *d_v2, float g, float dt, float sign,
+                   size_t n);
+/* Z-Image (ph, pw, c) patchify of [C][H][W] f32 -> bf16 rows [n_patch][ps*ps*C], and back */
+int iris_hip_patchify(uint16_t *d_out, const float *d_latent, int C, int H, int W, int ps);
+int iris_hip_unpatchify(float *d_latent, const float *d_patches, int C, int H, int W, int ps);
+/* copy one f32 row vector into rows [r0, r1) of a [*, cols] matrix */
+int iris_hip_fill_rows(float *d_x, const float *d_row, int r0, int r1, int cols);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

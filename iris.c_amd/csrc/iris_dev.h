@@ -1,0 +1,58 @@
+/*
+ * iris_dev.h - device-side helpers shared by the gfx950 kernels.
+ *
+ * Storage type for bf16 is uint16_t everywhere; MFMA operands are reinterpreted
+ * as __bf16 vectors. Wave size is 64 (CDNA).
+ */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define IRIS_WAVE 64
+
+__device__ __forceinline__ float bf2f(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+/* round-to-nearest-even f32 -> bf16 (NaN stays NaN) */
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+/* Sum over a block of `nwaves` waves; `red` is LDS scratch of >= nwaves floats.
+ * Every thread returns the total. */
+template <int NWAVES>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    int w = threadIdx.x / IRIS_WAVE, l = threadIdx.x % IRIS_WAVE;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NWAVES; i++) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }

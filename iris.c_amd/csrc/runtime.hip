@@ -1,0 +1,162 @@
+/*
+ * runtime.hip - device, memory, stream, events and graph capture of the HIP
+ * layer (role of iris_metal.m's runtime: init, buffer management, command
+ * buffers). One stream per process; not reentrant, like the reference
+ * (single caller thread, global state).
+ */
+#include "iris_internal.h"
+
+#include <atomic>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+static int g_init = 0;
+static int g_device = -1;
+static hipStream_t g_stream = nullptr;
+static char g_err[512] = "";
+static char g_name[256] = "";
+static std::atomic<size_t> g_in_use{0};
+static hipEvent_t g_events[64];
+static int g_events_made = 0;
+static hipGraph_t g_capture_graph = nullptr;
+
+hipStream_t iris_stream(void) { return g_stream; }
+
+int iris_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "iris_hip: %s\n", g_err);
+    return -1;
+}
+
+int iris_check(hipError_t e, const char *what) {
+    if (e == hipSuccess) return 0;
+    return iris_set_error("%s: %s", what, hipGetErrorString(e));
+}
+
+int iris_launch_check(const char *what) {
+    return iris_check(hipGetLastError(), what);
+}
+
+extern "C" {
+
+int iris_hip_init(int device) {
+    if (g_init) return device < 0 || device == g_device ? 0 : iris_set_error("already bound to device %d", g_device);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return iris_set_error("no HIP device");
+    if (device < 0) device = 0;
+    if (device >= n) return iris_set_error("device %d of %d", device, n);
+    if (iris_check(hipSetDevice(device), "hipSetDevice")) return -1;
+    hipDeviceProp_t p;
+    if (iris_check(hipGetDeviceProperties(&p, device), "hipGetDeviceProperties")) return -1;
+    snprintf(g_name, sizeof(g_name), "%s (%s, %d CUs)", p.name, p.gcnArchName, p.multiProcessorCount);
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return iris_set_error("kernels are built for gfx950, device is %s", p.gcnArchName);
+    if (iris_check(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate")) return -1;
+    g_device = device;
+    g_init = 1;
+    return 0;
+}
+
+int iris_hip_available(void) {
+    if (g_init) return 1;
+    return iris_hip_init(0) == 0;
+}
+
+const char *iris_hip_last_error(void) { return g_err; }
+const char *iris_hip_device_name(void) { return g_name; }
+
+void *iris_hip_malloc(size_t bytes) {
+    if (!iris_hip_available()) return nullptr;
+    void *p = nullptr;
+    size_t b = bytes ? bytes : 256;
+    if (hipMalloc(&p, b) != hipSuccess) {
+        iris_set_error("hipMalloc(%zu) failed", b);
+        return nullptr;
+    }
+    g_in_use += b;
+    return p;
+}
+
+void iris_hip_free(void *p) {
+    if (!p) return;
+    size_t sz = 0;
+    if (hipMemPtrGetInfo(p, &sz) != hipSuccess) sz = 0;
+    g_in_use -= sz;
+    (void)hipFree(p);
+}
+
+size_t iris_hip_mem_in_use(void) { return g_in_use; }
+
+int iris_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return 0;
+    return iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream), "memcpy h2d");
+}
+
+int iris_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return 0;
+    if (iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream), "memcpy d2h")) return -1;
+    return iris_check(hipStreamSynchronize(g_stream), "sync after d2h");
+}
+
+int iris_hip_memcpy_d2d(void *dst, const void *src, size_t bytes) {
+    if (!bytes) return 0;
+    return iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream), "memcpy d2d");
+}
+
+int iris_hip_memset(void *dst, int v, size_t bytes) {
+    if (!bytes) return 0;
+    return iris_check(hipMemsetAsync(dst, v, bytes, g_stream), "memset");
+}
+
+int iris_hip_sync(void) {
+    if (!g_init) return 0;
+    return iris_check(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+}
+
+int iris_hip_event_record(int slot) {
+    if (slot < 0 || slot >= 64) return iris_set_error("event slot %d", slot);
+    if (!g_events_made) {
+        for (int i = 0; i < 64; i++)
+            if (iris_check(hipEventCreate(&g_events[i]), "hipEventCreate")) return -1;
+        g_events_made = 1;
+    }
+    return iris_check(hipEventRecord(g_events[slot], g_stream), "hipEventRecord");
+}
+
+float iris_hip_event_elapsed_ms(int a, int b) {
+    float ms = -1.0f;
+    if (!g_events_made || a < 0 || b < 0 || a >= 64 || b >= 64) return -1.0f;
+    if (hipEventSynchronize(g_events[b]) != hipSuccess) return -1.0f;
+    if (hipEventElapsedTime(&ms, g_events[a], g_events[b]) != hipSuccess) return -1.0f;
+    return ms;
+}
+
+int iris_hip_graph_begin(void) {
+    if (!iris_hip_available()) return -1;
+    return iris_check(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "begin capture");
+}
+
+void *iris_hip_graph_end(void) {
+    hipGraph_t g = nullptr;
+    if (iris_check(hipStreamEndCapture(g_stream, &g), "end capture")) return nullptr;
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (iris_check(e, "hipGraphInstantiate")) return nullptr;
+    (void)g_capture_graph;
+    return (void *)ex;
+}
+
+int iris_hip_graph_launch(void *graph) {
+    return iris_check(hipGraphLaunch((hipGraphExec_t)graph, g_stream), "hipGraphLaunch");
+}
+
+void iris_hip_graph_destroy(void *graph) {
+    if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
+}  /* extern "C" */

@@ -1,0 +1,770 @@
+/*
+ * iris_flux.c - Flux.2-Klein denoiser forward of the HIP build (host C).
+ *
+ * Keeps the reference's entry points (iris_transformer_forward*, loaders,
+ * free) and the block structure of iris_transformer_flux.c, but runs every
+ * block on the device through the C ABI of iris_hip.h:
+ *   - weights are uploaded once as bf16 (no per-step bf16->f32 widening,
+ *     unlike the BLAS mmap path :4073-4077);
+ *   - the residual stream stays f32 in HBM in [txt rows | img rows] order, so
+ *     the double blocks' joint attention over cat([txt, img]) (:1899-1905) and
+ *     the single blocks' concatenation (:4110-4114) need no copies;
+ *   - one forward is captured once per geometry into a hipGraph and replayed
+ *     (the reference's Metal path encodes one command buffer per step,
+ *     :3565-3691).
+ * Block functions keep the reference's names and roles:
+ * double_block_forward (:2366-2614), single_block_forward (:3761-3928).
+ */
+#include "../../include/iris_transformer.h"
+#include "../../include/iris_hip.h"
+#include "../../include/iris_synth.h"
+#include "iris_st.h"
+#include "iris_tables.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define MAX_REFS 8
+
+typedef struct {
+    uint16_t *img_qkv, *img_o, *img_ffin, *img_down;    /* ffin rows gate/up interleaved by 64 */
+    uint16_t *txt_qkv, *txt_o, *txt_ffin, *txt_down;
+    float *img_nq, *img_nk, *txt_nq, *txt_nk;
+} dev_double_t;
+
+typedef struct {
+    uint16_t *qkv_mlp;   /* [3h + 2mlp][h]: Q,K,V rows, then gate/up interleaved by 64 */
+    uint16_t *out;       /* [h][h + mlp] */
+    float *nq, *nk;
+} dev_single_t;
+
+typedef struct {
+    int valid;
+    int ih, iw, n_refs, T, B;
+    int ref_h[MAX_REFS], ref_w[MAX_REFS], ref_t[MAX_REFS];
+    int I0, I, S, S_pad;
+    size_t cap_S;            /* rows the buffers were sized for */
+    /* device buffers */
+    float *x;                /* [B][S][h] residual stream */
+    uint16_t *a;             /* [B][S][h] normalised activations */
+    uint16_t *qkv;           /* [B][S][3h] */
+    uint16_t *q, *k;         /* [B][S][h] */
+    uint16_t *vt;            /* [B][heads][128][S_pad] */
+    uint16_t *cat;           /* [B][S][h + mlp]: attention | SwiGLU output */
+    uint16_t *tok;           /* [I][C] */
+    uint16_t *txtb;          /* [B][T][text_dim] */
+    float *txtf;             /* [B][T][text_dim] */
+    float *lat;              /* [C][I] target then refs, NCHW per image */
+    float *vel;              /* [B][C][I0] */
+    float *rope_cos, *rope_sin;   /* [S][128] */
+    float *tsin;             /* [256] */
+    float *tmp, *temb;       /* [h] */
+    float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
+    float *tsin_host;        /* pinned */
+    void *graph;
+} work_t;
+
+struct iris_transformer {
+    int hidden, heads, head_dim, mlp, n_double, n_single, text_dim, latent_ch, axis_dim;
+    float theta;
+    uint16_t *img_in, *txt_in, *t_fc1, *t_fc2, *mod_dimg, *mod_dtxt, *mod_single, *final_mod, *proj_out;
+    dev_double_t *dbl;
+    dev_single_t *sgl;
+    work_t w;
+};
+
+/* ------------------------------------------------------------------ config */
+
+/* parse_transformer_config, iris_transformer_flux.c:395-455 */
+static int parse_config(const char *dir, iris_transformer_t *tf) {
+    char path[2048];
+    snprintf(path, sizeof(path), "%s/transformer/config.json", dir);
+    FILE *f = fopen(path, "r");
+    if (!f) return -1;
+    char buf[4096];
+    size_t n = fread(buf, 1, sizeof(buf) - 1, f);
+    buf[n] = 0;
+    fclose(f);
+    int heads = 0, hd = 0, nl = 0, ns = 0, jd = 0, ic = 0;
+    float ratio = 0, theta = 0;
+    char *p;
+#define GETI(key, var) if ((p = strstr(buf, "\"" key "\"")) && (p = strchr(p, ':'))) var = atoi(p + 1)
+#define GETF(key, var) if ((p = strstr(buf, "\"" key "\"")) && (p = strchr(p, ':'))) var = (float)atof(p + 1)
+    GETI("num_attention_heads", heads);
+    GETI("attention_head_dim", hd);
+    GETI("num_layers", nl);
+    GETI("num_single_layers", ns);
+    GETI("joint_attention_dim", jd);
+    GETI("in_channels", ic);
+    GETF("mlp_ratio", ratio);
+    GETF("rope_theta", theta);
+#undef GETI
+#undef GETF
+    if (heads <= 0 || hd <= 0) return -1;
+    tf->heads = heads;
+    tf->head_dim = hd;
+    tf->hidden = heads * hd;
+    tf->mlp = (int)(tf->hidden * (ratio > 0 ? ratio : 3.0f));
+    tf->n_double = nl > 0 ? nl : 5;
+    tf->n_single = ns > 0 ? ns : 20;
+    tf->text_dim = jd > 0 ? jd : 7680;
+    tf->latent_ch = ic > 0 ? ic : 128;
+    tf->theta = theta > 0 ? theta : 2000.0f;
+    tf->axis_dim = hd / 4;
+    return 0;
+}
+
+static void defaults_4b(iris_transformer_t *tf) {   /* :5309-5321 */
+    tf->hidden = 3072; tf->heads = 24; tf->head_dim = 128; tf->mlp = 9216;
+    tf->n_double = 5; tf->n_single = 20; tf->text_dim = 7680; tf->latent_ch = 128;
+    tf->theta = 2000.0f; tf->axis_dim = 32;
+}
+
+static int check_dims(const iris_transformer_t *tf) {
+    if (tf->head_dim != 128) { fprintf(stderr, "iris_hip: head_dim %d unsupported (128)\n", tf->head_dim); return -1; }
+    if (tf->hidden % 64 || tf->mlp % 64 || tf->text_dim % 64 || tf->latent_ch % 64) {
+        fprintf(stderr, "iris_hip: hidden/mlp/text_dim/latent_ch must be multiples of 64\n");
+        return -1;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------ weight upload */
+
+/* A source fills a host bf16 buffer for a named tensor of n elements. */
+typedef struct {
+    const iris_st_set_t *st;      /* safetensors, or NULL for synthetic */
+    uint64_t seed;
+    uint16_t *stage;
+    size_t stage_n;
+} source_t;
+
+static const uint16_t *src_get(source_t *s, const char *name, size_t n, int is_norm) {
+    if (s->stage_n < n) {
+        free(s->stage);
+        s->stage = (uint16_t *)malloc(n * sizeof(uint16_t));
+        s->stage_n = s->stage ? n : 0;
+        if (!s->stage) return NULL;
+    }
+    if (s->st) {
+        const iris_st_file_t *f;
+        const iris_st_tensor_t *t = iris_st_set_find(s->st, name, &f);
+        if (!t) { fprintf(stderr, "Error: required tensor %s not found\n", name); return NULL; }
+        if ((size_t)iris_st_numel(t) != n) {
+            fprintf(stderr, "Error: tensor %s has %lld elements, expected %zu\n", name,
+                    (long long)iris_st_numel(t), n);
+            return NULL;
+        }
+        if (t->dtype == IRIS_ST_BF16) return (const uint16_t *)iris_st_ptr(f, t);   /* straight from the map */
+        if (iris_st_read_bf16(f, t, s->stage)) return NULL;
+        return s->stage;
+    }
+    iris_synth_fill_bf16(s->stage, n, iris_synth_seed(s->seed, name), 0, is_norm ? 1.0f : 0.0f, 0.02f);
+    return s->stage;
+}
+
+static uint16_t *upload_bf16(source_t *s, const char *name, size_t n) {
+    const uint16_t *h = src_get(s, name, n, 0);
+    if (!h) return NULL;
+    uint16_t *d = (uint16_t *)iris_hip_malloc(n * 2);
+    if (!d || iris_hip_memcpy_h2d(d, h, n * 2)) { iris_hip_free(d); return NULL; }
+    if (iris_hip_sync()) { iris_hip_free(d); return NULL; }     /* source buffer is reused */
+    return d;
+}
+
+/* Uploads [rows][cols] tensors one after another into a device matrix at row offset. */
+static int upload_rows(source_t *s, const char *name, uint16_t *d, size_t rows, size_t cols) {
+    const uint16_t *h = src_get(s, name, rows * cols, 0);
+    if (!h) return -1;
+    if (iris_hip_memcpy_h2d(d, h, rows * cols * 2)) return -1;
+    return iris_hip_sync();
+}
+
+/* linear_in rows are [gate (mlp rows) | up (mlp rows)] (:633-640); the device
+ * copy interleaves them in groups of 64 rows (gate g, up g, gate g+1, ...) so
+ * the SwiGLU epilogue of one 128-column wave tile sees matching gate/up. */
+static int upload_interleaved(source_t *s, const char *name, uint16_t *d, size_t mlp, size_t cols) {
+    const uint16_t *h = src_get(s, name, 2 * mlp * cols, 0);
+    if (!h) return -1;
+    for (size_t g = 0; g < mlp / 64; g++) {
+        if (iris_hip_memcpy_h2d(d + (2 * g) * 64 * cols, h + g * 64 * cols, 64 * cols * 2)) return -1;
+        if (iris_hip_memcpy_h2d(d + (2 * g + 1) * 64 * cols, h + (mlp + g * 64) * cols, 64 * cols * 2)) return -1;
+    }
+    return iris_hip_sync();
+}
+
+static float *upload_norm(source_t *s, const char *name, size_t n) {
+    const uint16_t *h = src_get(s, name, n, 1);
+    if (!h) return NULL;
+    float tmp[4096];
+    if (n > 4096) return NULL;
+    for (size_t i = 0; i < n; i++) tmp[i] = iris_bf16_to_f32(h[i]);
+    float *d = (float *)iris_hip_malloc(n * sizeof(float));
+    if (!d || iris_hip_memcpy_h2d(d, tmp, n * sizeof(float)) || iris_hip_sync()) { iris_hip_free(d); return NULL; }
+    return d;
+}
+
+static int load_weights(iris_transformer_t *tf, source_t *s) {
+    size_t h = tf->hidden, mlp = tf->mlp, C = tf->latent_ch;
+    char nm[256];
+#define UP(dst, name, n) do { if (!((dst) = upload_bf16(s, (name), (n)))) return -1; } while (0)
+    /* tensor names: iris_transformer_flux.c:5349-5497 */
+    UP(tf->img_in, "x_embedder.weight", h * C);
+    UP(tf->txt_in, "context_embedder.weight", h * tf->text_dim);
+    UP(tf->t_fc1, "time_guidance_embed.timestep_embedder.linear_1.weight", h * 256);
+    UP(tf->t_fc2, "time_guidance_embed.timestep_embedder.linear_2.weight", h * h);
+    UP(tf->mod_dimg, "double_stream_modulation_img.linear.weight", 6 * h * h);
+    UP(tf->mod_dtxt, "double_stream_modulation_txt.linear.weight", 6 * h * h);
+    UP(tf->mod_single, "single_stream_modulation.linear.weight", 3 * h * h);
+    UP(tf->final_mod, "norm_out.linear.weight", 2 * h * h);
+    UP(tf->proj_out, "proj_out.weight", C * h);
+    tf->dbl = (dev_double_t *)calloc((size_t)tf->n_double, sizeof(dev_double_t));
+    tf->sgl = (dev_single_t *)calloc((size_t)tf->n_single, sizeof(dev_single_t));
+    if (!tf->dbl || !tf->sgl) return -1;
+    for (int i = 0; i < tf->n_double; i++) {
+        dev_double_t *b = &tf->dbl[i];
+        static const char *const qkv_img[3] = {"to_q", "to_k", "to_v"};
+        static const char *const qkv_txt[3] = {"add_q_proj", "add_k_proj", "add_v_proj"};
+        b->img_qkv = (uint16_t *)iris_hip_malloc(3 * h * h * 2);
+        b->txt_qkv = (uint16_t *)iris_hip_malloc(3 * h * h * 2);
+        b->img_ffin = (uint16_t *)iris_hip_malloc(2 * mlp * h * 2);
+        b->txt_ffin = (uint16_t *)iris_hip_malloc(2 * mlp * h * 2);
+        if (!b->img_qkv || !b->txt_qkv || !b->img_ffin || !b->txt_ffin) return -1;
+        for (int j = 0; j < 3; j++) {
+            snprintf(nm, sizeof(nm), "transformer_blocks.%d.attn.%s.weight", i, qkv_img[j]);
+            if (upload_rows(s, nm, b->img_qkv + j * h * h, h, h)) return -1;
+            snprintf(nm, sizeof(nm), "transformer_blocks.%d.attn.%s.weight", i, qkv_txt[j]);
+            if (upload_rows(s, nm, b->txt_qkv + j * h * h, h, h)) return -1;
+        }
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.attn.to_out.0.weight", i);
+        UP(b->img_o, nm, h * h);
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.attn.to_add_out.weight", i);
+        UP(b->txt_o, nm, h * h);
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.ff.linear_in.weight", i);
+        if (upload_interleaved(s, nm, b->img_ffin, mlp, h)) return -1;
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.ff_context.linear_in.weight", i);
+        if (upload_interleaved(s, nm, b->txt_ffin, mlp, h)) return -1;
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.ff.linear_out.weight", i);
+        UP(b->img_down, nm, h * mlp);
+        snprintf(nm, sizeof(nm), "transformer_blocks.%d.ff_context.linear_out.weight", i);
+        UP(b->txt_down, nm, h * mlp);
+#define NORM(dst, fmt) do { snprintf(nm, sizeof(nm), fmt, i); if (!((dst) = upload_norm(s, nm, 128))) return -1; } while (0)
+        NORM(b->img_nq, "transformer_blocks.%d.attn.norm_q.weight");
+        NORM(b->img_nk, "transformer_blocks.%d.attn.norm_k.weight");
+        NORM(b->txt_nq, "transformer_blocks.%d.attn.norm_added_q.weight");
+        NORM(b->txt_nk, "transformer_blocks.%d.attn.norm_added_k.weight");
+    }
+    for (int i = 0; i < tf->n_single; i++) {
+        dev_single_t *b = &tf->sgl[i];
+        size_t fused = 3 * h + 2 * mlp;
+        b->qkv_mlp = (uint16_t *)iris_hip_malloc(fused * h * 2);
+        if (!b->qkv_mlp) return -1;
+        snprintf(nm, sizeof(nm), "single_transformer_blocks.%d.attn.to_qkv_mlp_proj.weight", i);
+        const uint16_t *src = src_get(s, nm, fused * h, 0);
+        if (!src) return -1;
+        if (iris_hip_memcpy_h2d(b->qkv_mlp, src, 3 * h * h * 2)) return -1;
+        for (size_t g = 0; g < mlp / 64; g++) {
+            if (iris_hip_memcpy_h2d(b->qkv_mlp + (3 * h + 2 * g * 64) * h, src + (3 * h + g * 64) * h, 64 * h * 2)) return -1;
+            if (iris_hip_memcpy_h2d(b->qkv_mlp + (3 * h + (2 * g + 1) * 64) * h, src + (3 * h + mlp + g * 64) * h,
+                                    64 * h * 2)) return -1;
+        }
+        if (iris_hip_sync()) return -1;
+        snprintf(nm, sizeof(nm), "single_transformer_blocks.%d.attn.to_out.weight", i);
+        UP(b->out, nm, h * (h + mlp));
+        NORM(b->nq, "single_transformer_blocks.%d.attn.norm_q.weight");
+        NORM(b->nk, "single_transformer_blocks.%d.attn.norm_k.weight");
+#undef NORM
+    }
+#undef UP
+    return 0;
+}
+
+static void work_free(work_t *w);
+
+void iris_transformer_free(iris_transformer_t *tf) {
+    if (!tf) return;
+    work_free(&tf->w);
+    iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
+    iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
+    iris_hip_free(tf->final_mod); iris_hip_free(tf->proj_out);
+    for (int i = 0; tf->dbl && i < tf->n_double; i++) {
+        dev_double_t *b = &tf->dbl[i];
+        iris_hip_free(b->img_qkv); iris_hip_free(b->img_o); iris_hip_free(b->img_ffin); iris_hip_free(b->img_down);
+        iris_hip_free(b->txt_qkv); iris_hip_free(b->txt_o); iris_hip_free(b->txt_ffin); iris_hip_free(b->txt_down);
+        iris_hip_free(b->img_nq); iris_hip_free(b->img_nk); iris_hip_free(b->txt_nq); iris_hip_free(b->txt_nk);
+    }
+    for (int i = 0; tf->sgl && i < tf->n_single; i++) {
+        iris_hip_free(tf->sgl[i].qkv_mlp); iris_hip_free(tf->sgl[i].out);
+        iris_hip_free(tf->sgl[i].nq); iris_hip_free(tf->sgl[i].nk);
+    }
+    free(tf->dbl);
+    free(tf->sgl);
+    free(tf);
+}
+
+static iris_transformer_t *finish_load(iris_transformer_t *tf, source_t *s) {
+    int rc = load_weights(tf, s);
+    free(s->stage);
+    if (rc) {
+        fprintf(stderr, "iris_transformer_load: weight upload failed: %s\n", iris_hip_last_error());
+        iris_transformer_free(tf);
+        return NULL;
+    }
+    return tf;
+}
+
+iris_transformer_t *iris_transformer_load_safetensors(const char *model_dir) {
+    if (!iris_hip_available()) {
+        fprintf(stderr, "iris_transformer_load: no usable HIP device: %s\n", iris_hip_last_error());
+        return NULL;
+    }
+    iris_transformer_t *tf = (iris_transformer_t *)calloc(1, sizeof(*tf));
+    if (!tf) return NULL;
+    if (parse_config(model_dir, tf)) defaults_4b(tf);
+    if (check_dims(tf)) { free(tf); return NULL; }
+    iris_st_set_t st;
+    if (iris_st_set_open(&st, model_dir)) {
+        fprintf(stderr, "iris_transformer_load: failed to open safetensors files\n");
+        free(tf);
+        return NULL;
+    }
+    source_t s = {&st, 0, NULL, 0};
+    tf = finish_load(tf, &s);
+    iris_st_set_close(&st);
+    return tf;
+}
+
+/* The weights are device-resident either way; mmap mode only changes how the
+ * reference's CPU path pages them (:5550-5683). */
+iris_transformer_t *iris_transformer_load_safetensors_mmap(const char *model_dir) {
+    return iris_transformer_load_safetensors(model_dir);
+}
+
+void iris_transformer_free_mmap_cache(iris_transformer_t *tf) { (void)tf; }
+
+iris_transformer_t *iris_transformer_create_synthetic(int hidden, int heads, int n_double, int n_single,
+                                                      int text_dim, int latent_ch, float mlp_ratio,
+                                                      float rope_theta, uint64_t seed) {
+    if (!iris_hip_available()) {
+        fprintf(stderr, "iris_transformer_create_synthetic: no usable HIP device: %s\n", iris_hip_last_error());
+        return NULL;
+    }
+    iris_transformer_t *tf = (iris_transformer_t *)calloc(1, sizeof(*tf));
+    if (!tf) return NULL;
+    tf->hidden = hidden; tf->heads = heads; tf->head_dim = hidden / heads;
+    tf->mlp = (int)(hidden * mlp_ratio); tf->n_double = n_double; tf->n_single = n_single;
+    tf->text_dim = text_dim; tf->latent_ch = latent_ch; tf->theta = rope_theta;
+    tf->axis_dim = tf->head_dim / 4;
+    if (check_dims(tf)) { free(tf); return NULL; }
+    source_t s = {NULL, seed, NULL, 0};
+    return finish_load(tf, &s);
+}
+
+int iris_transformer_hidden_size(iris_transformer_t *tf) { return tf->hidden; }
+int iris_transformer_num_double_layers(iris_transformer_t *tf) { return tf->n_double; }
+int iris_transformer_num_single_layers(iris_transformer_t *tf) { return tf->n_single; }
+int iris_transformer_text_dim(iris_transformer_t *tf) { return tf->text_dim; }
+
+/* -------------------------------------------------------------- workspace */
+
+static void work_free(work_t *w) {
+    iris_hip_graph_destroy(w->graph);
+    void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
+                    w->rope_cos, w->rope_sin, w->tsin, w->tmp, w->temb, w->mod};
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
+    free(w->tsin_host);
+    memset(w, 0, sizeof(*w));
+}
+
+static int same_geometry(const work_t *w, int ih, int iw, const iris_ref_t *refs, int n, int T, int B) {
+    if (!w->valid || w->ih != ih || w->iw != iw || w->n_refs != n || w->T != T || w->B != B) return 0;
+    for (int r = 0; r < n; r++)
+        if (w->ref_h[r] != refs[r].h || w->ref_w[r] != refs[r].w || w->ref_t[r] != refs[r].t_offset) return 0;
+    return 1;
+}
+
+static int enqueue_forward(iris_transformer_t *tf);
+
+int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *refs, int n_refs, int T, int B) {
+    work_t *w = &tf->w;
+    if (n_refs < 0 || n_refs > MAX_REFS) { fprintf(stderr, "iris_hip: %d references (max %d)\n", n_refs, MAX_REFS); return -1; }
+    if (B < 1 || B > 2) { fprintf(stderr, "iris_hip: batch %d (1 or 2)\n", B); return -1; }
+    if (ih <= 0 || iw <= 0 || T <= 0) { fprintf(stderr, "iris_hip: empty geometry\n"); return -1; }
+    if (same_geometry(w, ih, iw, refs, n_refs, T, B)) return 0;
+    work_free(w);
+    int h = tf->hidden, mlp = tf->mlp, C = tf->latent_ch, td = tf->text_dim, H = tf->heads;
+    w->ih = ih; w->iw = iw; w->n_refs = n_refs; w->T = T; w->B = B;
+    w->I0 = ih * iw;
+    w->I = w->I0;
+    for (int r = 0; r < n_refs; r++) {
+        w->ref_h[r] = refs[r].h; w->ref_w[r] = refs[r].w; w->ref_t[r] = refs[r].t_offset;
+        w->I += refs[r].h * refs[r].w;
+    }
+    w->S = w->I + T;
+    w->S_pad = (w->S + 63) / 64 * 64;
+    size_t S = w->S, BS = (size_t)B * S;
+#define DA(dst, bytes) do { if (!((dst) = iris_hip_malloc(bytes))) goto fail; } while (0)
+    DA(w->x, BS * h * 4);
+    DA(w->a, BS * h * 2);
+    DA(w->qkv, BS * 3 * h * 2);
+    DA(w->q, BS * h * 2);
+    DA(w->k, BS * h * 2);
+    DA(w->vt, (size_t)B * H * 128 * w->S_pad * 2);
+    DA(w->cat, BS * (h + mlp) * 2);
+    DA(w->tok, (size_t)w->I * C * 2);
+    DA(w->txtb, (size_t)B * T * td * 2);
+    DA(w->txtf, (size_t)B * T * td * 4);
+    DA(w->lat, (size_t)w->I * C * 4);
+    DA(w->vel, (size_t)B * C * w->I0 * 4);
+    DA(w->rope_cos, S * 128 * 4);
+    DA(w->rope_sin, S * 128 * 4);
+    DA(w->tsin, 256 * 4);
+    DA(w->tmp, (size_t)h * 4);
+    DA(w->temb, (size_t)h * 4);
+    DA(w->mod, (size_t)17 * h * 4);
+#undef DA
+    w->tsin_host = (float *)malloc(256 * sizeof(float));
+    if (!w->tsin_host) goto fail;
+    /* RoPE tables in sequence order: txt rows, target, references (:4634-4657) */
+    {
+        float *c = (float *)malloc(S * 128 * sizeof(float)), *s = (float *)malloc(S * 128 * sizeof(float));
+        if (!c || !s) { free(c); free(s); goto fail; }
+        iris_rope_txt(c, s, T, tf->axis_dim, tf->theta);
+        size_t off = (size_t)T * 128;
+        iris_rope_img(c + off, s + off, ih, iw, tf->axis_dim, tf->theta, 0);
+        off += (size_t)w->I0 * 128;
+        for (int r = 0; r < n_refs; r++) {
+            iris_rope_img(c + off, s + off, refs[r].h, refs[r].w, tf->axis_dim, tf->theta, refs[r].t_offset);
+            off += (size_t)refs[r].h * refs[r].w * 128;
+        }
+        int rc = iris_hip_memcpy_h2d(w->rope_cos, c, S * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, S * 128 * 4) ||
+                 iris_hip_sync();
+        free(c); free(s);
+        if (rc) goto fail;
+    }
+    w->valid = 1;
+    /* capture one forward */
+    if (iris_hip_graph_begin()) goto fail;
+    if (enqueue_forward(tf)) {
+        void *g = iris_hip_graph_end();
+        iris_hip_graph_destroy(g);
+        goto fail;
+    }
+    w->graph = iris_hip_graph_end();
+    if (!w->graph) goto fail;
+    return 0;
+fail:
+    fprintf(stderr, "iris_flux_prepare: %s\n", iris_hip_last_error());
+    work_free(w);
+    return -1;
+}
+
+/* ------------------------------------------------------------- the forward */
+
+#define CK(x) do { if ((x) != 0) return -1; } while (0)
+
+static int gemm(const iris_gemm_problem_t *p, int n) { return iris_hip_gemm(p, n); }
+
+static iris_gemm_problem_t prob(const void *A, int lda, const uint16_t *W, int ldw, void *out, int ldo,
+                                const float *vec, int M, int N, int K, int epi) {
+    iris_gemm_problem_t p;
+    p.A = (const uint16_t *)A; p.lda = lda; p.W = W; p.ldw = ldw; p.out = out; p.ldo = ldo;
+    p.vec = vec; p.M = M; p.N = N; p.K = K; p.epi = epi;
+    return p;
+}
+
+/* QK-RMSNorm + RoPE of each stream and V^T for every batch slot */
+static int qk_prepare(iris_transformer_t *tf, const float *wqA, const float *wkA, const float *wqB,
+                      const float *wkB, int split) {
+    work_t *w = &tf->w;
+    int h = tf->hidden;
+    for (int b = 0; b < w->B; b++) {
+        iris_qkprep_args_t a;
+        memset(&a, 0, sizeof(a));
+        a.qkv = w->qkv + (size_t)b * w->S * 3 * h;
+        a.ld_qkv = 3 * h; a.col_k = h; a.col_v = 2 * h;
+        a.q_out = w->q + (size_t)b * w->S * h;
+        a.k_out = w->k + (size_t)b * w->S * h;
+        a.vt_out = w->vt + (size_t)b * tf->heads * 128 * w->S_pad;
+        a.ld_vt = w->S_pad;
+        a.rows = w->S; a.heads = tf->heads;
+        a.wqA = wqA; a.wkA = wkA; a.wqB = wqB; a.wkB = wkB; a.split = split;
+        a.cos_t = w->rope_cos; a.sin_t = w->rope_sin;
+        a.eps = 1e-6f;
+        CK(iris_hip_qk_prepare(&a));
+    }
+    return 0;
+}
+
+static int attention(iris_transformer_t *tf, uint16_t *o, int ld_o) {
+    work_t *w = &tf->w;
+    int h = tf->hidden;
+    iris_attn_args_t a;
+    memset(&a, 0, sizeof(a));
+    a.q = w->q; a.k = w->k; a.vt = w->vt; a.o = o;
+    a.ld_q = h; a.ld_k = h; a.ld_vt = w->S_pad; a.ld_o = ld_o;
+    a.sq = w->S; a.sk = w->S; a.heads = tf->heads; a.batch = w->B;
+    a.q_bstride = (long long)w->S * h; a.k_bstride = (long long)w->S * h;
+    a.vt_bstride = (long long)tf->heads * 128 * w->S_pad; a.o_bstride = (long long)w->S * ld_o;
+    a.scale = 1.0f / sqrtf(128.0f);
+    a.kv_lo0 = 0; a.kv_hi0 = w->S;
+    return iris_hip_attention(&a);
+}
+
+static int adaln(iris_transformer_t *tf, const float *shA, const float *scA, const float *shB, const float *scB,
+                 int split) {
+    work_t *w = &tf->w;
+    iris_norm_args_t a;
+    memset(&a, 0, sizeof(a));
+    a.x = w->x; a.ldx = tf->hidden; a.out = w->a; a.ldo = tf->hidden; a.out_bf16 = 1;
+    a.rows = w->B * w->S; a.cols = tf->hidden; a.mode = IRIS_NORM_LN_MOD; a.eps = 1e-6f;
+    a.split = split; a.period = w->S;
+    a.shiftA = shA; a.scaleA = scA; a.shiftB = shB; a.scaleB = scB;
+    return iris_hip_rownorm(&a);
+}
+
+/* double_block_forward, iris_transformer_flux.c:2366-2614: per batch slot,
+ * txt rows [0, T) use the txt weights/modulation, img rows [T, S) the img ones. */
+static int double_block_forward(iris_transformer_t *tf, int i) {
+    work_t *w = &tf->w;
+    const dev_double_t *bw = &tf->dbl[i];
+    int h = tf->hidden, mlp = tf->mlp, T = w->T, I = w->I, S = w->S, B = w->B, hm = h + mlp;
+    const float *mi = w->mod, *mt = w->mod + 6 * h;      /* shift1 scale1 gate1 shift2 scale2 gate2 */
+    iris_gemm_problem_t p[4];
+    int n;
+    /* AdaLN (shift1, scale1) -> Q, K, V per stream */
+    CK(adaln(tf, mt, mt + h, mi, mi + h, T));
+    n = 0;
+    for (int b = 0; b < B; b++) {
+        size_t r0 = (size_t)b * S;
+        p[n++] = prob(w->a + r0 * h, h, bw->txt_qkv, h, w->qkv + r0 * 3 * h, 3 * h, NULL, T, 3 * h, h, IRIS_EPI_BF16);
+        p[n++] = prob(w->a + (r0 + T) * h, h, bw->img_qkv, h, w->qkv + (r0 + T) * 3 * h, 3 * h, NULL, I, 3 * h, h,
+                      IRIS_EPI_BF16);
+    }
+    CK(gemm(p, n));
+    CK(qk_prepare(tf, bw->txt_nq, bw->txt_nk, bw->img_nq, bw->img_nk, T));
+    /* joint attention over [txt, img] -> cat[:, 0:h] */
+    CK(attention(tf, w->cat, hm));
+    /* output projections, gated residual (gate1) */
+    n = 0;
+    for (int b = 0; b < B; b++) {
+        size_t r0 = (size_t)b * S;
+        p[n++] = prob(w->cat + r0 * hm, hm, bw->txt_o, h, w->x + r0 * h, h, mt + 2 * h, T, h, h, IRIS_EPI_GATED_ADD);
+        p[n++] = prob(w->cat + (r0 + T) * hm, hm, bw->img_o, h, w->x + (r0 + T) * h, h, mi + 2 * h, I, h, h,
+                      IRIS_EPI_GATED_ADD);
+    }
+    CK(gemm(p, n));
+    /* AdaLN (shift2, scale2) -> SwiGLU FFN -> gated residual (gate2) */
+    CK(adaln(tf, mt + 3 * h, mt + 4 * h, mi + 3 * h, mi + 4 * h, T));
+    n = 0;
+    for (int b = 0; b < B; b++) {
+        size_t r0 = (size_t)b * S;
+        p[n++] = prob(w->a + r0 * h, h, bw->txt_ffin, h, w->cat + r0 * hm + h, hm, NULL, T, 2 * mlp, h, IRIS_EPI_SWIGLU);
+        p[n++] = prob(w->a + (r0 + T) * h, h, bw->img_ffin, h, w->cat + (r0 + T) * hm + h, hm, NULL, I, 2 * mlp, h,
+                      IRIS_EPI_SWIGLU);
+    }
+    CK(gemm(p, n));
+    n = 0;
+    for (int b = 0; b < B; b++) {
+        size_t r0 = (size_t)b * S;
+        p[n++] = prob(w->cat + r0 * hm + h, hm, bw->txt_down, mlp, w->x + r0 * h, h, mt + 5 * h, T, h, mlp,
+                      IRIS_EPI_GATED_ADD);
+        p[n++] = prob(w->cat + (r0 + T) * hm + h, hm, bw->img_down, mlp, w->x + (r0 + T) * h, h, mi + 5 * h, I, h, mlp,
+                      IRIS_EPI_GATED_ADD);
+    }
+    CK(gemm(p, n));
+    return 0;
+}
+
+/* single_block_forward, iris_transformer_flux.c:3761-3928 */
+static int single_block_forward(iris_transformer_t *tf, int i) {
+    work_t *w = &tf->w;
+    const dev_single_t *bw = &tf->sgl[i];
+    int h = tf->hidden, mlp = tf->mlp, hm = h + mlp, BS = w->B * w->S;
+    const float *ms = w->mod + 12 * h;                   /* shift scale gate */
+    CK(adaln(tf, ms, ms + h, ms, ms + h, w->S));
+    /* fused projection: Q,K,V rows -> qkv; gate/up rows -> SwiGLU -> cat[:, h:] */
+    iris_gemm_problem_t p[2];
+    p[0] = prob(w->a, h, bw->qkv_mlp, h, w->qkv, 3 * h, NULL, BS, 3 * h, h, IRIS_EPI_BF16);
+    p[1] = prob(w->a, h, bw->qkv_mlp + (size_t)3 * h * h, h, w->cat + h, hm, NULL, BS, 2 * mlp, h, IRIS_EPI_SWIGLU);
+    CK(gemm(p, 2));
+    CK(qk_prepare(tf, bw->nq, bw->nk, bw->nq, bw->nk, w->S));
+    CK(attention(tf, w->cat, hm));
+    /* [attn | mlp] . W_out^T, gated residual */
+    p[0] = prob(w->cat, hm, bw->out, hm, w->x, h, ms + 2 * h, BS, h, hm, IRIS_EPI_GATED_ADD);
+    CK(gemm(p, 1));
+    return 0;
+}
+
+static int enqueue_forward(iris_transformer_t *tf) {
+    work_t *w = &tf->w;
+    int h = tf->hidden, C = tf->latent_ch, td = tf->text_dim, T = w->T, I0 = w->I0, S = w->S, B = w->B;
+    /* timestep MLP (:1366-1379) and the modulation GEMVs on SiLU(t_emb) (:4059-4069,
+     * :3787-3797, :4270-4277); the single-block modulation is the same for all
+     * 20 blocks and is computed once */
+    CK(iris_hip_gemv(w->tmp, tf->t_fc1, w->tsin, NULL, h, 256, 0));
+    CK(iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, NULL, h, h, 1));
+    CK(iris_hip_gemv(w->mod, tf->mod_dimg, w->temb, NULL, 6 * h, h, 1));
+    CK(iris_hip_gemv(w->mod + 6 * h, tf->mod_dtxt, w->temb, NULL, 6 * h, h, 1));
+    CK(iris_hip_gemv(w->mod + 12 * h, tf->mod_single, w->temb, NULL, 3 * h, h, 1));
+    CK(iris_hip_gemv(w->mod + 15 * h, tf->final_mod, w->temb, NULL, 2 * h, h, 1));
+    /* NCHW -> token rows for the target and each reference (:3986-3993, :4667-4689) */
+    size_t off = 0;
+    CK(iris_hip_nchw_to_tokens(w->tok, w->lat, C, I0));
+    off = I0;
+    for (int r = 0; r < w->n_refs; r++) {
+        int rs = w->ref_h[r] * w->ref_w[r];
+        CK(iris_hip_nchw_to_tokens(w->tok + off * C, w->lat + off * C, C, rs));
+        off += rs;
+    }
+    CK(iris_hip_f32_to_bf16(w->txtb, w->txtf, (size_t)B * T * td));
+    /* img_in / txt_in into the residual stream rows [T, S) and [0, T) (:4022-4031) */
+    iris_gemm_problem_t p[4];
+    int n = 0;
+    for (int b = 0; b < B; b++) {
+        size_t r0 = (size_t)b * S;
+        p[n++] = prob(w->txtb + (size_t)b * T * td, td, tf->txt_in, td, w->x + r0 * h, h, NULL, T, h, td, IRIS_EPI_F32);
+        p[n++] = prob(w->tok, C, tf->img_in, C, w->x + (r0 + T) * h, h, NULL, w->I, h, C, IRIS_EPI_F32);
+    }
+    CK(gemm(p, n));
+    for (int i = 0; i < tf->n_double; i++) CK(double_block_forward(tf, i));
+    for (int i = 0; i < tf->n_single; i++) CK(single_block_forward(tf, i));
+    /* final layer on the target rows: AdaLN with (scale, shift) order, proj_out,
+     * written transposed to NCHW (:4254-4301) */
+    const float *fm = w->mod + 15 * h;
+    n = 0;
+    for (int b = 0; b < B; b++) {
+        iris_norm_args_t a;
+        memset(&a, 0, sizeof(a));
+        a.x = w->x + ((size_t)b * S + T) * h; a.ldx = h;
+        a.out = w->a + (size_t)b * I0 * h; a.ldo = h; a.out_bf16 = 1;
+        a.rows = I0; a.cols = h; a.mode = IRIS_NORM_LN_MOD; a.eps = 1e-6f;
+        a.split = I0; a.shiftA = fm + h; a.scaleA = fm;
+        CK(iris_hip_rownorm(&a));
+        p[n++] = prob(w->a + (size_t)b * I0 * h, h, tf->proj_out, h, w->vel + (size_t)b * C * I0, I0, NULL, I0, C, h,
+                      IRIS_EPI_F32_T);
+    }
+    CK(gemm(p, n));
+    return 0;
+}
+
+/* One block on the resident stream (x, modulation, RoPE tables as uploaded),
+ * outside the captured graph: the block functions of the reference
+ * (double_block_forward :2366, single_block_forward :3761) as C entry points. */
+int iris_flux_double_block_forward(iris_transformer_t *tf, int idx) {
+    if (!tf->w.valid || idx < 0 || idx >= tf->n_double) return -1;
+    if (double_block_forward(tf, idx)) return -1;
+    return iris_hip_sync();
+}
+
+int iris_flux_single_block_forward(iris_transformer_t *tf, int idx) {
+    if (!tf->w.valid || idx < 0 || idx >= tf->n_single) return -1;
+    if (single_block_forward(tf, idx)) return -1;
+    return iris_hip_sync();
+}
+
+/* -------------------------------------------------------- step entry points */
+
+int iris_flux_upload(iris_transformer_t *tf, const float *latent, const iris_ref_t *refs, const float *txt) {
+    work_t *w = &tf->w;
+    if (!w->valid) return -1;
+    int C = tf->latent_ch;
+    if (latent && iris_hip_memcpy_h2d(w->lat, latent, (size_t)C * w->I0 * 4)) return -1;
+    size_t off = w->I0;
+    for (int r = 0; refs && r < w->n_refs; r++) {
+        size_t rs = (size_t)w->ref_h[r] * w->ref_w[r];
+        if (iris_hip_memcpy_h2d(w->lat + off * C, refs[r].latent, C * rs * 4)) return -1;
+        off += rs;
+    }
+    if (txt && iris_hip_memcpy_h2d(w->txtf, txt, (size_t)w->B * w->T * tf->text_dim * 4)) return -1;
+    return iris_hip_sync();
+}
+
+int iris_flux_velocity(iris_transformer_t *tf, float t) {
+    work_t *w = &tf->w;
+    if (!w->valid) return -1;
+    /* get_timestep_embedding(t * 1000), :3967 */
+    iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
+    if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
+    if (iris_hip_graph_launch(w->graph)) return -1;
+    return 0;
+}
+
+int iris_flux_step(iris_transformer_t *tf, float t_curr, float t_next, float guidance) {
+    work_t *w = &tf->w;
+    if (iris_flux_velocity(tf, t_curr)) return -1;
+    size_t n = (size_t)tf->latent_ch * w->I0;
+    /* Euler (iris_sample.c:359) or CFG combine (:768-771): slot 0 uncond, 1 cond */
+    if (w->B == 2) return iris_hip_euler(w->lat, w->vel, w->vel + n, guidance, t_next - t_curr, 1.0f, n);
+    return iris_hip_euler(w->lat, w->vel, NULL, 0.0f, t_next - t_curr, 1.0f, n);
+}
+
+int iris_flux_download_latent(iris_transformer_t *tf, float *latent) {
+    return iris_hip_memcpy_d2h(latent, tf->w.lat, (size_t)tf->latent_ch * tf->w.I0 * 4);
+}
+
+int iris_flux_download_velocity(iris_transformer_t *tf, float *v) {
+    return iris_hip_memcpy_d2h(v, tf->w.vel, (size_t)tf->w.B * tf->latent_ch * tf->w.I0 * 4);
+}
+
+void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
+    work_t *w = &tf->w;
+    if (!strcmp(name, "x")) return w->x;
+    if (!strcmp(name, "latent")) return w->lat;
+    if (!strcmp(name, "velocity")) return w->vel;
+    if (!strcmp(name, "tokens")) return w->tok;
+    if (!strcmp(name, "rope_cos")) return w->rope_cos;
+    if (!strcmp(name, "rope_sin")) return w->rope_sin;
+    if (!strcmp(name, "t_emb")) return w->temb;
+    if (!strcmp(name, "mod")) return w->mod;
+    if (!strcmp(name, "a")) return w->a;
+    if (!strcmp(name, "cat")) return w->cat;
+    if (!strcmp(name, "qkv")) return w->qkv;
+    if (!strcmp(name, "q")) return w->q;
+    if (!strcmp(name, "k")) return w->k;
+    if (!strcmp(name, "vt")) return w->vt;
+    if (!strcmp(name, "txt")) return w->txtf;
+    return NULL;
+}
+
+/* ------------------------------------------------------ reference entries */
+
+static float *forward_host(iris_transformer_t *tf, const float *latent, int ih, int iw, const iris_ref_t *refs,
+                           int n_refs, const float *txt, int T, float t) {
+    if (!tf || !latent || !txt) return NULL;
+    if (iris_flux_prepare(tf, ih, iw, refs, n_refs, T, 1)) return NULL;
+    if (iris_flux_upload(tf, latent, refs, txt)) return NULL;
+    if (iris_flux_velocity(tf, t)) return NULL;
+    size_t n = (size_t)tf->latent_ch * ih * iw;
+    float *out = (float *)malloc(n * sizeof(float));
+    if (!out) return NULL;
+    if (iris_hip_memcpy_d2h(out, tf->w.vel, n * sizeof(float))) {
+        fprintf(stderr, "iris_transformer_forward: %s\n", iris_hip_last_error());
+        free(out);
+        return NULL;
+    }
+    return out;
+}
+
+float *iris_transformer_forward(iris_transformer_t *tf, const float *img_latent, int img_h, int img_w,
+                                const float *txt_emb, int txt_seq, float timestep) {
+    return forward_host(tf, img_latent, img_h, img_w, NULL, 0, txt_emb, txt_seq, timestep);
+}
+
+float *iris_transformer_forward_with_refs(iris_transformer_t *tf, const float *img_latent, int img_h, int img_w,
+                                          const float *ref_latent, int ref_h, int ref_w, int t_offset,
+                                          const float *txt_emb, int txt_seq, float timestep) {
+    if (!ref_latent) return iris_transformer_forward(tf, img_latent, img_h, img_w, txt_emb, txt_seq, timestep);
+    iris_ref_t r = {ref_latent, ref_h, ref_w, t_offset};
+    return forward_host(tf, img_latent, img_h, img_w, &r, 1, txt_emb, txt_seq, timestep);
+}
+
+float *iris_transformer_forward_with_multi_refs(iris_transformer_t *tf, const float *img_latent, int img_h,
+                                                int img_w, const iris_ref_t *refs, int num_refs,
+                                                const float *txt_emb, int txt_seq, float timestep) {
+    if (!refs || num_refs == 0)
+        return iris_transformer_forward(tf, img_latent, img_h, img_w, txt_emb, txt_seq, timestep);
+    return forward_host(tf, img_latent, img_h, img_w, refs, num_refs, txt_emb, txt_seq, timestep);
+}

@@ -1,0 +1,189 @@
+/*
+ * iris_sample.c - schedules, seeded noise and Euler samplers (host C).
+ *
+ * Schedules and noise follow iris_sample.c:61-244, :1146-1188 and the
+ * xoshiro256** RNG of iris_kernels.c:50-107 (same seeds give the same noise).
+ * The Euler loops (iris_sample.c:313-405, :412-536, :630-702, :717-802) keep
+ * the latent resident on the device: one upload, one graph replay and one
+ * update kernel per step, one download at the end.
+ */
+#include "../../include/iris_sample.h"
+#include "../../include/iris_hip.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+volatile int iris_cancel_requested = 0;
+
+float *iris_linear_schedule(int n) {
+    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
+    if (!s) return NULL;
+    for (int i = 0; i <= n; i++) s[i] = 1.0f - (float)i / (float)n;
+    return s;
+}
+
+/* compute_empirical_mu, iris_sample.c:144-158 */
+static float empirical_mu(int seq, int n) {
+    const float a1 = 8.73809524e-05f, b1 = 1.89833333f, a2 = 0.00016927f, b2 = 0.45666666f;
+    if (seq > 4300) return a2 * seq + b2;
+    float m200 = a2 * seq + b2, m10 = a1 * seq + b1;
+    float a = (m200 - m10) / 190.0f;
+    return a * n + (m200 - 200.0f * a);
+}
+
+/* iris_official_schedule with generalized_time_snr_shift(sigma = 1), :160-182 */
+float *iris_official_schedule(int n, int seq) {
+    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
+    if (!s) return NULL;
+    float mu = empirical_mu(seq, n);
+    for (int i = 0; i <= n; i++) {
+        float t = 1.0f - (float)i / (float)n;
+        s[i] = t <= 0.0f ? 0.0f : t >= 1.0f ? 1.0f : expf(mu) / (expf(mu) + powf(1.0f / t - 1.0f, 1.0f));
+    }
+    return s;
+}
+
+/* iris_zimage_schedule, :216-244 */
+float *iris_zimage_schedule(int n, int seq) {
+    (void)seq;
+    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
+    if (!s) return NULL;
+    float shift = 3.0f;
+    const char *e = getenv("IRIS_ZIMAGE_SHIFT");
+    if (e && atof(e) > 0.0) shift = (float)atof(e);
+    const float smin = shift * (1.0f / 1000.0f) / (1.0f + (shift - 1.0f) * (1.0f / 1000.0f));
+    for (int i = 0; i < n; i++) {
+        float u = n > 1 ? (float)i / (float)(n - 1) : 0.0f;
+        float raw = 1.0f + (smin - 1.0f) * u;
+        s[i] = shift * raw / (1.0f + (shift - 1.0f) * raw);
+    }
+    s[n] = 0.0f;
+    return s;
+}
+
+/* xoshiro256** seeded with SplitMix64; Box-Muller normals */
+static uint64_t rng[4] = {0x853c49e6748fea9bULL, 0xda3e39cb94b95bdbULL, 0x647c4677a2884327ULL,
+                          0xc6e7918d2e2969f5ULL};
+static inline uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+static uint64_t next64(void) {
+    uint64_t r = rotl64(rng[1] * 5, 7) * 9, t = rng[1] << 17;
+    rng[2] ^= rng[0]; rng[3] ^= rng[1]; rng[1] ^= rng[2]; rng[0] ^= rng[3];
+    rng[2] ^= t; rng[3] = rotl64(rng[3], 45);
+    return r;
+}
+void iris_rng_seed(uint64_t seed) {
+    for (int i = 0; i < 4; i++) {
+        seed += 0x9e3779b97f4a7c15ULL;
+        uint64_t z = seed;
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+        rng[i] = z ^ (z >> 31);
+    }
+}
+float iris_random_uniform(void) { return (float)((next64() >> 11) * (1.0 / 9007199254740992.0)); }
+float iris_random_normal(void) {
+    float u1 = iris_random_uniform(), u2 = iris_random_uniform();
+    while (u1 == 0.0f) u1 = iris_random_uniform();
+    return sqrtf(-2.0f * logf(u1)) * cosf(2.0f * 3.14159265358979323846f * u2);
+}
+
+/* iris_init_noise: a 112x112 field subsampled for smaller latents so a seed
+ * gives the same image at every size (:1146-1188) */
+float *iris_init_noise(int batch, int ch, int h, int w, int64_t seed) {
+    size_t n = (size_t)batch * ch * h * w;
+    float *out = (float *)malloc(n * sizeof(float));
+    if (!out) return NULL;
+    if (seed >= 0) iris_rng_seed((uint64_t)seed);
+    const int M = 112;
+    if (h >= M && w >= M) {
+        for (size_t i = 0; i < n; i++) out[i] = iris_random_normal();
+        return out;
+    }
+    size_t mn = (size_t)batch * ch * M * M;
+    float *mx = (float *)malloc(mn * sizeof(float));
+    if (!mx) { free(out); return NULL; }
+    for (size_t i = 0; i < mn; i++) mx[i] = iris_random_normal();
+    for (int b = 0; b < batch; b++)
+        for (int c = 0; c < ch; c++)
+            for (int y = 0; y < h; y++)
+                for (int x = 0; x < w; x++)
+                    out[(((size_t)b * ch + c) * h + y) * w + x] =
+                        mx[(((size_t)b * ch + c) * M + y * M / h) * M + x * M / w];
+    free(mx);
+    return out;
+}
+
+static float *flux_loop(iris_transformer_t *tf, const float *z, int channels, int h, int w, const iris_ref_t *refs,
+                        int nrefs, const float *txt, int T, int B, float g, const float *sched, int n,
+                        void (*cb)(int, int)) {
+    if (n > IRIS_MAX_STEPS) {
+        fprintf(stderr, "iris_sample: num_steps %d exceeds IRIS_MAX_STEPS %d\n", n, IRIS_MAX_STEPS);
+        return NULL;
+    }
+    (void)channels;
+    if (iris_flux_prepare(tf, h, w, refs, nrefs, T, B) || iris_flux_upload(tf, z, refs, txt)) return NULL;
+    for (int i = 0; i < n; i++) {
+        if (iris_cancel_requested) return NULL;
+        if (iris_flux_step(tf, sched[i], sched[i + 1], g)) return NULL;
+        if (cb) cb(i + 1, n);
+    }
+    size_t sz = (size_t)channels * h * w;
+    float *out = (float *)malloc(sz * sizeof(float));
+    if (!out || iris_flux_download_latent(tf, out)) { free(out); return NULL; }
+    return out;
+}
+
+float *iris_sample_euler(void *transformer, void *text_encoder, float *z, int batch, int channels, int h, int w,
+                         const float *text_emb, int text_seq, const float *schedule, int num_steps,
+                         void (*progress_callback)(int, int)) {
+    (void)text_encoder; (void)batch;
+    return flux_loop((iris_transformer_t *)transformer, z, channels, h, w, NULL, 0, text_emb, text_seq, 1, 0.0f,
+                     schedule, num_steps, progress_callback);
+}
+
+float *iris_sample_euler_with_multi_refs(void *transformer, void *text_encoder, float *z, int batch, int channels,
+                                         int h, int w, const iris_ref_t *refs, int num_refs, const float *text_emb,
+                                         int text_seq, const float *schedule, int num_steps,
+                                         void (*progress_callback)(int, int)) {
+    (void)text_encoder; (void)batch;
+    return flux_loop((iris_transformer_t *)transformer, z, channels, h, w, refs, num_refs, text_emb, text_seq, 1, 0.0f,
+                     schedule, num_steps, progress_callback);
+}
+
+float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, int batch, int channels, int h, int w,
+                             const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
+                             int text_seq_uncond, float guidance_scale, const float *schedule, int num_steps,
+                             void (*progress_callback)(int, int)) {
+    (void)text_encoder; (void)batch;
+    iris_transformer_t *tf = (iris_transformer_t *)transformer;
+    if (text_seq_cond == text_seq_uncond) {
+        /* one batch-2 pass per step: slot 0 = uncond, slot 1 = cond */
+        size_t tsz = (size_t)text_seq_cond * iris_transformer_text_dim(tf);
+        float *both = (float *)malloc(2 * tsz * sizeof(float));
+        if (!both) return NULL;
+        memcpy(both, text_emb_uncond, tsz * sizeof(float));
+        memcpy(both + tsz, text_emb_cond, tsz * sizeof(float));
+        float *r = flux_loop(tf, z, channels, h, w, NULL, 0, both, text_seq_cond, 2, guidance_scale, schedule,
+                             num_steps, progress_callback);
+        free(both);
+        return r;
+    }
+    /* different text lengths: two sequential forwards per step, as the reference */
+    size_t n = (size_t)channels * h * w;
+    float *zc = (float *)malloc(n * sizeof(float));
+    if (!zc) return NULL;
+    memcpy(zc, z, n * sizeof(float));
+    for (int i = 0; i < num_steps; i++) {
+        if (iris_cancel_requested) { free(zc); return NULL; }
+        float *vu = iris_transformer_forward(tf, zc, h, w, text_emb_uncond, text_seq_uncond, schedule[i]);
+        float *vc = vu ? iris_transformer_forward(tf, zc, h, w, text_emb_cond, text_seq_cond, schedule[i]) : NULL;
+        if (!vu || !vc) { free(vu); free(vc); free(zc); return NULL; }
+        float dt = schedule[i + 1] - schedule[i];
+        for (size_t j = 0; j < n; j++) zc[j] += dt * (vu[j] + guidance_scale * (vc[j] - vu[j]));
+        free(vu); free(vc);
+        if (progress_callback) progress_callback(i + 1, num_steps);
+    }
+    return zc;
+}

@@ -54,6 +54,150 @@ def oracle():
     return _libs["oracle"]
 
 
+class GemmProblem(ctypes.Structure):
+    _fields_ = [("A", ctypes.c_void_p), ("W", ctypes.c_void_p), ("out", ctypes.c_void_p), ("vec", ctypes.c_void_p),
+                ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("lda", ctypes.c_int),
+                ("ldw", ctypes.c_int), ("ldo", ctypes.c_int), ("epi", ctypes.c_int)]
+
+
+class NormArgs(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("ldx", ctypes.c_int), ("out", ctypes.c_void_p), ("ldo", ctypes.c_int),
+                ("out_bf16", ctypes.c_int), ("rows", ctypes.c_int), ("cols", ctypes.c_int), ("mode", ctypes.c_int),
+                ("eps", ctypes.c_float), ("split", ctypes.c_int), ("period", ctypes.c_int),
+                ("shiftA", ctypes.c_void_p), ("scaleA", ctypes.c_void_p), ("wA", ctypes.c_void_p),
+                ("shiftB", ctypes.c_void_p), ("scaleB", ctypes.c_void_p), ("wB", ctypes.c_void_p)]
+
+
+class QkPrepArgs(ctypes.Structure):
+    _fields_ = [("qkv", ctypes.c_void_p), ("ld_qkv", ctypes.c_int), ("col_k", ctypes.c_int), ("col_v", ctypes.c_int),
+                ("q_out", ctypes.c_void_p), ("k_out", ctypes.c_void_p), ("vt_out", ctypes.c_void_p),
+                ("ld_vt", ctypes.c_int), ("rows", ctypes.c_int), ("heads", ctypes.c_int),
+                ("wqA", ctypes.c_void_p), ("wkA", ctypes.c_void_p), ("wqB", ctypes.c_void_p), ("wkB", ctypes.c_void_p),
+                ("split", ctypes.c_int), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
+                ("period", ctypes.c_int), ("eps", ctypes.c_float)]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("vt", ctypes.c_void_p), ("o", ctypes.c_void_p),
+                ("ld_q", ctypes.c_int), ("ld_k", ctypes.c_int), ("ld_vt", ctypes.c_int), ("ld_o", ctypes.c_int),
+                ("sq", ctypes.c_int), ("sk", ctypes.c_int), ("heads", ctypes.c_int), ("batch", ctypes.c_int),
+                ("q_bstride", ctypes.c_longlong), ("k_bstride", ctypes.c_longlong),
+                ("vt_bstride", ctypes.c_longlong), ("o_bstride", ctypes.c_longlong),
+                ("scale", ctypes.c_float), ("kv_lo0", ctypes.c_int), ("kv_hi0", ctypes.c_int),
+                ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int)]
+
+
+class IrisRef(ctypes.Structure):
+    _fields_ = [("latent", FP), ("h", ctypes.c_int), ("w", ctypes.c_int), ("t_offset", ctypes.c_int)]
+
+
+def hip():
+    """The product: the HIP build's C ABI (iris.c_amd/libiris_hip.so). Fails
+    loudly when it is missing: there is no fallback path."""
+    if "hip" not in _libs:
+        if not os.path.exists(HIP_SO):
+            raise RuntimeError(f"{HIP_SO} is not built (python -c 'import __graft_entry__ as g; g.build()')")
+        lib = ctypes.CDLL(HIP_SO)
+        vp = ctypes.c_void_p
+        lib.iris_hip_malloc.restype = vp
+        lib.iris_hip_malloc.argtypes = [ctypes.c_size_t]
+        lib.iris_hip_free.argtypes = [vp]
+        lib.iris_hip_memcpy_h2d.argtypes = [vp, vp, ctypes.c_size_t]
+        lib.iris_hip_memcpy_d2h.argtypes = [vp, vp, ctypes.c_size_t]
+        lib.iris_hip_memset.argtypes = [vp, ctypes.c_int, ctypes.c_size_t]
+        lib.iris_hip_last_error.restype = ctypes.c_char_p
+        lib.iris_hip_device_name.restype = ctypes.c_char_p
+        lib.iris_hip_event_elapsed_ms.restype = ctypes.c_float
+        lib.iris_hip_gemv.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_euler.argtypes = [vp, vp, vp, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_size_t]
+        lib.iris_hip_nchw_to_tokens.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_patchify.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_unpatchify.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_rms_gated_add.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        lib.iris_transformer_load_safetensors.restype = vp
+        lib.iris_transformer_create_synthetic.restype = vp
+        lib.iris_transformer_create_synthetic.argtypes = [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_float,
+                                                                                ctypes.c_uint64]
+        lib.iris_transformer_free.argtypes = [vp]
+        for fn in ("iris_transformer_forward", "iris_transformer_forward_with_multi_refs",
+                   "iris_transformer_forward_with_refs", "iris_sample_euler", "iris_sample_euler_cfg",
+                   "iris_sample_euler_with_multi_refs", "zi_transformer_forward", "iris_official_schedule",
+                   "iris_init_noise", "zi_transformer_load_safetensors", "zi_transformer_create_synthetic",
+                   "iris_sample_euler_zimage", "iris_zimage_schedule"):
+            if hasattr(lib, fn):
+                getattr(lib, fn).restype = vp
+        lib.iris_flux_device_buffer.restype = vp
+        lib.iris_flux_device_buffer.argtypes = [vp, ctypes.c_char_p]
+        for fn in ("iris_flux_prepare", "iris_flux_upload", "iris_flux_velocity", "iris_flux_step",
+                   "iris_flux_download_latent", "iris_flux_download_velocity", "iris_flux_double_block_forward",
+                   "iris_flux_single_block_forward"):
+            getattr(lib, fn).restype = ctypes.c_int
+        lib.iris_flux_prepare.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int]
+        lib.iris_flux_upload.argtypes = [vp, vp, vp, vp]
+        lib.iris_flux_velocity.argtypes = [vp, ctypes.c_float]
+        lib.iris_flux_step.argtypes = [vp, ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        lib.iris_flux_download_latent.argtypes = [vp, vp]
+        lib.iris_flux_download_velocity.argtypes = [vp, vp]
+        lib.iris_flux_double_block_forward.argtypes = [vp, ctypes.c_int]
+        lib.iris_flux_single_block_forward.argtypes = [vp, ctypes.c_int]
+        if lib.iris_hip_init(0) != 0:
+            raise RuntimeError("iris_hip_init failed: " + lib.iris_hip_last_error().decode())
+        _libs["hip"] = lib
+    return _libs["hip"]
+
+
+class Dev:
+    """A device buffer of the product library (freed on close/gc)."""
+
+    def __init__(self, nbytes):
+        self.lib = hip()
+        self.n = int(nbytes)
+        self.ptr = self.lib.iris_hip_malloc(max(self.n, 1))
+        assert self.ptr, self.lib.iris_hip_last_error()
+
+    @classmethod
+    def of(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        d = cls(arr.nbytes)
+        d.put(arr)
+        return d
+
+    def put(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert self.lib.iris_hip_memcpy_h2d(self.ptr, arr.ctypes.data, arr.nbytes) == 0
+        assert self.lib.iris_hip_sync() == 0
+
+    def get(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        assert self.lib.iris_hip_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes) == 0
+        return out
+
+    def close(self):
+        if self.ptr:
+            self.lib.iris_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def to_bf16(a):
+    """float32 -> bf16 bits, round to nearest even (same as the device)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def d2h_f32(lib, ptr, shape):
+    out = np.empty(shape, np.float32)
+    assert lib.iris_hip_memcpy_d2h(out.ctypes.data, ptr, out.nbytes) == 0
+    return out
+
+
 def find_openblas():
     """The OpenBLAS bundled with scipy (same image on every machine)."""
     try:

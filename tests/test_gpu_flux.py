@@ -1,0 +1,279 @@
+"""Flux.2-Klein denoiser parity: HIP build vs the oracle and the reference goldens.
+
+Bars: RoPE tables and token layout bit-exact; each
+block's output within rel-L2 1e-2 of the f32 reference; final latents cosine
+>= 0.999. Blocks are also checked on their residual delta (out - in), which is
+the part the block computes, at rel-L2 3e-2.
+"""
+import ctypes
+import json
+import os
+import tempfile
+
+import numpy as np
+import pytest
+
+import iris_testlib as tl
+
+pytestmark = pytest.mark.gpu
+F = ctypes.c_float
+G = np.load(os.path.join(tl.GOLDEN, "reference_small.npz"), allow_pickle=False)
+MAN = json.load(open(os.path.join(tl.GOLDEN, "manifest.json")))
+TINY = MAN["flux_tiny"]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return tl.hip()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return tl.oracle()
+
+
+@pytest.fixture(scope="module")
+def tiny_dir():
+    with tempfile.TemporaryDirectory() as d:
+        tl.write_flux_model(d, TINY, TINY["seed"])
+        yield d
+
+
+@pytest.fixture(scope="module")
+def tiny(lib, tiny_dir):
+    tf = lib.iris_transformer_load_safetensors(tiny_dir.encode())
+    assert tf, lib.iris_hip_last_error()
+    yield ctypes.c_void_p(tf)
+    lib.iris_transformer_free(ctypes.c_void_p(tf))
+
+
+@pytest.fixture(scope="module")
+def tiny_orc(orc, tiny_dir):
+    m = orc.orc_flux_load(tiny_dir.encode())
+    yield ctypes.c_void_p(m)
+    orc.orc_flux_free(ctypes.c_void_p(m))
+
+
+def buf(lib, tf, name):
+    p = lib.iris_flux_device_buffer(tf, name.encode())
+    assert p
+    return p
+
+
+def put(lib, ptr, arr):
+    arr = np.ascontiguousarray(arr)
+    assert lib.iris_hip_memcpy_h2d(ptr, arr.ctypes.data, arr.nbytes) == 0
+    assert lib.iris_hip_sync() == 0
+
+
+def oracle_rope(orc, ph, pw, T):
+    ic, is_ = np.zeros(ph * pw * 128, np.float32), np.zeros(ph * pw * 128, np.float32)
+    orc.orc_rope_img(tl.fptr(ic), tl.fptr(is_), ph, pw, 32, F(2000.0), 0)
+    tc, ts = np.zeros(T * 128, np.float32), np.zeros(T * 128, np.float32)
+    orc.orc_rope_txt(tl.fptr(tc), tl.fptr(ts), T, 32, F(2000.0))
+    return ic, is_, tc, ts
+
+
+def test_rope_tables_resident_bit_exact(lib, orc, tiny):
+    """Tables uploaded by the HIP build == the reference build's (digest) == oracle."""
+    for (ph, pw, T) in [(64, 64, 512), (8, 8, 32)]:
+        assert lib.iris_flux_prepare(tiny, ph, pw, None, 0, T, 1) == 0
+        S = ph * pw + T
+        c = tl.d2h_f32(lib, buf(lib, tiny, "rope_cos"), (S, 128))
+        s = tl.d2h_f32(lib, buf(lib, tiny, "rope_sin"), (S, 128))
+        assert tl.sha(c[T:], s[T:]) == MAN["sha256"][f"img_{ph}x{pw}_t0"]
+        assert tl.sha(c[:T], s[:T]) == MAN["sha256"][f"txt_{T}"]
+        ic, is_, tc, ts = oracle_rope(orc, ph, pw, T)
+        assert tl.sha(c[T:], s[T:]) == tl.sha(ic, is_) and tl.sha(c[:T], s[:T]) == tl.sha(tc, ts)
+
+
+def test_multiref_rope_and_token_layout_bit_exact(lib, tiny):
+    """Reference rows follow the target with their own T offsets (t = 1, 2), and
+    the token matrix is the NCHW -> [pos][channel] permutation (bf16 of the input)."""
+    lat = tl.synth_f32((128, 8, 8), 21)
+    r1, r2 = tl.synth_f32((128, 8, 8), 23), tl.synth_f32((128, 4, 6), 24)
+    refs = (tl.IrisRef * 2)(tl.IrisRef(tl.fptr(r1), 8, 8, 1), tl.IrisRef(tl.fptr(r2), 4, 6, 2))
+    txt = tl.synth_f32((32, 256), 22)
+    p = lib.iris_transformer_forward_with_multi_refs(tiny, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(txt), 32, F(0.6))
+    assert p
+    ctypes.CDLL(None).free(ctypes.c_void_p(p))
+    S = 32 + 64 + 64 + 24
+    c = tl.d2h_f32(lib, buf(lib, tiny, "rope_cos"), (S, 128))
+    s = tl.d2h_f32(lib, buf(lib, tiny, "rope_sin"), (S, 128))
+    assert tl.sha(c[96:160], s[96:160]) == MAN["sha256"]["img_8x8_t1"]
+    assert tl.sha(c[160:], s[160:]) == MAN["sha256"]["img_4x6_t2"]
+    tok = np.empty((64 + 64 + 24, 128), np.uint16)
+    assert lib.iris_hip_memcpy_d2h(tok.ctypes.data, buf(lib, tiny, "tokens"), tok.nbytes) == 0
+    want = np.concatenate([a.reshape(128, -1).T for a in (lat, r1, r2)])
+    np.testing.assert_array_equal(tok, tl.to_bf16(want))
+
+
+def test_double_block(lib, orc, tiny, tiny_orc):
+    I, T, h = 64, 32, 256
+    img, txt = tl.synth_f32((I, h), 11), tl.synth_f32((T, h), 12)
+    mi, mt = tl.synth_f32((6 * h,), 13, 0, 0.5), tl.synth_f32((6 * h,), 14, 0, 0.5)
+    assert lib.iris_flux_prepare(tiny, 8, 8, None, 0, T, 1) == 0
+    put(lib, buf(lib, tiny, "x"), np.concatenate([txt, img]))
+    put(lib, buf(lib, tiny, "mod"), np.concatenate([mi, mt]))
+    assert lib.iris_flux_double_block_forward(tiny, 1) == 0, lib.iris_hip_last_error()
+    got = tl.d2h_f32(lib, buf(lib, tiny, "x"), (T + I, h))
+    ri, rt = img.copy(), txt.copy()
+    r = oracle_rope(orc, 8, 8, T)
+    orc.orc_flux_double_block(tiny_orc, 1, tl.fptr(ri), tl.fptr(rt), tl.fptr(mi), tl.fptr(mt), *map(tl.fptr, r), I, T)
+    ref = np.concatenate([rt, ri])
+    assert tl.rel_l2(got, ref) < 1e-2
+    assert tl.rel_l2(got - np.concatenate([txt, img]), ref - np.concatenate([txt, img])) < 3e-2
+    # and the reference's own output on the same inputs
+    assert tl.rel_l2(got, np.concatenate([G["flux_dbl1_txt"], G["flux_dbl1_img"]])) < 1e-2
+
+
+def test_single_block(lib, orc, tiny, tiny_orc):
+    I, T, h = 64, 32, 256
+    x, temb = tl.synth_f32((T + I, h), 15), tl.synth_f32((h,), 16)
+    sgl = np.zeros(3 * h, np.float32)
+    orc.orc_flux_modulation(tiny_orc, tl.fptr(temb), None, None, tl.fptr(sgl), None)
+    assert lib.iris_flux_prepare(tiny, 8, 8, None, 0, T, 1) == 0
+    put(lib, buf(lib, tiny, "x"), x)
+    put(lib, buf(lib, tiny, "mod") + 12 * h * 4, sgl)
+    assert lib.iris_flux_single_block_forward(tiny, 1) == 0, lib.iris_hip_last_error()
+    got = tl.d2h_f32(lib, buf(lib, tiny, "x"), (T + I, h))
+    ref = x.copy()
+    orc.orc_flux_single_block(tiny_orc, 1, tl.fptr(ref), tl.fptr(temb), *map(tl.fptr, oracle_rope(orc, 8, 8, T)),
+                              T + I, T)
+    assert tl.rel_l2(got, ref) < 1e-2
+    assert tl.rel_l2(got - x, ref - x) < 3e-2
+    assert tl.rel_l2(got, G["flux_sgl1_x"]) < 1e-2
+
+
+def take(lib, p, n):
+    assert p, lib.iris_hip_last_error()
+    out = np.ctypeslib.as_array(ctypes.cast(p, tl.FP), shape=(n,)).copy()
+    ctypes.CDLL(None).free(ctypes.c_void_p(p))
+    return out
+
+
+def test_forward_vs_reference(lib, orc, tiny, tiny_orc):
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    got = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+    ref = tl.take_f32(orc, orc.orc_flux_forward(tiny_orc, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+    assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+    assert tl.rel_l2(got, G["flux_fwd"]) < 1e-2 and tl.cosine(got, G["flux_fwd"]) > 0.999
+
+
+def test_forward_multi_refs_vs_reference(lib, tiny):
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    r1, r2 = tl.synth_f32((128, 8, 8), 23), tl.synth_f32((128, 4, 6), 24)
+    refs = (tl.IrisRef * 2)(tl.IrisRef(tl.fptr(r1), 8, 8, 1), tl.IrisRef(tl.fptr(r2), 4, 6, 2))
+    got = take(lib, lib.iris_transformer_forward_with_multi_refs(tiny, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(txt), 32,
+                                                                 F(0.6)), 8192)
+    assert tl.rel_l2(got, G["flux_fwd_refs"]) < 1e-2 and tl.cosine(got, G["flux_fwd_refs"]) > 0.999
+
+
+def test_two_step_sample_vs_reference(lib, tiny):
+    """iris_sample_euler on the reference's own noise and schedule."""
+    sched = G["flux_sample2_sched"].copy()
+    z = G["flux_noise42"].copy()
+    txt = tl.synth_f32((32, 256), 22)
+    lib.iris_sample_euler.argtypes = [ctypes.c_void_p, ctypes.c_void_p, tl.FP, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, tl.FP, ctypes.c_int, tl.FP, ctypes.c_int,
+                                      ctypes.c_void_p]
+    got = take(lib, lib.iris_sample_euler(tiny, None, tl.fptr(z), 1, 128, 8, 8, tl.fptr(txt), 32, tl.fptr(sched), 2,
+                                          None), 8192)
+    assert tl.cosine(got, G["flux_sample2"]) > 0.999 and tl.rel_l2(got, G["flux_sample2"]) < 1e-2
+
+
+def test_cfg_batch2_equals_two_passes(lib, tiny):
+    """CFG as one batch-2 pass == v_u + g (v_c - v_u) from two single passes."""
+    lat = tl.synth_f32((128, 8, 8), 51)
+    tc, tu = tl.synth_f32((32, 256), 52), tl.synth_f32((32, 256), 53)
+    vu = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(tu), 32, F(0.7)), 8192)
+    vc = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(tc), 32, F(0.7)), 8192)
+    sched = np.array([0.7, 0.5], np.float32)
+    lib.iris_sample_euler_cfg.argtypes = [ctypes.c_void_p, ctypes.c_void_p, tl.FP] + [ctypes.c_int] * 4 + [
+        tl.FP, ctypes.c_int, tl.FP, ctypes.c_int, ctypes.c_float, tl.FP, ctypes.c_int, ctypes.c_void_p]
+    got = take(lib, lib.iris_sample_euler_cfg(tiny, None, tl.fptr(lat), 1, 128, 8, 8, tl.fptr(tc), 32, tl.fptr(tu), 32,
+                                              4.0, tl.fptr(sched), 1, None), 8192)
+    want = lat.ravel() + np.float32(-0.2) * (vu + 4.0 * (vc - vu))
+    assert tl.rel_l2(got, want) < 1e-5
+
+
+def test_synthetic_equals_safetensors(lib, tiny):
+    """iris_transformer_create_synthetic == loading the written safetensors."""
+    tf2 = ctypes.c_void_p(lib.iris_transformer_create_synthetic(256, 2, TINY["n_double"], TINY["n_single"],
+                                                                TINY["text_dim"], 128, 3.0, 2000.0, TINY["seed"]))
+    assert tf2
+    lat, txt = tl.synth_f32((128, 8, 8), 61), tl.synth_f32((32, 256), 62)
+    a = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.5)), 8192)
+    b = take(lib, lib.iris_transformer_forward(tf2, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.5)), 8192)
+    lib.iris_transformer_free(tf2)
+    np.testing.assert_array_equal(a, b)
+
+
+C1_PATH = os.path.join(tl.GOLDEN, "reference_c1_single_block.npz")
+
+
+@pytest.fixture(scope="module")
+def c1_models(lib, orc):
+    seed = MAN["c1"]["seed"]
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 1, 7680, 128, 3.0, 2000.0, seed))
+    m = ctypes.c_void_p(orc.orc_flux_create_synth(3072, 24, 1, 1, 7680, 128, 3.0, 2000.0, seed))
+    assert tf and m
+    yield tf, m
+    lib.iris_transformer_free(tf)
+    orc.orc_flux_free(m)
+
+
+def test_c1_single_block_4b_shape(lib, orc, c1_models):
+    """one 4B-shaped single block, 128 txt + 256 img (16x16),
+    x ~ N(0,1), conditioning ~ N(0,1); vs the oracle and the reference golden."""
+    tf, m = c1_models
+    T, I, h = 128, 256, 3072
+    x, temb = tl.synth_f32((T + I, h), 41), tl.synth_f32((h,), 42)
+    sgl = np.zeros(3 * h, np.float32)
+    orc.orc_flux_modulation(m, tl.fptr(temb), None, None, tl.fptr(sgl), None)
+    assert lib.iris_flux_prepare(tf, 16, 16, None, 0, T, 1) == 0
+    put(lib, buf(lib, tf, "x"), x)
+    put(lib, buf(lib, tf, "mod") + 12 * h * 4, sgl)
+    assert lib.iris_flux_single_block_forward(tf, 0) == 0
+    got = tl.d2h_f32(lib, buf(lib, tf, "x"), (T + I, h))
+    ref = x.copy()
+    orc.orc_flux_single_block(m, 0, tl.fptr(ref), tl.fptr(temb), *map(tl.fptr, oracle_rope(orc, 16, 16, T)), T + I, T)
+    assert tl.rel_l2(got, ref) < 1e-2
+    assert tl.rel_l2(got - x, ref - x) < 3e-2
+    if os.path.exists(C1_PATH):
+        g = np.load(C1_PATH, allow_pickle=False)
+        assert tl.rel_l2(got.ravel()[::97], g["c1_out_sub"]) < 1e-2
+        assert tl.rel_l2((got - x).ravel()[::97], g["c1_delta_sub"]) < 3e-2
+
+
+def test_c1_double_block_4b_shape(lib, orc, c1_models):
+    tf, m = c1_models
+    T, I, h = 128, 256, 3072
+    img, txt = tl.synth_f32((I, h), 43), tl.synth_f32((T, h), 44)
+    mi, mt = tl.synth_f32((6 * h,), 45, 0, 0.3), tl.synth_f32((6 * h,), 46, 0, 0.3)
+    assert lib.iris_flux_prepare(tf, 16, 16, None, 0, T, 1) == 0
+    put(lib, buf(lib, tf, "x"), np.concatenate([txt, img]))
+    put(lib, buf(lib, tf, "mod"), np.concatenate([mi, mt]))
+    assert lib.iris_flux_double_block_forward(tf, 0) == 0
+    got = tl.d2h_f32(lib, buf(lib, tf, "x"), (T + I, h))
+    ri, rt = img.copy(), txt.copy()
+    orc.orc_flux_double_block(m, 0, tl.fptr(ri), tl.fptr(rt), tl.fptr(mi), tl.fptr(mt),
+                              *map(tl.fptr, oracle_rope(orc, 16, 16, T)), I, T)
+    ref = np.concatenate([rt, ri])
+    x0 = np.concatenate([txt, img])
+    assert tl.rel_l2(got, ref) < 1e-2
+    assert tl.rel_l2(got - x0, ref - x0) < 3e-2
+
+
+def test_4b_forward_reduced_depth(lib, orc):
+    """4B widths (h 3072, 24 heads, text 7680) with 1 double + 2 single blocks at
+    512^2 geometry (32x32 latents, 512 text tokens): full forward vs the oracle."""
+    seed = 99
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 2, 7680, 128, 3.0, 2000.0, seed))
+    m = ctypes.c_void_p(orc.orc_flux_create_synth(3072, 24, 1, 2, 7680, 128, 3.0, 2000.0, seed))
+    lat, txt = tl.synth_f32((128, 32, 32), 71), tl.synth_f32((512, 7680), 72)
+    got = take(lib, lib.iris_transformer_forward(tf, tl.fptr(lat), 32, 32, tl.fptr(txt), 512, F(0.9)), 128 * 1024)
+    ref = tl.take_f32(orc, orc.orc_flux_forward(m, tl.fptr(lat), 32, 32, tl.fptr(txt), 512, F(0.9)), 128 * 1024)
+    lib.iris_transformer_free(tf)
+    orc.orc_flux_free(m)
+    assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999

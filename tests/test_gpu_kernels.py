@@ -1,0 +1,230 @@
+"""Kernel-level parity of the HIP layer through its C ABI (needs an MI355X).
+
+References are float64 numpy computations on the same bf16-rounded operands;
+tolerances are stated per test (bf16 outputs carry ~2^-9 relative rounding).
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+import iris_testlib as tl
+
+pytestmark = pytest.mark.gpu
+EPI_F32, EPI_BF16, EPI_GATED_ADD, EPI_SWIGLU, EPI_F32_T = range(5)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return tl.hip()
+
+
+def bf(a):
+    return tl.bf16_to_f32(tl.to_bf16(a))
+
+
+def run_gemm(lib, problems):
+    arr = (tl.GemmProblem * len(problems))(*problems)
+    rc = lib.iris_hip_gemm(arr, len(problems))
+    assert rc == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 64), (384, 3072, 3072), (1000, 520, 128), (64, 27648, 256),
+                                   (4608, 256, 12288), (17, 33 * 8, 192)])
+def test_gemm_f32(lib, M, N, K):
+    rng = np.random.default_rng(M * 7 + N)
+    A = rng.standard_normal((M, K), np.float32)
+    W = (rng.standard_normal((N, K), np.float32) * 0.02)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dW = tl.Dev.of(tl.to_bf16(A)), tl.Dev.of(tl.to_bf16(W))
+    dO, dB = tl.Dev(M * N * 4), tl.Dev.of(bias)
+    run_gemm(lib, [tl.GemmProblem(dA.ptr, dW.ptr, dO.ptr, dB.ptr, M, N, K, K, K, N, EPI_F32)])
+    got = dO.get(np.float32, (M, N))
+    ref = bf(A).astype(np.float64) @ bf(W).astype(np.float64).T + bias
+    assert tl.rel_l2(got, ref) < 1e-5
+
+
+def test_gemm_epilogues_and_grouping(lib):
+    """bf16 store, gated residual, SwiGLU on 64-row interleaved gate/up, transposed
+    store, and four problems in one launch with strided operands."""
+    rng = np.random.default_rng(1)
+    T, I, K, N, mlp = 70, 300, 256, 384, 256
+    A = rng.standard_normal((T + I, K), np.float32)
+    W1 = rng.standard_normal((N, K), np.float32) * 0.05
+    W2 = rng.standard_normal((N, K), np.float32) * 0.05
+    gate = rng.standard_normal(N).astype(np.float32)
+    x0 = rng.standard_normal((T + I, N), np.float32)
+    Wg = rng.standard_normal((2 * mlp, K), np.float32) * 0.05     # gate rows, then up rows
+    inter = np.concatenate([np.concatenate([Wg[g * 64:(g + 1) * 64], Wg[mlp + g * 64:mlp + (g + 1) * 64]])
+                            for g in range(mlp // 64)])
+    dA = tl.Dev.of(tl.to_bf16(A))
+    dW1, dW2, dWg = tl.Dev.of(tl.to_bf16(W1)), tl.Dev.of(tl.to_bf16(W2)), tl.Dev.of(tl.to_bf16(inter))
+    dX, dG = tl.Dev.of(x0), tl.Dev.of(gate)
+    dO16 = tl.Dev((T + I) * N * 2)
+    dSw = tl.Dev((T + I) * mlp * 2)
+    dT = tl.Dev(N * I * 4)
+    P = tl.GemmProblem
+    run_gemm(lib, [P(dA.ptr, dW1.ptr, dX.ptr, dG.ptr, T, N, K, K, K, N, EPI_GATED_ADD),
+                   P(dA.ptr + T * K * 2, dW2.ptr, dX.ptr + T * N * 4, dG.ptr, I, N, K, K, K, N, EPI_GATED_ADD),
+                   P(dA.ptr, dW1.ptr, dO16.ptr, None, T + I, N, K, K, K, N, EPI_BF16),
+                   P(dA.ptr, dWg.ptr, dSw.ptr, None, T + I, 2 * mlp, K, K, K, mlp, EPI_SWIGLU)])
+    run_gemm(lib, [P(dA.ptr + T * K * 2, dW1.ptr, dT.ptr, dG.ptr, I, N, K, K, K, I, EPI_F32_T)])
+    a64 = bf(A).astype(np.float64)
+    y1 = a64[:T] @ bf(W1).astype(np.float64).T
+    y2 = a64[T:] @ bf(W2).astype(np.float64).T
+    ref_x = x0.astype(np.float64) + gate * np.concatenate([y1, y2])
+    assert tl.rel_l2(dX.get(np.float32, (T + I, N)), ref_x) < 1e-6
+    ref16 = a64 @ bf(W1).astype(np.float64).T
+    assert tl.rel_l2(tl.bf16_to_f32(dO16.get(np.uint16, (T + I, N))), ref16) < 4e-3
+    g = a64 @ bf(Wg[:mlp]).astype(np.float64).T
+    u = a64 @ bf(Wg[mlp:]).astype(np.float64).T
+    ref_sw = g / (1 + np.exp(-g)) * u
+    assert tl.rel_l2(tl.bf16_to_f32(dSw.get(np.uint16, (T + I, mlp))), ref_sw) < 4e-3
+    ref_t = (a64[T:] @ bf(W1).astype(np.float64).T + gate).T
+    assert tl.rel_l2(dT.get(np.float32, (N, I)), ref_t) < 1e-5
+
+
+def attention_ref(q, k, v, scale, valid=None):
+    s = q.astype(np.float64) @ k.astype(np.float64).T * scale
+    if valid is not None:
+        s[:, ~valid] = -np.inf
+    s -= s.max(1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(1, keepdims=True)
+    return p @ v.astype(np.float64)
+
+
+@pytest.mark.parametrize("S,H,batch,mask", [(96, 2, 1, None), (300, 3, 2, None), (1000, 1, 1, (0, 700, 768, 1000)),
+                                            (4608, 2, 1, None)])
+def test_flash_attention(lib, S, H, batch, mask):
+    rng = np.random.default_rng(S + H)
+    hd = H * 128
+    S_pad = (S + 63) // 64 * 64
+    q = rng.standard_normal((batch, S, hd), np.float32)
+    k = rng.standard_normal((batch, S, hd), np.float32)
+    v = rng.standard_normal((batch, S, hd), np.float32)
+    vt = np.zeros((batch, H, 128, S_pad), np.float32)
+    for b in range(batch):
+        for h in range(H):
+            vt[b, h, :, :S] = v[b, :, h * 128:(h + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(q)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    do = tl.Dev(batch * S * hd * 2)
+    lo0, hi0, lo1, hi1 = mask if mask else (0, S, 0, 0)
+    a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, do.ptr, hd, hd, S_pad, hd, S, S, H, batch, S * hd, S * hd,
+                    H * 128 * S_pad, S * hd, 1 / math.sqrt(128), lo0, hi0, lo1, hi1)
+    assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(do.get(np.uint16, (batch, S, hd)))
+    valid = None
+    if mask:
+        idx = np.arange(S)
+        valid = ((idx >= lo0) & (idx < hi0)) | ((idx >= lo1) & (idx < hi1))
+    for b in range(batch):
+        for h in range(H):
+            sl = slice(h * 128, (h + 1) * 128)
+            ref = attention_ref(bf(q[b, :, sl]), bf(k[b, :, sl]), bf(v[b, :, sl]), 1 / math.sqrt(128), valid)
+            assert tl.rel_l2(got[b, :, sl], ref) < 1e-2, (b, h)
+
+
+def test_rownorm_modes(lib):
+    rng = np.random.default_rng(3)
+    rows, cols, split = 50, 3072, 20
+    x = rng.standard_normal((rows, cols), np.float32) * 3 + 1
+    shA, scA, shB, scB, w = (rng.standard_normal(cols).astype(np.float32) * 0.3 for _ in range(5))
+    dx, dout = tl.Dev.of(x), tl.Dev(rows * cols * 4)
+    bufs = [tl.Dev.of(v) for v in (shA, scA, shB, scB, w)]
+    x64 = x.astype(np.float64)
+    mean, var = x64.mean(1, keepdims=True), x64.var(1, keepdims=True)
+    n = (x64 - mean) / np.sqrt(var + 1e-6)
+    for mode, ref in [
+        (0, np.where(np.arange(rows)[:, None] < split, (1 + scA) * n + shA, (1 + scB) * n + shB)),
+        (1, n * np.where(np.arange(rows)[:, None] < split, scA, scB)),
+        (2, x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-6) * w * scA)]:
+        a = tl.NormArgs(dx.ptr, cols, dout.ptr, cols, 0, rows, cols, mode, 1e-6, split, 0, bufs[0].ptr, bufs[1].ptr,
+                        bufs[4].ptr, bufs[2].ptr, bufs[3].ptr, bufs[4].ptr)
+        if mode == 2:
+            a.scaleB = bufs[1].ptr
+        assert lib.iris_hip_rownorm(ctypes.byref(a)) == 0
+        assert tl.rel_l2(dout.get(np.float32, (rows, cols)), ref) < 1e-6, mode
+
+
+def test_qk_prepare(lib):
+    rng = np.random.default_rng(4)
+    S, H, split = 200, 3, 60
+    h = H * 128
+    qkv = rng.standard_normal((S, 3 * h), np.float32)
+    wqA, wkA, wqB, wkB = (1 + 0.1 * rng.standard_normal(128).astype(np.float32) for _ in range(4))
+    ang = rng.uniform(-3, 3, (S, 64)).astype(np.float32)
+    cos = np.repeat(np.cos(ang), 2, 1).astype(np.float32)
+    sin = np.repeat(np.sin(ang), 2, 1).astype(np.float32)
+    S_pad = 256
+    d = dict(qkv=tl.Dev.of(tl.to_bf16(qkv)), q=tl.Dev(S * h * 2), k=tl.Dev(S * h * 2),
+             vt=tl.Dev(H * 128 * S_pad * 2), c=tl.Dev.of(cos), s=tl.Dev.of(sin))
+    ws = [tl.Dev.of(w) for w in (wqA, wkA, wqB, wkB)]
+    d["vt"].put(np.full(H * 128 * S_pad, 0x7FC0, np.uint16))     # poison: padding must be rewritten
+    a = tl.QkPrepArgs(d["qkv"].ptr, 3 * h, h, 2 * h, d["q"].ptr, d["k"].ptr, d["vt"].ptr, S_pad, S, H,
+                      ws[0].ptr, ws[1].ptr, ws[2].ptr, ws[3].ptr, split, d["c"].ptr, d["s"].ptr, 0, 1e-6)
+    assert lib.iris_hip_qk_prepare(ctypes.byref(a)) == 0
+    assert lib.iris_hip_sync() == 0
+    x = bf(qkv).astype(np.float64)
+    for which, col, wa, wb, dev in [(0, 0, wqA, wqB, "q"), (1, h, wkA, wkB, "k")]:
+        got = tl.bf16_to_f32(d[dev].get(np.uint16, (S, h)))
+        for hh in range(H):
+            v = x[:, col + hh * 128: col + (hh + 1) * 128]
+            w = np.where(np.arange(S)[:, None] < split, wa, wb)
+            n = v / np.sqrt((v ** 2).mean(1, keepdims=True) + 1e-6) * w
+            r0 = n[:, 0::2] * cos[:, 0::2] - n[:, 1::2] * sin[:, 0::2]
+            r1 = n[:, 1::2] * cos[:, 0::2] + n[:, 0::2] * sin[:, 0::2]
+            ref = np.stack([r0, r1], 2).reshape(S, 128)
+            assert tl.rel_l2(got[:, hh * 128:(hh + 1) * 128], ref) < 4e-3
+    vt = d["vt"].get(np.uint16, (H, 128, S_pad))
+    vref = tl.to_bf16(qkv[:, 2 * h:]).reshape(S, H, 128).transpose(1, 2, 0)
+    np.testing.assert_array_equal(vt[:, :, :S], vref)
+    assert np.all(vt[:, :, S:] == 0)
+
+
+@pytest.mark.parametrize("N,K,act", [(18432, 3072, 1), (3072, 256, 0), (100, 3840, 1)])
+def test_gemv(lib, N, K, act):
+    rng = np.random.default_rng(N)
+    W = rng.standard_normal((N, K), np.float32) * 0.02
+    x = rng.standard_normal(K).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    dW, dx, db, dy = tl.Dev.of(tl.to_bf16(W)), tl.Dev.of(x), tl.Dev.of(b), tl.Dev(N * 4)
+    assert lib.iris_hip_gemv(dy.ptr, dW.ptr, dx.ptr, db.ptr, N, K, act) == 0
+    xa = x.astype(np.float64)
+    if act:
+        xa = xa / (1 + np.exp(-xa))
+    ref = bf(W).astype(np.float64) @ xa + b
+    assert tl.rel_l2(dy.get(np.float32, (N,)), ref) < 1e-5
+
+
+def test_layout_bit_exact(lib):
+    """NCHW -> token rows and the Z-Image (ph, pw, c) patchify are permutations:
+    bit-exact against numpy (and the round trip against the input)."""
+    rng = np.random.default_rng(5)
+    C, h, w = 128, 24, 40
+    lat = rng.standard_normal((C, h, w), np.float32)
+    dl, dt = tl.Dev.of(lat), tl.Dev(h * w * C * 2)
+    assert lib.iris_hip_nchw_to_tokens(dt.ptr, dl.ptr, C, h * w) == 0
+    np.testing.assert_array_equal(dt.get(np.uint16, (h * w, C)), tl.to_bf16(lat.reshape(C, h * w).T))
+    C, H, W, ps = 16, 12, 20, 2
+    lat = rng.standard_normal((C, H, W), np.float32)
+    dl, dp = tl.Dev.of(lat), tl.Dev((H // ps) * (W // ps) * ps * ps * C * 2)
+    assert lib.iris_hip_patchify(dp.ptr, dl.ptr, C, H, W, ps) == 0
+    want = lat.reshape(C, H // ps, ps, W // ps, ps).transpose(1, 3, 2, 4, 0).reshape(-1, ps * ps * C)
+    np.testing.assert_array_equal(dp.get(np.uint16, want.shape), tl.to_bf16(want))
+    dpf, dback = tl.Dev.of(want.astype(np.float32)), tl.Dev(lat.nbytes)
+    assert lib.iris_hip_unpatchify(dback.ptr, dpf.ptr, C, H, W, ps) == 0
+    np.testing.assert_array_equal(dback.get(np.float32, lat.shape), lat)
+
+
+def test_euler_and_cfg(lib):
+    rng = np.random.default_rng(6)
+    n = 10000
+    z, v, v2 = (rng.standard_normal(n).astype(np.float32) for _ in range(3))
+    dz, dv, dv2 = tl.Dev.of(z), tl.Dev.of(v), tl.Dev.of(v2)
+    assert lib.iris_hip_euler(dz.ptr, dv.ptr, dv2.ptr, 4.0, -0.1, 1.0, n) == 0
+    np.testing.assert_allclose(dz.get(np.float32, (n,)), z + np.float32(-0.1) * (v + 4 * (v2 - v)), rtol=1e-5,
+                               atol=1e-6)
