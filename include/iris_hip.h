@@ -55,7 +55,7 @@ enum {
     IRIS_EPI_F32 = 0,        /* out f32[M,ldo] = acc (+ vec[n] bias)                 */
     IRIS_EPI_BF16 = 1,       /* out bf16[M,ldo] = acc (+ vec[n] bias)                */
     IRIS_EPI_GATED_ADD = 2,  /* out f32[M,ldo] += vec[n] * acc  (vec NULL: += acc)   */
-    IRIS_EPI_SWIGLU = 3,     /* W rows interleaved in 64-row gate/up groups:
+    IRIS_EPI_SWIGLU = 3,     /* W rows interleaved in 32-row gate/up groups:
                                 out bf16[M,ldo] col j = silu(gate_j) * up_j         */
     IRIS_EPI_F32_T = 4       /* out f32[n*ldo + m] = acc (+ vec[n] bias): transposed */
 };

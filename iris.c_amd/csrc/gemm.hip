@@ -6,24 +6,30 @@
  * elementwise passes that follow them (gated_add :136-143, iris_silu_mul
  * iris_kernels.c:626-638, the split/concat copies :3833-3840, :3897-3902).
  *
- * out = A[M,K] . W[N,K]^T. Block tile 256x256x64, 256 threads = 4 waves in a
- * 2x2 arrangement, each wave 128x128 as 4x4 v_mfma_f32_32x32x16_bf16 tiles.
- * A and W tiles are staged through LDS (128 KiB, double buffered) with a
- * 16-byte-chunk XOR swizzle so the column reads of the MFMA operands are free
- * of bank conflicts. Blocks are mapped XCD-major: block b runs on XCD b % 8,
- * so each XCD receives a contiguous range of tiles, ordered in groups of 8
- * M-tiles so concurrently running blocks of one XCD share A and W panels in
- * that XCD's L2.
+ * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
+ * a 2x4 arrangement (2 waves per SIMD, so one wave's LDS reads overlap the
+ * other's MFMAs); each wave owns 128x64 as 4x2 v_mfma_f32_32x32x16_bf16 tiles.
+ * A and W stream through LDS (128 KiB, double buffered, 16-byte-chunk XOR
+ * swizzle so the MFMA operand reads are bank-conflict free). Global loads are
+ * issued two K-steps ahead into two register sets (the K loop is unrolled by
+ * two so the sets are named statically). Blocks are mapped XCD-major: block b
+ * runs on XCD b % 8, so each XCD receives a contiguous range of tiles, ordered
+ * in groups of 8 M-tiles so concurrently running blocks of one XCD share A and
+ * W panels in that XCD's L2.
  */
 #include "iris_internal.h"
 
 #include <string.h>
+#include <type_traits>
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64, NT = 256;
+constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
+constexpr int WAVES_N = 4, TW_M = 128, TW_N = 64, FM = TW_M / 32, FN = TW_N / 32;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
 constexpr size_t SMEM_BYTES = 2 * 2 * TILE_ELEMS * sizeof(uint16_t);
+constexpr int CH = BM * (BK / 8) / NT;              /* 16-byte chunks per operand per thread = 4 */
+constexpr int ROWS_PER = NT / 8;                    /* rows covered by one chunk sweep = 64 */
 constexpr int GROUP_M = 8;
 constexpr int MAXP = 4;
 
@@ -58,14 +64,13 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int lr = lane & 31, lg = lane >> 5;
 
-    /* global -> register staging: 8 chunks of A and 8 of W per thread, through
-     * buffer resources whose range ends at the last valid row, so rows past M
-     * (or N) read as zero without per-row predicates. Offsets are 32-bit bytes
-     * relative to the tile's first row: one VGPR offset per operand plus a
-     * uniform per-chunk row step. */
+    /* global -> register staging through buffer resources whose range ends at
+     * the last valid row, so rows past M (or N) read as zero without
+     * predicates. 32-bit byte offsets relative to the tile's first row: one
+     * VGPR offset per operand plus a uniform per-chunk row step. */
     const int ld_row = tid >> 3, ld_ch = tid & 7;
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
@@ -75,88 +80,98 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)w_base, (short)0, w_rows * pr.ldw * 2, 0x00020000);
     const int a_off = (ld_row * pr.lda + ld_ch * 8) * 2, w_off = (ld_row * pr.ldw + ld_ch * 8) * 2;
-    const int a_step = 32 * pr.lda * 2, w_step = 32 * pr.ldw * 2;
-    uint4 ra[8], rw[8];
+    const int a_step = ROWS_PER * pr.lda * 2, w_step = ROWS_PER * pr.ldw * 2;
+    uint4 ra[2][CH], rw[2][CH];
 
-    auto gload = [&](int kt) {
+    auto gload = [&](int kt, auto SET) {
+        constexpr int s = decltype(SET)::value;
         const int k0 = kt * BK * 2;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off + k0, i * a_step, 0));
-            rw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + k0, i * w_step, 0));
+        for (int i = 0; i < CH; i++) {
+            ra[s][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off + k0, i * a_step, 0));
+            rw[s][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + k0, i * w_step, 0));
         }
     };
-    auto sstore = [&](int buf) {
+    auto sstore = [&](int buf, auto SET) {
+        constexpr int s = decltype(SET)::value;
         uint16_t *As = smem + buf * 2 * TILE_ELEMS;
         uint16_t *Ws = As + TILE_ELEMS;
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            int r = ld_row + 32 * i;
-            *(uint4 *)(As + swz(r, ld_ch)) = ra[i];
-            *(uint4 *)(Ws + swz(r, ld_ch)) = rw[i];
+        for (int i = 0; i < CH; i++) {
+            const int r = ld_row + ROWS_PER * i;
+            *(uint4 *)(As + swz(r, ld_ch)) = ra[s][i];
+            *(uint4 *)(Ws + swz(r, ld_ch)) = rw[s][i];
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
+    const std::integral_constant<int, 0> S0;
+    const std::integral_constant<int, 1> S1;
     const int nk = pr.K / BK;
-    gload(0);
-    sstore(0);
+    gload(0, S0);
+    sstore(0, S0);
+    if (nk > 1) gload(1, S1);
     __syncthreads();
 
-    for (int kt = 0; kt < nk; ++kt) {
+    /* K-step kt computes from LDS buffer kt & 1; loads for kt + 2 go to
+     * register set kt & 1 (free since kt's data is in LDS); kt + 1's set is
+     * stored to the other LDS buffer after the MFMAs. */
+    auto step = [&](int kt, auto SET) {
+        constexpr int s = decltype(SET)::value;
         const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
+        if (kt + 2 < nk) gload(kt + 2, SET);
         const uint16_t *As = smem + cur * 2 * TILE_ELEMS;
         const uint16_t *Ws = As + TILE_ELEMS;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int kk = 0; kk < BK / 16; ++kk) {
             const int ch = kk * 2 + lg;
-            bf16x8 a[4], w[4];
+            bf16x8 a[FM], w[FN];
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++) {
-                int r = wm * 128 + mi * 32 + lr;
-                a[mi] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(As + swz(r, ch)));
-            }
+            for (int mi = 0; mi < FM; mi++)
+                a[mi] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch)));
 #pragma unroll
-            for (int ni = 0; ni < 4; ni++) {
-                int r = wn * 128 + ni * 32 + lr;
-                w[ni] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(Ws + swz(r, ch)));
-            }
+            for (int ni = 0; ni < FN; ni++)
+                w[ni] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch)));
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < FM; mi++)
 #pragma unroll
-                for (int ni = 0; ni < 4; ni++)
+                for (int ni = 0; ni < FN; ni++)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], w[ni], acc[mi][ni], 0, 0, 0);
         }
-        if (kt + 1 < nk) sstore(cur ^ 1);
+        if (kt + 1 < nk) sstore(cur ^ 1, std::integral_constant<int, s ^ 1>());
         __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, S0);
+        if (kt + 1 < nk) step(kt + 1, S1);
     }
 
     /* ---- epilogue: lane holds column lr of each 32x32 tile, rows
      *      (r>>2)*8 + lg*4 + (r&3) ---- */
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
+    const int row0 = m0 + wm * TW_M;
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
     case IRIS_EPI_GATED_ADD: {
 #pragma unroll
-        for (int ni = 0; ni < 4; ni++) {
-            const int col = n0 + wn * 128 + ni * 32 + lr;
+        for (int ni = 0; ni < FN; ni++) {
+            const int col = n0 + wn * TW_N + ni * 32 + lr;
             if (col >= N) continue;
             const float v = vec ? vec[col] : (pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f);
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 128 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     if (row >= M) continue;
                     const size_t o = (size_t)row * ldo + col;
                     const float x = acc[mi][ni][r];
@@ -168,20 +183,17 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         break;
     }
     case IRIS_EPI_SWIGLU: {
-        /* wave column range [n0 + wn*128, +128): tiles 0,1 = gate rows, 2,3 = up rows
-         * of interleaved group (n0 + wn*128) / 128; output columns are the group's 64 */
-        const int half_n = N >> 1;
+        /* the wave's 64 columns are one interleaved group: tile 0 = 32 gate
+         * rows, tile 1 = the matching 32 up rows; output column = group * 32 + lr */
+        const int col = ((n0 + wn * TW_N) >> 1) + lr;
+        if (col < (N >> 1)) {
 #pragma unroll
-        for (int ni = 0; ni < 2; ni++) {
-            const int col = ((n0 + wn * 128) >> 1) + ni * 32 + lr;
-            if (col >= half_n) continue;
-#pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 128 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     if (row >= M) continue;
-                    const float g = acc[mi][ni][r], u = acc[mi][ni + 2][r];
+                    const float g = acc[mi][0][r], u = acc[mi][1][r];
                     ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(g) * u);
                 }
         }
@@ -189,15 +201,15 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
     case IRIS_EPI_F32_T: {
 #pragma unroll
-        for (int ni = 0; ni < 4; ni++) {
-            const int col = n0 + wn * 128 + ni * 32 + lr;
+        for (int ni = 0; ni < FN; ni++) {
+            const int col = n0 + wn * TW_N + ni * 32 + lr;
             if (col >= N) continue;
             const float v = vec ? vec[col] : 0.0f;
 #pragma unroll
-            for (int mi = 0; mi < 4; mi++)
+            for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * 128 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     if (row < M) ((float *)pr.out)[(size_t)col * ldo + row] = acc[mi][ni][r] + v;
                 }
         }
@@ -220,24 +232,26 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     int total = 0;
     for (int i = 0; i < n; i++) {
         const iris_gemm_problem_t &p = probs[i];
-        if (p.M <= 0 || p.N <= 0) { P.tile_start[i] = total; P.tiles_m[i] = P.tiles_n[i] = 0; P.p[i] = p; continue; }
+        P.p[i] = p;
+        P.tile_start[i] = total;
+        if (p.M <= 0 || p.N <= 0) { P.tiles_m[i] = P.tiles_n[i] = 0; continue; }
         if (p.K <= 0 || p.K % BK) return iris_set_error("gemm: K=%d must be a positive multiple of %d", p.K, BK);
         if (p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
             return iris_set_error("gemm: lda=%d ldw=%d must be multiples of 8 and >= K=%d", p.lda, p.ldw, p.K);
         if (((uintptr_t)p.A | (uintptr_t)p.W) & 15) return iris_set_error("gemm: A/W must be 16-byte aligned");
         if (!p.A || !p.W || !p.out) return iris_set_error("gemm: null operand");
-        if (p.epi == IRIS_EPI_SWIGLU && (p.N % 128)) return iris_set_error("gemm: SwiGLU needs N %% 128 == 0");
+        if (p.epi == IRIS_EPI_SWIGLU && (p.N % 64)) return iris_set_error("gemm: SwiGLU needs N %% 64 == 0");
         if (p.epi < 0 || p.epi > IRIS_EPI_F32_T) return iris_set_error("gemm: epilogue %d", p.epi);
-        int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
+        const int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
         if (p.ldo < ldo_need) return iris_set_error("gemm: ldo=%d < %d", p.ldo, ldo_need);
-        P.p[i] = p;
+        /* 32-bit buffer offsets: one tile's rows must span < 2 GiB */
+        if ((long long)BM * p.lda * 2 >= (1LL << 31) || (long long)BN * p.ldw * 2 >= (1LL << 31))
+            return iris_set_error("gemm: leading dimension too large");
         P.tiles_m[i] = (p.M + BM - 1) / BM;
         P.tiles_n[i] = (p.N + BN - 1) / BN;
-        P.tile_start[i] = total;
         total += P.tiles_m[i] * P.tiles_n[i];
     }
-    P.tile_start[n] = total;
-    for (int i = n; i < MAXP; i++) P.tile_start[i] = total;
+    for (int i = n; i <= MAXP; i++) P.tile_start[i] = total;
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;

@@ -29,13 +29,13 @@
 #define MAX_REFS 8
 
 typedef struct {
-    uint16_t *img_qkv, *img_o, *img_ffin, *img_down;    /* ffin rows gate/up interleaved by 64 */
+    uint16_t *img_qkv, *img_o, *img_ffin, *img_down;    /* ffin rows gate/up interleaved by 32 */
     uint16_t *txt_qkv, *txt_o, *txt_ffin, *txt_down;
     float *img_nq, *img_nk, *txt_nq, *txt_nk;
 } dev_double_t;
 
 typedef struct {
-    uint16_t *qkv_mlp;   /* [3h + 2mlp][h]: Q,K,V rows, then gate/up interleaved by 64 */
+    uint16_t *qkv_mlp;   /* [3h + 2mlp][h]: Q,K,V rows, then gate/up interleaved by 32 */
     uint16_t *out;       /* [h][h + mlp] */
     float *nq, *nk;
 } dev_single_t;
@@ -183,16 +183,23 @@ static int upload_rows(source_t *s, const char *name, uint16_t *d, size_t rows, 
 }
 
 /* linear_in rows are [gate (mlp rows) | up (mlp rows)] (:633-640); the device
- * copy interleaves them in groups of 64 rows (gate g, up g, gate g+1, ...) so
- * the SwiGLU epilogue of one 128-column wave tile sees matching gate/up. */
+ * copy interleaves them in groups of SWIGLU_GROUP rows (gate g, up g, gate g+1,
+ * ...) so the SwiGLU epilogue of one 64-column wave tile of the GEMM holds a
+ * gate column and its up column in the same lane. */
+#define SWIGLU_GROUP 32
+static int copy_interleaved(uint16_t *d, const uint16_t *h, size_t mlp, size_t cols) {
+    const size_t G = SWIGLU_GROUP;
+    for (size_t g = 0; g < mlp / G; g++) {
+        if (iris_hip_memcpy_h2d(d + (2 * g) * G * cols, h + g * G * cols, G * cols * 2)) return -1;
+        if (iris_hip_memcpy_h2d(d + (2 * g + 1) * G * cols, h + (mlp + g * G) * cols, G * cols * 2)) return -1;
+    }
+    return iris_hip_sync();
+}
+
 static int upload_interleaved(source_t *s, const char *name, uint16_t *d, size_t mlp, size_t cols) {
     const uint16_t *h = src_get(s, name, 2 * mlp * cols, 0);
     if (!h) return -1;
-    for (size_t g = 0; g < mlp / 64; g++) {
-        if (iris_hip_memcpy_h2d(d + (2 * g) * 64 * cols, h + g * 64 * cols, 64 * cols * 2)) return -1;
-        if (iris_hip_memcpy_h2d(d + (2 * g + 1) * 64 * cols, h + (mlp + g * 64) * cols, 64 * cols * 2)) return -1;
-    }
-    return iris_hip_sync();
+    return copy_interleaved(d, h, mlp, cols);
 }
 
 static float *upload_norm(source_t *s, const char *name, size_t n) {
@@ -265,12 +272,7 @@ static int load_weights(iris_transformer_t *tf, source_t *s) {
         const uint16_t *src = src_get(s, nm, fused * h, 0);
         if (!src) return -1;
         if (iris_hip_memcpy_h2d(b->qkv_mlp, src, 3 * h * h * 2)) return -1;
-        for (size_t g = 0; g < mlp / 64; g++) {
-            if (iris_hip_memcpy_h2d(b->qkv_mlp + (3 * h + 2 * g * 64) * h, src + (3 * h + g * 64) * h, 64 * h * 2)) return -1;
-            if (iris_hip_memcpy_h2d(b->qkv_mlp + (3 * h + (2 * g + 1) * 64) * h, src + (3 * h + mlp + g * 64) * h,
-                                    64 * h * 2)) return -1;
-        }
-        if (iris_hip_sync()) return -1;
+        if (copy_interleaved(b->qkv_mlp + 3 * h * h, src + 3 * h * h, mlp, h)) return -1;
         snprintf(nm, sizeof(nm), "single_transformer_blocks.%d.attn.to_out.weight", i);
         UP(b->out, nm, h * (h + mlp));
         NORM(b->nq, "single_transformer_blocks.%d.attn.norm_q.weight");

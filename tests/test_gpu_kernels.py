@@ -47,7 +47,7 @@ def test_gemm_f32(lib, M, N, K):
 
 
 def test_gemm_epilogues_and_grouping(lib):
-    """bf16 store, gated residual, SwiGLU on 64-row interleaved gate/up, transposed
+    """bf16 store, gated residual, SwiGLU on 32-row interleaved gate/up, transposed
     store, and four problems in one launch with strided operands."""
     rng = np.random.default_rng(1)
     T, I, K, N, mlp = 70, 300, 256, 384, 256
@@ -57,8 +57,8 @@ def test_gemm_epilogues_and_grouping(lib):
     gate = rng.standard_normal(N).astype(np.float32)
     x0 = rng.standard_normal((T + I, N), np.float32)
     Wg = rng.standard_normal((2 * mlp, K), np.float32) * 0.05     # gate rows, then up rows
-    inter = np.concatenate([np.concatenate([Wg[g * 64:(g + 1) * 64], Wg[mlp + g * 64:mlp + (g + 1) * 64]])
-                            for g in range(mlp // 64)])
+    inter = np.concatenate([np.concatenate([Wg[g * 32:(g + 1) * 32], Wg[mlp + g * 32:mlp + (g + 1) * 32]])
+                            for g in range(mlp // 32)])
     dA = tl.Dev.of(tl.to_bf16(A))
     dW1, dW2, dWg = tl.Dev.of(tl.to_bf16(W1)), tl.Dev.of(tl.to_bf16(W2)), tl.Dev.of(tl.to_bf16(inter))
     dX, dG = tl.Dev.of(x0), tl.Dev.of(gate)
