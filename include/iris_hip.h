@@ -96,9 +96,10 @@ typedef struct {
 } iris_norm_args_t;
 int iris_hip_rownorm(const iris_norm_args_t *a);
 
-/* Z-Image gated residual: x[r,:] += gate[:] * RMSNorm(y[r,:]) * w[:]  (gate NULL: 1). */
+/* Z-Image gated residual: x[r,:] += g[:] * RMSNorm(y[r,:]) * w[:] with
+ * g = gate (gate_tanh 0), tanh(gate) (gate_tanh 1), or 1 when gate is NULL. */
 int iris_hip_rms_gated_add(float *d_x, const float *d_y, const float *d_w, const float *d_gate,
-                           int rows, int cols, float eps);
+                           int rows, int cols, float eps, int gate_tanh);
 
 /* ---- attention pieces ---- */
 /* Per (row, head) RMSNorm of Q and K (x w_q / w_k, rows < split use set A) and

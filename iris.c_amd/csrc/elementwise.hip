@@ -89,7 +89,7 @@ __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
 }
 
 __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float *y, const float *w,
-                                                           const float *gate, int cols, float eps) {
+                                                           const float *gate, int cols, float eps, int gate_tanh) {
     __shared__ float red[NT / IRIS_WAVE];
     const int row = blockIdx.x, tid = threadIdx.x, nv = cols >> 2;
     const float *yr = y + (size_t)row * cols;
@@ -114,7 +114,7 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int col = 4 * c + j;
-            const float g = gate ? gate[col] : 1.0f;
+            const float g = gate ? (gate_tanh ? tanhf(gate[col]) : gate[col]) : 1.0f;
             xp[j] += g * (e[j] * inv * w[col]);
         }
         ((float4 *)xr)[c] = xo;
@@ -273,10 +273,11 @@ int iris_hip_rownorm(const iris_norm_args_t *a) {
 }
 
 int iris_hip_rms_gated_add(float *x, const float *y, const float *w, const float *gate, int rows, int cols,
-                           float eps) {
+                           float eps, int gate_tanh) {
     if (rows <= 0) return 0;
     if (cols % 4 || cols > NT * 4 * MAXV) return iris_set_error("rms_gated_add: cols=%d", cols);
-    hipLaunchKernelGGL(rms_gated_add_kernel, dim3(rows), dim3(NT), 0, iris_stream(), x, y, w, gate, cols, eps);
+    hipLaunchKernelGGL(rms_gated_add_kernel, dim3(rows), dim3(NT), 0, iris_stream(), x, y, w, gate, cols, eps,
+                       gate_tanh);
     return iris_launch_check("rms_gated_add_kernel");
 }
 

@@ -187,3 +187,31 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
     }
     return zc;
 }
+
+/* iris_sample_euler_zimage (iris_sample.c:412-536): velocity at timestep
+ * 1 - sigma, z += (sigma_next - sigma) * (-v); one image per call, as the
+ * reference transformer forward handles one latent. */
+float *iris_sample_euler_zimage(void *transformer, float *z, int batch, int channels, int h, int w, int patch_size,
+                                const float *cap_feats, int cap_seq, const float *schedule, int num_steps,
+                                void (*progress_callback)(int, int)) {
+    zi_transformer_t *tf = (zi_transformer_t *)transformer;
+    (void)channels; (void)patch_size;
+    if (num_steps > IRIS_MAX_STEPS) {
+        fprintf(stderr, "iris_sample: num_steps %d exceeds IRIS_MAX_STEPS %d\n", num_steps, IRIS_MAX_STEPS);
+        return NULL;
+    }
+    if (batch != 1) {
+        fprintf(stderr, "iris_sample_euler_zimage: batch %d unsupported (one latent per call)\n", batch);
+        return NULL;
+    }
+    if (zi_prepare(tf, h, w, cap_seq) || zi_upload(tf, z, cap_feats)) return NULL;
+    for (int i = 0; i < num_steps; i++) {
+        if (iris_cancel_requested) return NULL;
+        if (zi_step(tf, schedule[i], schedule[i + 1])) return NULL;
+        if (progress_callback) progress_callback(i + 1, num_steps);
+    }
+    size_t n = (size_t)channels * h * w;
+    float *out = (float *)malloc(n * sizeof(float));
+    if (!out || zi_download_latent(tf, out)) { free(out); return NULL; }
+    return out;
+}

@@ -113,7 +113,9 @@ def hip():
         lib.iris_hip_nchw_to_tokens.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int]
         lib.iris_hip_patchify.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_hip_unpatchify.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
-        lib.iris_hip_rms_gated_add.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        lib.iris_hip_rms_gated_add.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                               ctypes.c_int]
+        lib.iris_hip_fill_rows.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_transformer_load_safetensors.restype = vp
         lib.iris_transformer_create_synthetic.restype = vp
         lib.iris_transformer_create_synthetic.argtypes = [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_float,
@@ -141,6 +143,20 @@ def hip():
         lib.iris_flux_download_velocity.argtypes = [vp, vp]
         lib.iris_flux_double_block_forward.argtypes = [vp, ctypes.c_int]
         lib.iris_flux_single_block_forward.argtypes = [vp, ctypes.c_int]
+        lib.zi_transformer_load_safetensors.argtypes = [ctypes.c_char_p] + [ctypes.c_int] * 7 + [ctypes.c_float, vp]
+        lib.zi_transformer_create_synthetic.argtypes = ([ctypes.c_int] * 7 + [ctypes.c_float, vp, ctypes.c_int,
+                                                        ctypes.c_int, ctypes.c_uint64])
+        lib.zi_transformer_forward.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float, vp, ctypes.c_int]
+        lib.zi_transformer_free.argtypes = [vp]
+        lib.iris_sample_euler_zimage.argtypes = [vp, vp] + [ctypes.c_int] * 5 + [vp, ctypes.c_int, vp, ctypes.c_int,
+                                                                                 vp]
+        lib.zi_device_buffer.restype = vp
+        lib.zi_device_buffer.argtypes = [vp, ctypes.c_char_p]
+        lib.zi_prepare.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.zi_upload.argtypes = [vp, vp, vp]
+        lib.zi_velocity.argtypes = [vp, ctypes.c_float]
+        lib.zi_step.argtypes = [vp, ctypes.c_float, ctypes.c_float]
+        lib.zi_download_latent.argtypes = [vp, vp]
         if lib.iris_hip_init(0) != 0:
             raise RuntimeError("iris_hip_init failed: " + lib.iris_hip_last_error().decode())
         _libs["hip"] = lib

@@ -150,6 +150,24 @@ def test_rownorm_modes(lib):
         assert tl.rel_l2(dout.get(np.float32, (rows, cols)), ref) < 1e-6, mode
 
 
+@pytest.mark.parametrize("gate_mode", ["none", "plain", "tanh"])
+def test_rms_gated_add(lib, gate_mode):
+    """x += g * RMSNorm(y) * w with g = 1, gate or tanh(gate) (zimage :818-836)."""
+    rng = np.random.default_rng(5)
+    rows, cols = 70, 3840
+    x = rng.standard_normal((rows, cols), np.float32)
+    y = rng.standard_normal((rows, cols), np.float32) * 4 + 0.5
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    gate = rng.standard_normal(cols).astype(np.float32) * 2
+    dx, dy, dw, dg = tl.Dev.of(x), tl.Dev.of(y), tl.Dev.of(w), tl.Dev.of(gate)
+    gp = None if gate_mode == "none" else dg.ptr
+    assert lib.iris_hip_rms_gated_add(dx.ptr, dy.ptr, dw.ptr, gp, rows, cols, 1e-5, int(gate_mode == "tanh")) == 0
+    y64 = y.astype(np.float64)
+    g = {"none": 1.0, "plain": gate.astype(np.float64), "tanh": np.tanh(gate.astype(np.float64))}[gate_mode]
+    want = x + g * (y64 / np.sqrt((y64 ** 2).mean(1, keepdims=True) + 1e-5) * w)
+    assert tl.rel_l2(dx.get(np.float32, (rows, cols)), want) < 1e-6
+
+
 def test_qk_prepare(lib):
     rng = np.random.default_rng(4)
     S, H, split = 200, 3, 60
