@@ -25,6 +25,7 @@
 
 #include <stddef.h>
 #include <stdint.h>
+#include <stdio.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -56,6 +57,25 @@ int iris_transformer_hidden_size(iris_transformer_t *tf);
 int iris_transformer_num_double_layers(iris_transformer_t *tf);
 int iris_transformer_num_single_layers(iris_transformer_t *tf);
 int iris_transformer_text_dim(iris_transformer_t *tf);
+
+/* Adapter setters of the reference (iris_transformer_flux.c:5131-5201; LoRA
+ * state and IP-Adapter passed as opaque pointers, same ABI). Ownership passes
+ * to the transformer as in the reference. The HIP forward applies no adapter:
+ * while LoRA, IP-Adapter, an unskipped CSD delta, or SREF bands/strength other
+ * than off are attached, every forward returns NULL with a message. */
+void iris_transformer_set_lora(iris_transformer_t *tf, void *lora);
+void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta);
+void iris_transformer_set_csd_skip(iris_transformer_t *tf, int skip);
+void iris_transformer_set_sref_bands(iris_transformer_t *tf, float shf, float slf);
+void iris_transformer_set_sref_strength(iris_transformer_t *tf, float gamma);
+int iris_transformer_set_ip_adapter(iris_transformer_t *tf, void *ip, float *ip_embeds);
+int iris_transformer_set_ip_schedule(iris_transformer_t *tf, const char *spec);
+void iris_transformer_set_ip_step(iris_transformer_t *tf, int step, int num_steps);
+/* legacy single-file loader (:4845): returns NULL (safetensors directories only) */
+iris_transformer_t *iris_transformer_load(FILE *f);
+/* BLAS profile counters of the CPU path (:55-80): no-ops here */
+void iris_print_blas_profile(void);
+void iris_reset_blas_profile(void);
 
 /* ---- reference entry points (Z-Image) ---- */
 zi_transformer_t *zi_transformer_load_safetensors(const char *model_dir, int dim, int n_heads, int n_layers,

@@ -73,6 +73,11 @@ struct iris_transformer {
     dev_double_t *dbl;
     dev_single_t *sgl;
     work_t w;
+    /* adapters set through the reference's setters (owned, not applied) */
+    void *lora, *ip, *ip_embeds;
+    float *csd_delta;
+    int csd_skip;
+    float sref_shf, sref_slf, sref_strength;
 };
 
 /* ------------------------------------------------------------------ config */
@@ -284,6 +289,8 @@ static int load_weights(iris_transformer_t *tf, source_t *s) {
 }
 
 static void work_free(work_t *w);
+static void release_adapters(iris_transformer_t *tf);
+static int adapter_active(const iris_transformer_t *tf);
 
 void iris_transformer_free(iris_transformer_t *tf) {
     if (!tf) return;
@@ -303,10 +310,12 @@ void iris_transformer_free(iris_transformer_t *tf) {
     }
     free(tf->dbl);
     free(tf->sgl);
+    release_adapters(tf);
     free(tf);
 }
 
 static iris_transformer_t *finish_load(iris_transformer_t *tf, source_t *s) {
+    tf->sref_shf = tf->sref_slf = tf->sref_strength = 1.0f;
     int rc = load_weights(tf, s);
     free(s->stage);
     if (rc) {
@@ -687,6 +696,7 @@ int iris_flux_upload(iris_transformer_t *tf, const float *latent, const iris_ref
 int iris_flux_velocity(iris_transformer_t *tf, float t) {
     work_t *w = &tf->w;
     if (!w->valid) return -1;
+    if (adapter_active(tf)) return -1;
     /* get_timestep_embedding(t * 1000), :3967 */
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
@@ -730,6 +740,99 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
     if (!strcmp(name, "txt")) return w->txtf;
     return NULL;
 }
+
+/* ------------------------------------------------------------- adapters */
+
+/* The reference's adapter setters (iris_transformer_flux.c:5131-5201), kept
+ * so a caller links unchanged. The HIP forward implements none of the
+ * adapters: while one is attached (LoRA, CSD style delta, SREF bands or
+ * strength other than off, IP-Adapter) every forward fails with a message
+ * instead of silently ignoring it. Ownership follows the reference: the
+ * transformer takes what it is given and releases it on replacement or free
+ * through the reference's own release functions when those are linked in. */
+void lora_free(void *lora) __attribute__((weak));
+void iris_ip_adapter_free(void *ip) __attribute__((weak));
+int iris_ip_adapter_set_schedule(void *ip, const char *spec) __attribute__((weak));
+void iris_ip_adapter_set_step(void *ip, int step, int num_steps) __attribute__((weak));
+
+static void release_adapters(iris_transformer_t *tf) {
+    if (tf->lora && lora_free) lora_free(tf->lora);
+    if (tf->ip && iris_ip_adapter_free) iris_ip_adapter_free(tf->ip);
+    free(tf->ip_embeds);
+    free(tf->csd_delta);
+    tf->lora = tf->ip = tf->ip_embeds = NULL;
+    tf->csd_delta = NULL;
+}
+
+static int adapter_active(const iris_transformer_t *tf) {
+    const char *what = tf->lora ? "LoRA" : tf->ip ? "IP-Adapter"
+                     : (tf->csd_delta && !tf->csd_skip) ? "CSD style delta"
+                     : (tf->sref_shf != 1.0f || tf->sref_slf != 1.0f) ? "SREF RoPE bands"
+                     : tf->sref_strength != 1.0f ? "SREF strength" : NULL;
+    if (what) fprintf(stderr, "iris_hip: %s is attached; the HIP denoiser does not apply adapters\n", what);
+    return what != NULL;
+}
+
+void iris_transformer_set_lora(iris_transformer_t *tf, void *lora) {
+    if (!tf) return;
+    if (tf->lora && tf->lora != lora && lora_free) lora_free(tf->lora);
+    tf->lora = lora;
+}
+
+void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta) {
+    if (!tf) return;
+    if (tf->csd_delta != delta) free(tf->csd_delta);
+    tf->csd_delta = delta;
+}
+
+void iris_transformer_set_csd_skip(iris_transformer_t *tf, int skip) {
+    if (tf) tf->csd_skip = skip;
+}
+
+void iris_transformer_set_sref_bands(iris_transformer_t *tf, float shf, float slf) {
+    if (!tf) return;
+    tf->sref_shf = (shf >= 0.0f && shf <= 1.0f) ? shf : 1.0f;
+    tf->sref_slf = (slf >= 1.0f) ? slf : 1.0f;
+}
+
+void iris_transformer_set_sref_strength(iris_transformer_t *tf, float gamma) {
+    if (!tf) return;
+    if (!(gamma > 0.0f) || gamma == 1.0f) { tf->sref_strength = 1.0f; return; }
+    tf->sref_strength = gamma < 1e-3f ? 1e-3f : gamma > 8.0f ? 8.0f : gamma;
+}
+
+int iris_transformer_set_ip_adapter(iris_transformer_t *tf, void *ip, float *ip_embeds) {
+    if (!tf) return -1;
+    if (tf->ip && iris_ip_adapter_free) iris_ip_adapter_free(tf->ip);
+    free(tf->ip_embeds);
+    tf->ip = ip;
+    tf->ip_embeds = ip ? ip_embeds : NULL;
+    if (!ip) free(ip_embeds);
+    return 0;
+}
+
+int iris_transformer_set_ip_schedule(iris_transformer_t *tf, const char *spec) {
+    if (!tf || !tf->ip || !iris_ip_adapter_set_schedule) return -1;
+    return iris_ip_adapter_set_schedule(tf->ip, spec);
+}
+
+void iris_transformer_set_ip_step(iris_transformer_t *tf, int step, int num_steps) {
+    if (tf && tf->ip && iris_ip_adapter_set_step) iris_ip_adapter_set_step(tf->ip, step, num_steps);
+}
+
+/* Legacy single-file loader (iris_transformer_flux.c:4845): the HIP build
+ * reads safetensors directories only. */
+iris_transformer_t *iris_transformer_load(FILE *f) {
+    (void)f;
+    fprintf(stderr, "iris_transformer_load: the HIP build loads safetensors directories "
+                    "(iris_transformer_load_safetensors)\n");
+    return NULL;
+}
+
+/* BLAS profile counters of the reference CPU path (:55-80); the HIP path is
+ * profiled with rocprofv3 instead. */
+void iris_print_blas_profile(void) {}
+void iris_reset_blas_profile(void) {}
 
 /* ------------------------------------------------------ reference entries */
 

@@ -9,6 +9,30 @@
  * linears through cblas_sgemm, per-head sgemm/softmax/sgemm attention) with the
  * same operation order. Each function cites the reference file:line it follows.
  * sgemm is OpenBLAS when orc_set_blas() bound one, else a plain loop nest.
+ *
+ * How each part is pinned (tests/test_oracle.py, fixtures in tests/golden/
+ * written by the reference compiled from its own sources, oracle/Makefile ref):
+ *   RoPE tables (Flux img/txt/T-offsets, Z-Image axes), timestep sinusoid,
+ *   patchify, noise                     bit-exact (SHA-256) vs the reference;
+ *   fast_expf                           reference grid, rel 1e-5, plus the
+ *                                       closed-form bound |e/exp - 1| < 1e-5;
+ *   schedules                           the reference's own golden arrays
+ *                                       (debug/test_zimage_scheduler.c:71-79)
+ *                                       and reference outputs, rel 5e-6;
+ *   Flux t-embed, modulation, double and single block, forward, multi-ref
+ *   forward, 2-step sampler, 4B-shaped single block
+ *                                       reference outputs, rel-L2 1e-5..1e-4;
+ *   Z-Image t-embed, blocks, forward    reference outputs with the in-place
+ *                                       output projection emulated (alias 1),
+ *                                       rel-L2 1e-5..1e-4;
+ *   Z-Image out-of-place forward (alias 0)
+ *                                       reference outputs on upper-triangular
+ *                                       output projections, where in-place and
+ *                                       out-of-place coincide, rel-L2 1e-4;
+ *   softmax, RMSNorm, LayerNorm, SiLU   textbook known answers.
+ * Nothing on the path is "parity unpinned"; whether the reference C matches
+ * the upstream Python models is outside this oracle (the reference's own
+ * parity tests for that are skipped scaffolds).
  */
 #ifndef IRIS_ORACLE_H
 #define IRIS_ORACLE_H

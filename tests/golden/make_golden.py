@@ -26,6 +26,7 @@ FLUX_TINY = {"heads": 2, "n_double": 2, "n_single": 2, "text_dim": 256, "latent_
              "mlp_ratio": 3.0, "theta": 2000.0, "seed": 1234}
 ZI_TINY = {"dim": 256, "heads": 2, "layers": 2, "refiners": 1, "cap_dim": 128, "in_ch": 16, "ps": 2,
            "theta": 256.0, "axes": [32, 48, 48], "ffn": 768, "t_mid": 256, "seed": 4321}
+ZI_TRIU_CASES = [(12, 20, 0.4, (31, 34)), (16, 32, 0.9, (35, 36)), (8, 7, 0.05, (37, 38))]
 C1 = {"heads": 24, "n_double": 1, "n_single": 1, "text_dim": 7680, "latent_ch": 128, "mlp_ratio": 3.0,
       "theta": 2000.0, "seed": 777}
 
@@ -158,6 +159,25 @@ def zimage_goldens(r, d, res, hashes):
     r.zi_transformer_free(tf)
 
 
+def zimage_triu_goldens(r, d, res):
+    """Same tiny model with upper-triangular attention output projections: the
+    reference CPU path's in-place projection then equals the out-of-place one,
+    so these outputs are the model's out-of-place forward."""
+    cfg = ZI_TINY
+    tl.write_zimage_model(d, cfg, cfg["seed"], triu_out=True)
+    axes = (ctypes.c_int * 3)(*cfg["axes"])
+    tf = r.zi_transformer_load_safetensors(d.encode(), cfg["dim"], cfg["heads"], cfg["layers"], cfg["refiners"],
+                                           cfg["cap_dim"], cfg["in_ch"], cfg["ps"], cfg["theta"], axes)
+    assert tf, "reference failed to load the synthetic Z-Image model"
+    tf = ctypes.c_void_p(tf)
+    for hw, cap_len, t, seeds in ZI_TRIU_CASES:
+        lat = tl.synth_f32((16, hw, hw), seeds[0])
+        cap = tl.synth_f32((cap_len, 128), seeds[1])
+        p = r.zi_transformer_forward(tf, tl.fptr(lat), hw, hw, ctypes.c_float(t), tl.fptr(cap), cap_len)
+        res[f"zi_triu_fwd_{hw}x{hw}_cap{cap_len}"] = tl.take_f32(r, p, 16 * hw * hw)
+    r.zi_transformer_free(tf)
+
+
 def fast_expf_golden(r, res):
     r.ref_fast_expf.restype = ctypes.c_float
     xs = np.linspace(-90.0, 90.0, 2001).astype(np.float32)
@@ -210,6 +230,8 @@ def main():
         flux_goldens(r, d, res)
     with tempfile.TemporaryDirectory() as d:
         zimage_goldens(r, d, res, hashes)
+    with tempfile.TemporaryDirectory() as d:
+        zimage_triu_goldens(r, d, res)
     sampler_goldens(r, res, hashes)
     fast_expf_golden(r, res)
     np.savez_compressed(os.path.join(tl.GOLDEN, "reference_small.npz"), **res)
@@ -221,7 +243,7 @@ def main():
     manifest = {
         "generator": "tests/golden/make_golden.py",
         "reference_build": "oracle/Makefile `ref`: gcc -O3 -march=native -ffast-math -DGENERIC_BUILD",
-        "flux_tiny": FLUX_TINY, "zimage_tiny": ZI_TINY, "c1": C1,
+        "flux_tiny": FLUX_TINY, "zimage_tiny": ZI_TINY, "zimage_triu_cases": ZI_TRIU_CASES, "c1": C1,
         "inputs": "iris_synth f32 N(0,1) by seed (see make_golden.py); weights bf16 via iris_synth_seed(name)",
         "sha256": hashes,
     }

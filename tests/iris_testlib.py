@@ -386,9 +386,19 @@ def zimage_tensor_list(cfg):
     return t
 
 
-def write_zimage_model(d, cfg, seed):
+def write_zimage_model(d, cfg, seed, triu_out=False):
+    """triu_out: every attention output projection W[n][k] is zeroed for k < n.
+    Then an in-place product row <- row . W^T taken column by column in
+    increasing n reads only inputs it has not yet overwritten, so it equals
+    the out-of-place product (pins the out-of-place oracle on the reference's
+    in-place CPU path)."""
     os.makedirs(os.path.join(d, "transformer"), exist_ok=True)
-    tensors = [(n, synth_bf16(n, s, seed, m, sd)) for n, s, m, sd in zimage_tensor_list(cfg)]
+    tensors = []
+    for n, s, m, sd in zimage_tensor_list(cfg):
+        a = synth_bf16(n, s, seed, m, sd)
+        if triu_out and n.endswith("attention.to_out.0.weight"):
+            a = np.triu(a)
+        tensors.append((n, a))
     write_safetensors(os.path.join(d, "transformer", "diffusion_pytorch_model.safetensors"), tensors)
 
 

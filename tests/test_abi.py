@@ -1,0 +1,61 @@
+"""The C-ABI boundary without a GPU: libiris_hip.so loads and exports every
+function include/*.h declares (no compute calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import iris_testlib as tl
+
+INCLUDE = os.path.join(tl.ROOT, "include")
+
+
+def declared_functions():
+    names = {}
+    for fn in sorted(os.listdir(INCLUDE)):
+        if not fn.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, fn)).read()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        text = re.sub(r"^\s*#[^\n]*", " ", text, flags=re.M)
+        # statements at file scope: the C++ linkage wrapper, then struct/enum bodies removed
+        text = text.replace('extern "C" {', " ")
+        text = re.sub(r"\{[^{}]*\}", " ", text)
+        text = text.replace("}", " ")
+        for stmt in text.split(";"):
+            s = " ".join(stmt.split())
+            if not s or s.startswith("typedef") or s.startswith("extern \"C\""):
+                continue
+            m = re.match(r"^(?:extern\s+)?[A-Za-z_][\w\s\*]*?[\s\*](\w+)\s*\((.*)\)$", s)
+            if m:
+                names.setdefault(fn, []).append(m.group(1))
+    return names
+
+
+DECLS = declared_functions()
+
+
+def test_headers_parsed():
+    assert "iris_hip.h" in DECLS and "iris_transformer.h" in DECLS and "iris_sample.h" in DECLS
+    assert "iris_hip_gemm" in DECLS["iris_hip.h"]
+    assert "iris_transformer_forward" in DECLS["iris_transformer.h"]
+    assert "zi_transformer_forward" in DECLS["iris_transformer.h"]
+    assert sum(len(v) for v in DECLS.values()) > 60
+
+
+@pytest.mark.parametrize("header", sorted(DECLS))
+def test_library_exports_declared(header):
+    if not os.path.exists(tl.HIP_SO):
+        pytest.fail(f"{tl.HIP_SO} is not built")
+    lib = ctypes.CDLL(tl.HIP_SO)          # loads without a GPU; nothing is called
+    missing = [n for n in DECLS[header] if not hasattr(lib, n)]
+    assert not missing, f"{header}: not exported: {missing}"
+
+
+def test_no_oracle_symbols_in_product():
+    """The product library does not carry the oracle's functions."""
+    lib = ctypes.CDLL(tl.HIP_SO)
+    for n in ("orc_flux_forward", "orc_zi_forward", "orc_set_blas", "orc_linear"):
+        assert not hasattr(lib, n), n

@@ -277,3 +277,26 @@ def test_4b_forward_reduced_depth(lib, orc):
     lib.iris_transformer_free(tf)
     orc.orc_flux_free(m)
     assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+
+
+def test_adapters_fail_loudly(lib, tiny):
+    """Adapter setters link and take ownership; an attached adapter makes the
+    forward fail (the HIP denoiser applies none) instead of being ignored."""
+    vp = ctypes.c_void_p
+    libc = ctypes.CDLL(None)
+    libc.malloc.restype = vp
+    lib.iris_transformer_set_csd_delta.argtypes = [vp, vp]
+    lib.iris_transformer_set_sref_strength.argtypes = [vp, ctypes.c_float]
+    lib.iris_transformer_set_sref_bands.argtypes = [vp, ctypes.c_float, ctypes.c_float]
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    lib.iris_transformer_set_sref_strength(tiny, 1.0)          # off
+    lib.iris_transformer_set_sref_bands(tiny, 1.0, 1.0)        # off
+    base = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+    lib.iris_transformer_set_csd_delta(tiny, libc.malloc(256 * 4))
+    assert not lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8))
+    lib.iris_transformer_set_csd_delta(tiny, None)
+    lib.iris_transformer_set_sref_strength(tiny, 0.5)
+    assert not lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8))
+    lib.iris_transformer_set_sref_strength(tiny, 1.0)
+    again = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+    np.testing.assert_array_equal(base, again)

@@ -87,6 +87,26 @@ def test_forward_vs_oracle(lib, orc, models, hw, cap_len, t, seeds):
     assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
 
 
+@pytest.mark.parametrize("case", range(3))
+def test_forward_vs_reference_goldens(lib, case):
+    """Against the reference's own outputs on a model whose output projections
+    are upper triangular (there the reference CPU path's in-place projection
+    equals the out-of-place product)."""
+    hw, cap_len, t, seeds = MAN["zimage_triu_cases"][case]
+    G = np.load(os.path.join(tl.GOLDEN, "reference_small.npz"), allow_pickle=False)
+    with tempfile.TemporaryDirectory() as d:
+        tl.write_zimage_model(d, TINY, TINY["seed"], triu_out=True)
+        tf = lib.zi_transformer_load_safetensors(d.encode(), *tiny_args())
+    assert tf, lib.iris_hip_last_error()
+    tf = ctypes.c_void_p(tf)
+    lat = tl.synth_f32((16, hw, hw), seeds[0])
+    cap = tl.synth_f32((cap_len, TINY["cap_dim"]), seeds[1])
+    got = forward(lib, tf, lat, hw, t, cap)
+    lib.zi_transformer_free(tf)
+    want = G[f"zi_triu_fwd_{hw}x{hw}_cap{cap_len}"]
+    assert tl.rel_l2(got, want) < 1e-2 and tl.cosine(got, want) > 0.999
+
+
 def test_rope_tables_resident_bit_exact(lib, orc, models):
     """Per-row tables of the unified [image | caption] sequence == the oracle's
     per-axis tables gathered at the reference's position ids."""

@@ -324,6 +324,48 @@ def test_zimage_forward(lib, zi, hw, cap_len, t, key, seeds):
     assert tl.rel_l2(out, G[key]) < 1e-4
 
 
+@pytest.fixture(scope="module")
+def zi_triu(lib):
+    cfg = MAN["zimage_tiny"]
+    axes = (ctypes.c_int * 3)(*cfg["axes"])
+    with tempfile.TemporaryDirectory() as d:
+        tl.write_zimage_model(d, cfg, cfg["seed"], triu_out=True)
+        m = lib.orc_zi_load(d.encode(), cfg["dim"], cfg["heads"], cfg["layers"], cfg["refiners"], cfg["cap_dim"],
+                            cfg["in_ch"], cfg["ps"], cfg["theta"], axes)
+    assert m
+    yield ctypes.c_void_p(m)
+    lib.orc_zi_set_reference_aliasing(0)
+    lib.orc_zi_free(ctypes.c_void_p(m))
+
+
+@pytest.mark.parametrize("case", range(3))
+@pytest.mark.parametrize("alias", [0, 1])
+def test_zimage_out_of_place_forward_pinned(lib, zi_triu, case, alias):
+    """With upper-triangular output projections the reference CPU path's
+    in-place projection equals the out-of-place one, so its outputs pin the
+    oracle's out-of-place forward (the path the HIP build computes)."""
+    hw, cap_len, t, seeds = MAN["zimage_triu_cases"][case]
+    lib.orc_zi_set_reference_aliasing(alias)
+    lat = tl.synth_f32((16, hw, hw), seeds[0])
+    cap = tl.synth_f32((cap_len, 128), seeds[1])
+    out = tl.take_f32(lib, lib.orc_zi_forward(zi_triu, tl.fptr(lat), hw, hw, F(t), tl.fptr(cap), cap_len),
+                      16 * hw * hw)
+    lib.orc_zi_set_reference_aliasing(0)
+    assert tl.rel_l2(out, G[f"zi_triu_fwd_{hw}x{hw}_cap{cap_len}"]) < 1e-4
+
+
+def test_zimage_reference_cpu_aliasing_is_visible(lib, zi):
+    """With full output projections the in-place product changes the result:
+    the reference CPU outputs differ from the out-of-place forward by far more
+    than rounding (why the HIP build is checked against the out-of-place oracle)."""
+    lat = tl.synth_f32((16, 12, 12), 31)
+    cap = tl.synth_f32((20, 128), 34)
+    lib.orc_zi_set_reference_aliasing(0)
+    out = tl.take_f32(lib, lib.orc_zi_forward(zi, tl.fptr(lat), 12, 12, F(0.4), tl.fptr(cap), 20), 16 * 144)
+    lib.orc_zi_set_reference_aliasing(1)
+    assert tl.rel_l2(out, G["zi_fwd_12x12_cap20"]) > 5e-2
+
+
 C1_PATH = os.path.join(tl.GOLDEN, "reference_c1_single_block.npz")
 
 
