@@ -96,14 +96,22 @@ def attention_ref(q, k, v, scale, valid=None):
     return p @ v.astype(np.float64)
 
 
-@pytest.mark.parametrize("S,H,batch,mask", [(96, 2, 1, None), (300, 3, 2, None), (1000, 1, 1, (0, 700, 768, 1000)),
-                                            (4608, 2, 1, None)])
-def test_flash_attention(lib, S, H, batch, mask):
+@pytest.mark.parametrize("S,H,batch,mask,qscale,kramp", [
+    (96, 2, 1, None, 1.0, False), (300, 3, 2, None, 1.0, False), (1000, 1, 1, (0, 700, 768, 1000), 1.0, False),
+    (4608, 2, 1, None, 1.0, False),
+    # sharp softmax (logits ~ N(0, 36)) and key norms growing along the sequence,
+    # so the running max keeps rising and the lazy rescale fires many times
+    (1000, 2, 1, None, 6.0, False), (2048, 2, 1, None, 3.0, True),
+    # leading tiles fully masked, ragged end
+    (900, 1, 1, (130, 900, 0, 0), 2.0, True)])
+def test_flash_attention(lib, S, H, batch, mask, qscale, kramp):
     rng = np.random.default_rng(S + H)
     hd = H * 128
     S_pad = (S + 63) // 64 * 64
-    q = rng.standard_normal((batch, S, hd), np.float32)
+    q = rng.standard_normal((batch, S, hd), np.float32) * np.float32(qscale)
     k = rng.standard_normal((batch, S, hd), np.float32)
+    if kramp:
+        k *= np.linspace(0.2, 2.0, S, dtype=np.float32)[None, :, None]
     v = rng.standard_normal((batch, S, hd), np.float32)
     vt = np.zeros((batch, H, 128, S_pad), np.float32)
     for b in range(batch):
