@@ -7,25 +7,35 @@
  * iris_kernels.c:626-638, the split/concat copies :3833-3840, :3897-3902).
  *
  * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
- * a 2x4 arrangement (2 waves per SIMD, so one wave's LDS reads overlap the
- * other's MFMAs); each wave owns 128x64 as 4x2 v_mfma_f32_32x32x16_bf16 tiles.
- * A and W stream through LDS (128 KiB, double buffered, 16-byte-chunk XOR
- * swizzle so the MFMA operand reads are bank-conflict free). Global loads are
- * issued two K-steps ahead into two register sets (the K loop is unrolled by
- * two so the sets are named statically). Blocks are mapped XCD-major: block b
- * runs on XCD b % 8, so each XCD receives a contiguous range of tiles, ordered
- * in groups of 8 M-tiles so concurrently running blocks of one XCD share A and
- * W panels in that XCD's L2.
+ * a 4x2 arrangement (2 waves per SIMD); each wave owns 64x128 as 2x4
+ * v_mfma_f32_32x32x16_bf16 tiles and reads the next 16-wide K slice's operand
+ * fragments from LDS while the current slice's MFMAs run.
+ *
+ * A and W stream through two 64 KiB LDS stages. Each thread stages 4 16-byte
+ * chunks per operand in registers: in K-step t, after the first half of the
+ * MFMAs, it writes the chunks of tile t+1 (loaded during step t-1) into the
+ * stage that step t-1 read, then reloads the registers with tile t+2, so
+ * global latency is covered by a whole K-step and the LDS writes overlap
+ * matrix work. LDS serves a 16-byte-per-lane read 16 lanes at a time over 64
+ * banks: a group reads rows r..r+15 at one logical 16-byte chunk, and XOR with
+ * (row / 2) mod 8 puts those rows on 16 distinct (row parity, chunk) bank
+ * groups.
+ *
+ * Loads use buffer resources whose range ends at the operand's last valid row,
+ * so rows past M (or N) read as zero without predicates. Blocks are mapped
+ * XCD-major: block b runs on XCD b % 8 and takes a contiguous range of tiles,
+ * ordered in groups of 8 M-tiles, so concurrently running blocks of one XCD
+ * share A and W panels in that XCD's L2.
  */
 #include "iris_internal.h"
 
 #include <string.h>
-#include <type_traits>
 
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
-constexpr int WAVES_N = 4, TW_M = 128, TW_N = 64, FM = TW_M / 32, FN = TW_N / 32;
+constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M, TW_N = BN / WAVES_N;
+constexpr int FM = TW_M / 32, FN = TW_N / 32;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
 constexpr size_t SMEM_BYTES = 2 * 2 * TILE_ELEMS * sizeof(uint16_t);
 constexpr int CH = BM * (BK / 8) / NT;              /* 16-byte chunks per operand per thread = 4 */
@@ -40,7 +50,7 @@ struct GemmParams {
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in a tile */
-    return row * BK + ((chunk ^ (row & 7)) << 3);
+    return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
@@ -67,10 +77,8 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int lr = lane & 31, lg = lane >> 5;
 
-    /* global -> register staging through buffer resources whose range ends at
-     * the last valid row, so rows past M (or N) read as zero without
-     * predicates. 32-bit byte offsets relative to the tile's first row: one
-     * VGPR offset per operand plus a uniform per-chunk row step. */
+    /* 32-bit byte offsets relative to the tile's first row: one VGPR offset
+     * per operand plus a uniform per-chunk row step */
     const int ld_row = tid >> 3, ld_ch = tid & 7;
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
@@ -81,26 +89,24 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         (void *)w_base, (short)0, w_rows * pr.ldw * 2, 0x00020000);
     const int a_off = (ld_row * pr.lda + ld_ch * 8) * 2, w_off = (ld_row * pr.ldw + ld_ch * 8) * 2;
     const int a_step = ROWS_PER * pr.lda * 2, w_step = ROWS_PER * pr.ldw * 2;
-    uint4 ra[2][CH], rw[2][CH];
+    uint4 ra[CH], rw[CH];
 
-    auto gload = [&](int kt, auto SET) {
-        constexpr int s = decltype(SET)::value;
+    auto gload = [&](int kt) {
         const int k0 = kt * BK * 2;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
-            ra[s][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off + k0, i * a_step, 0));
-            rw[s][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + k0, i * w_step, 0));
+            ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off + k0, i * a_step, 0));
+            rw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + k0, i * w_step, 0));
         }
     };
-    auto sstore = [&](int buf, auto SET) {
-        constexpr int s = decltype(SET)::value;
+    auto sstore = [&](int buf) {
         uint16_t *As = smem + buf * 2 * TILE_ELEMS;
         uint16_t *Ws = As + TILE_ELEMS;
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const int r = ld_row + ROWS_PER * i;
-            *(uint4 *)(As + swz(r, ld_ch)) = ra[s][i];
-            *(uint4 *)(Ws + swz(r, ld_ch)) = rw[s][i];
+            *(uint4 *)(As + swz(r, ld_ch)) = ra[i];
+            *(uint4 *)(Ws + swz(r, ld_ch)) = rw[i];
         }
     };
 
@@ -112,45 +118,41 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-    const std::integral_constant<int, 0> S0;
-    const std::integral_constant<int, 1> S1;
     const int nk = pr.K / BK;
-    gload(0, S0);
-    sstore(0, S0);
-    if (nk > 1) gload(1, S1);
+    gload(0);
+    sstore(0);
+    if (nk > 1) gload(1);
     __syncthreads();
-
-    /* K-step kt computes from LDS buffer kt & 1; loads for kt + 2 go to
-     * register set kt & 1 (free since kt's data is in LDS); kt + 1's set is
-     * stored to the other LDS buffer after the MFMAs. */
-    auto step = [&](int kt, auto SET) {
-        constexpr int s = decltype(SET)::value;
-        const int cur = kt & 1;
-        if (kt + 2 < nk) gload(kt + 2, SET);
-        const uint16_t *As = smem + cur * 2 * TILE_ELEMS;
+    for (int kt = 0; kt < nk; ++kt) {
+        const uint16_t *As = smem + (kt & 1) * 2 * TILE_ELEMS;
         const uint16_t *Ws = As + TILE_ELEMS;
-#pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
+        bf16x8 a[2][FM], w[2][FN];
+        auto frag = [&](int kk, int buf) {
             const int ch = kk * 2 + lg;
-            bf16x8 a[FM], w[FN];
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
-                a[mi] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch)));
+                a[buf][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch));
 #pragma unroll
             for (int ni = 0; ni < FN; ni++)
-                w[ni] = __builtin_bit_cast(bf16x8, *(const u16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch)));
+                w[buf][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch));
+        };
+        frag(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            if (kk + 1 < BK / 16) frag(kk + 1, (kk + 1) & 1);
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int ni = 0; ni < FN; ni++)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[mi], w[ni], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][mi], w[kk & 1][ni],
+                                                                          acc[mi][ni], 0, 0, 0);
+            if (kk == 1) {
+                /* the stage read in step kt-1 is free (barrier); tile kt+1 goes there */
+                if (kt + 1 < nk) sstore((kt + 1) & 1);
+                if (kt + 2 < nk) gload(kt + 2);
+            }
         }
-        if (kt + 1 < nk) sstore(cur ^ 1, std::integral_constant<int, s ^ 1>());
         __syncthreads();
-    };
-    for (int kt = 0; kt < nk; kt += 2) {
-        step(kt, S0);
-        if (kt + 1 < nk) step(kt + 1, S1);
     }
 
     /* ---- epilogue: lane holds column lr of each 32x32 tile, rows
@@ -158,6 +160,48 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
     const int row0 = m0 + wm * TW_M;
+    /* interior tiles skip the per-element bounds checks */
+    if (m0 + BM <= M && n0 + BN <= N) {
+        switch (pr.epi) {
+        case IRIS_EPI_F32:
+        case IRIS_EPI_BF16:
+        case IRIS_EPI_GATED_ADD: {
+#pragma unroll
+            for (int ni = 0; ni < FN; ni++) {
+                const int col = n0 + wn * TW_N + ni * 32 + lr;
+                const float v = vec ? vec[col] : (pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f);
+#pragma unroll
+                for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const size_t o = (size_t)(row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3)) * ldo + col;
+                        const float x = acc[mi][ni][r];
+                        if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
+                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf(x + v);
+                        else ((float *)pr.out)[o] += v * x;
+                    }
+            }
+            return;
+        }
+        case IRIS_EPI_SWIGLU: {
+#pragma unroll
+            for (int g = 0; g < FN / 2; g++) {
+                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + lr;
+#pragma unroll
+                for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                        const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
+                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(gt) * up);
+                    }
+            }
+            return;
+        }
+        default:
+            break;
+        }
+    }
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
@@ -183,18 +227,21 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         break;
     }
     case IRIS_EPI_SWIGLU: {
-        /* the wave's 64 columns are one interleaved group: tile 0 = 32 gate
-         * rows, tile 1 = the matching 32 up rows; output column = group * 32 + lr */
-        const int col = ((n0 + wn * TW_N) >> 1) + lr;
-        if (col < (N >> 1)) {
+        /* each 64 columns of the wave are one interleaved group: tile 2g = 32
+         * gate rows, tile 2g+1 = the matching 32 up rows; output column =
+         * group * 32 + lr */
+#pragma unroll
+        for (int g = 0; g < FN / 2; g++) {
+            const int col = ((n0 + wn * TW_N + g * 64) >> 1) + lr;
+            if (col >= (N >> 1)) continue;
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     if (row >= M) continue;
-                    const float g = acc[mi][0][r], u = acc[mi][1][r];
-                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(g) * u);
+                    const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
+                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(gt) * up);
                 }
         }
         break;
