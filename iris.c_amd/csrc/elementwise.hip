@@ -11,26 +11,28 @@
  *   gemv           timestep MLP and modulation (:1366-1379, :4059-4069)
  *   layout         NCHW -> tokens (:3986-3993), patchify (zimage :1634-1684),
  *                  f32 <-> bf16, Euler update (iris_sample.c:359, :472-474)
- * One block of 256 threads per row for the row kernels; float4 / 16-byte
- * accesses throughout.
+ * One wave per row for the row kernels (wave-shuffle reductions, no block
+ * barriers); float4 / 16-byte accesses throughout.
  */
 #include "iris_internal.h"
 
 namespace {
 
 constexpr int NT = 256;
-constexpr int MAXV = 4;      /* float4 per thread: cols <= 4096 */
 
+/* One wave per row: lane owns float4 columns lane, lane + 64, ... (V of them),
+ * so both reductions are wave shuffles with no block barrier. */
+template <int V>
 __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
-    __shared__ float red[NT / IRIS_WAVE];
-    const int row = blockIdx.x, tid = threadIdx.x;
+    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= a.rows) return;
     const float *x = a.x + (size_t)row * a.ldx;
     const int nv = a.cols >> 2;
-    float4 v[MAXV];
+    float4 v[V];
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        const int c = tid + i * NT;
+    for (int i = 0; i < V; i++) {
+        const int c = lane + i * IRIS_WAVE;
         v[i] = c < nv ? ((const float4 *)x)[c] : make_float4(0, 0, 0, 0);
         s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
@@ -42,40 +44,43 @@ __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
     if (a.mode == IRIS_NORM_RMS) {
         float q = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MAXV; i++) q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-        q = block_sum<NT / IRIS_WAVE>(q, red);
-        inv = 1.0f / sqrtf(q / a.cols + a.eps);
+        for (int i = 0; i < V; i++) q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+        inv = 1.0f / sqrtf(wave_sum(q) / a.cols + a.eps);
     } else {
-        mean = block_sum<NT / IRIS_WAVE>(s, red) / a.cols;
+        mean = wave_sum(s) / a.cols;
         float q = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MAXV; i++) {
-            const int c = tid + i * NT;
+        for (int i = 0; i < V; i++) {
+            const int c = lane + i * IRIS_WAVE;
             if (c < nv) {
                 float d0 = v[i].x - mean, d1 = v[i].y - mean, d2 = v[i].z - mean, d3 = v[i].w - mean;
                 q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
             }
         }
-        q = block_sum<NT / IRIS_WAVE>(q, red);
-        inv = 1.0f / sqrtf(q / a.cols + a.eps);
+        inv = 1.0f / sqrtf(wave_sum(q) / a.cols + a.eps);
     }
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        const int c = tid + i * NT;
+    for (int i = 0; i < V; i++) {
+        const int c = lane + i * IRIS_WAVE;
         if (c >= nv) continue;
         float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
         float y[4];
+        float4 sc4 = make_float4(0, 0, 0, 0), sh4 = make_float4(0, 0, 0, 0), w4 = make_float4(1, 1, 1, 1);
+        if (scale) sc4 = ((const float4 *)scale)[c];
+        if (a.mode == IRIS_NORM_LN_MOD) sh4 = ((const float4 *)shift)[c];
+        if (a.mode == IRIS_NORM_RMS) w4 = ((const float4 *)w)[c];
+        const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w}, sh[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
+        const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int col = 4 * c + j;
             if (a.mode == IRIS_NORM_LN_MOD) {
                 const float n = (e[j] - mean) * inv;
-                y[j] = (1.0f + scale[col]) * n + shift[col];
+                y[j] = (1.0f + sc[j]) * n + sh[j];
             } else if (a.mode == IRIS_NORM_LN_SCALE) {
-                y[j] = (e[j] - mean) * inv * scale[col];
+                y[j] = (e[j] - mean) * inv * sc[j];
             } else {
-                float t = e[j] * inv * w[col];
-                if (scale) t *= scale[col];
+                float t = e[j] * inv * ww[j];
+                if (scale) t *= sc[j];
                 y[j] = t;
             }
         }
@@ -88,89 +93,125 @@ __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
     }
 }
 
+template <int V>
 __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float *y, const float *w,
-                                                           const float *gate, int cols, float eps, int gate_tanh) {
-    __shared__ float red[NT / IRIS_WAVE];
-    const int row = blockIdx.x, tid = threadIdx.x, nv = cols >> 2;
+                                                           const float *gate, int rows, int cols, float eps,
+                                                           int gate_tanh) {
+    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const int nv = cols >> 2;
     const float *yr = y + (size_t)row * cols;
     float *xr = x + (size_t)row * cols;
-    float4 v[MAXV];
+    float4 v[V];
     float q = 0.0f;
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        const int c = tid + i * NT;
+    for (int i = 0; i < V; i++) {
+        const int c = lane + i * IRIS_WAVE;
         v[i] = c < nv ? ((const float4 *)yr)[c] : make_float4(0, 0, 0, 0);
         q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
-    q = block_sum<NT / IRIS_WAVE>(q, red);
-    const float inv = 1.0f / sqrtf(q / cols + eps);
+    const float inv = 1.0f / sqrtf(wave_sum(q) / cols + eps);
 #pragma unroll
-    for (int i = 0; i < MAXV; i++) {
-        const int c = tid + i * NT;
+    for (int i = 0; i < V; i++) {
+        const int c = lane + i * IRIS_WAVE;
         if (c >= nv) continue;
         float4 xo = ((float4 *)xr)[c];
-        float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        const float4 w4 = ((const float4 *)w)[c];
+        float4 g4 = make_float4(1, 1, 1, 1);
+        if (gate) g4 = ((const float4 *)gate)[c];
+        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w}, ww[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float gg[4] = {g4.x, g4.y, g4.z, g4.w};
         float *xp = &xo.x;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int col = 4 * c + j;
-            const float g = gate ? (gate_tanh ? tanhf(gate[col]) : gate[col]) : 1.0f;
-            xp[j] += g * (e[j] * inv * w[col]);
+            const float g = gate ? (gate_tanh ? tanhf(gg[j]) : gg[j]) : 1.0f;
+            xp[j] += g * (e[j] * inv * ww[j]);
         }
         ((float4 *)xr)[c] = xo;
     }
 }
 
-/* one wave per (row, head): lane i owns the rotation pair (2i, 2i+1) */
+/* One wave per row: 16 lanes per head, lane owns dims d0..d0+7 (four rotation
+ * pairs); a 16-byte load covers 4 heads per wave, the head's sum of squares is
+ * a 16-lane shuffle reduction. */
 __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args_t a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * (NT / IRIS_WAVE) + wave, head = blockIdx.y;
+    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= a.rows) return;
     const int prow = a.period ? row % a.period : row;
     const bool use_b = prow >= a.split;
-    const float *wq = use_b ? a.wqB : a.wqA;
-    const float *wk = use_b ? a.wkB : a.wkA;
-    const int d = 2 * lane;
-    float c = 1.0f, s = 0.0f;
+    const int hl = lane & 15, hq = lane >> 4, d0 = hl * 8;
+    float c[8], sn[8];
     if (a.cos_t) {
-        c = a.cos_t[(size_t)prow * 128 + d];
-        s = a.sin_t[(size_t)prow * 128 + d];
+        const float4 c0 = *(const float4 *)(a.cos_t + (size_t)prow * 128 + d0);
+        const float4 c1 = *(const float4 *)(a.cos_t + (size_t)prow * 128 + d0 + 4);
+        const float4 s0 = *(const float4 *)(a.sin_t + (size_t)prow * 128 + d0);
+        const float4 s1 = *(const float4 *)(a.sin_t + (size_t)prow * 128 + d0 + 4);
+        c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) { c[j] = 1.0f; sn[j] = 0.0f; }
     }
-    const size_t out_off = (size_t)row * a.heads * 128 + head * 128 + d;
 #pragma unroll
     for (int which = 0; which < 2; which++) {
-        const uint16_t *src = a.qkv + (size_t)row * a.ld_qkv + (which ? a.col_k : 0) + head * 128 + d;
-        const uint32_t pr = *(const uint32_t *)src;
-        float x0 = bf2f((uint16_t)(pr & 0xffff)), x1 = bf2f((uint16_t)(pr >> 16));
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
-        const float *w = which ? wk : wq;
-        x0 = x0 * inv * w[d];
-        x1 = x1 * inv * w[d + 1];
-        const float y0 = x0 * c - x1 * s, y1 = x1 * c + x0 * s;
-        uint16_t *dst = (which ? a.k_out : a.q_out) + out_off;
-        *(uint32_t *)dst = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+        const float *wsel = which ? (use_b ? a.wkB : a.wkA) : (use_b ? a.wqB : a.wqA);
+        const float4 w0 = *(const float4 *)(wsel + d0), w1 = *(const float4 *)(wsel + d0 + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const uint16_t *src = a.qkv + (size_t)row * a.ld_qkv + (which ? a.col_k : 0) + d0;
+        uint16_t *dst = (which ? a.k_out : a.q_out) + (size_t)row * a.heads * 128 + d0;
+        for (int hb = 0; hb < a.heads; hb += 4) {
+            const int head = hb + hq;
+            const bool on = head < a.heads;                   /* uniform per 16-lane group */
+            u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (on) raw = *(const u16x8 *)(src + head * 128);
+            float x[8];
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[j]); ss += x[j] * x[j]; }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+            const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+            u16x8 out;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float x0 = x[j] * inv * w[j], x1 = x[j + 1] * inv * w[j + 1];
+                out[j] = f2bf(x0 * c[j] - x1 * sn[j]);
+                out[j + 1] = f2bf(x1 * c[j] + x0 * sn[j]);
+            }
+            if (on) *(u16x8 *)(dst + head * 128) = out;
+        }
     }
 }
 
-/* V [rows][128] (head slice of qkv) -> V^T [head][128][ld_vt], 64 rows per block */
+/* V [rows][128] (head slice of qkv) -> V^T [head][128][ld_vt], 64 rows per
+ * block. LDS holds the tile as [d][row] in rows of 72 elements (16-byte
+ * aligned); 8-row chunks are XOR-swizzled by (d / 8) mod 8 to spread the
+ * two-row writes over the banks. Rows past the end are written as zeros. */
 __global__ __launch_bounds__(NT) void v_transpose_kernel(const iris_qkprep_args_t a) {
-    __shared__ uint16_t t[128][64 + 2];
+    __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
     const int r0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
-    for (int i = tid; i < 64 * 64; i += NT) {              /* 64 rows x 64 pairs */
-        const int r = i >> 6, p = i & 63;
-        uint32_t pr = 0;
-        if (r0 + r < a.rows)
-            pr = *(const uint32_t *)(a.qkv + (size_t)(r0 + r) * a.ld_qkv + a.col_v + head * 128 + 2 * p);
-        t[2 * p][r] = (uint16_t)(pr & 0xffff);
-        t[2 * p + 1][r] = (uint16_t)(pr >> 16);
+#pragma unroll
+    for (int it = 0; it < 2; it++) {                       /* 32 row pairs x 16 chunks of 8 dims */
+        const int item = tid + NT * it, p = item >> 4, ch = item & 15;
+        const int ra = r0 + 2 * p;
+        const uint16_t *src = a.qkv + (size_t)ra * a.ld_qkv + a.col_v + head * 128 + ch * 8;
+        u16x8 va = {0, 0, 0, 0, 0, 0, 0, 0}, vb = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (ra < a.rows) va = *(const u16x8 *)src;
+        if (ra + 1 < a.rows) vb = *(const u16x8 *)(src + a.ld_qkv);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int d = ch * 8 + j;
+            const int col = (2 * p) ^ (((d >> 3) & 7) << 3);
+            *(uint32_t *)(&t[d * 72 + col]) = (uint32_t)va[j] | ((uint32_t)vb[j] << 16);
+        }
     }
     __syncthreads();
     uint16_t *dst = a.vt_out + (size_t)head * 128 * a.ld_vt + r0;
-    for (int i = tid; i < 128 * 32; i += NT) {             /* 128 d x 32 pairs of rows */
-        const int d = i >> 5, p = i & 31;
-        if (r0 + 2 * p < a.ld_vt)
-            *(uint32_t *)(dst + (size_t)d * a.ld_vt + 2 * p) = (uint32_t)t[d][2 * p] | ((uint32_t)t[d][2 * p + 1] << 16);
+#pragma unroll
+    for (int it = 0; it < 4; it++) {                       /* 128 d x 8 chunks of 8 rows */
+        const int item = tid + NT * it, d = item >> 3, c8 = item & 7;
+        const uint4 v = *(const uint4 *)(&t[d * 72 + ((c8 ^ ((d >> 3) & 7)) << 3)]);
+        *(uint4 *)(dst + (size_t)d * a.ld_vt + c8 * 8) = v;
     }
 }
 
@@ -264,28 +305,57 @@ int grid1d(size_t n) {
 
 extern "C" {
 
+#define IRIS_ROWS_V(KERNEL, v, grid, ...)                                                                  \
+    do {                                                                                                   \
+        switch (v) {                                                                                       \
+        case 1: hipLaunchKernelGGL(KERNEL<1>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
+        case 2: hipLaunchKernelGGL(KERNEL<2>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
+        case 4: hipLaunchKernelGGL(KERNEL<4>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
+        case 8: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
+        case 10: hipLaunchKernelGGL(KERNEL<10>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
+        case 12: hipLaunchKernelGGL(KERNEL<12>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
+        case 16: hipLaunchKernelGGL(KERNEL<16>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
+        default: return iris_set_error(#KERNEL ": unsupported width");                                     \
+        }                                                                                                  \
+    } while (0)
+
+/* float4 columns per lane: the smallest instantiated count covering cols */
+static int lanes_v(int cols) {
+    const int need = (cols / 4 + IRIS_WAVE - 1) / IRIS_WAVE;
+    static const int vs[] = {1, 2, 4, 8, 10, 12, 16};
+    for (int v : vs)
+        if (v >= need) return v;
+    return 0;
+}
+
 int iris_hip_rownorm(const iris_norm_args_t *a) {
     if (a->rows <= 0) return 0;
-    if (a->cols % 4 || a->cols > NT * 4 * MAXV) return iris_set_error("rownorm: cols=%d", a->cols);
+    const int v = lanes_v(a->cols);
+    if (a->cols % 4 || !v) return iris_set_error("rownorm: cols=%d", a->cols);
     if (a->ldx % 4 || a->ldo % 4) return iris_set_error("rownorm: ld must be multiple of 4");
-    hipLaunchKernelGGL(rownorm_kernel, dim3(a->rows), dim3(NT), 0, iris_stream(), *a);
+    const dim3 grid((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE));
+    IRIS_ROWS_V(rownorm_kernel, v, grid, *a);
     return iris_launch_check("rownorm_kernel");
 }
 
 int iris_hip_rms_gated_add(float *x, const float *y, const float *w, const float *gate, int rows, int cols,
                            float eps, int gate_tanh) {
     if (rows <= 0) return 0;
-    if (cols % 4 || cols > NT * 4 * MAXV) return iris_set_error("rms_gated_add: cols=%d", cols);
-    hipLaunchKernelGGL(rms_gated_add_kernel, dim3(rows), dim3(NT), 0, iris_stream(), x, y, w, gate, cols, eps,
-                       gate_tanh);
+    const int v = lanes_v(cols);
+    if (cols % 4 || !v) return iris_set_error("rms_gated_add: cols=%d", cols);
+    const dim3 grid((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE));
+    IRIS_ROWS_V(rms_gated_add_kernel, v, grid, x, y, w, gate, rows, cols, eps, gate_tanh);
     return iris_launch_check("rms_gated_add_kernel");
 }
 
 int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
     if (a->rows <= 0) return 0;
-    if (a->ld_qkv % 2 || a->col_k % 2 || a->col_v % 2) return iris_set_error("qk_prepare: odd layout");
+    if (a->ld_qkv % 8 || a->col_k % 8 || a->col_v % 8) return iris_set_error("qk_prepare: layout not 16-byte aligned");
     if (a->ld_vt < a->rows || a->ld_vt % 64) return iris_set_error("qk_prepare: ld_vt=%d", a->ld_vt);
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((a->rows + 3) / 4, a->heads), dim3(NT), 0, iris_stream(), *a);
+    if (((uintptr_t)a->qkv | (uintptr_t)a->q_out | (uintptr_t)a->k_out | (uintptr_t)a->vt_out) & 15)
+        return iris_set_error("qk_prepare: buffers must be 16-byte aligned");
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+                       iris_stream(), *a);
     if (iris_launch_check("qk_norm_rope_kernel")) return -1;
     hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, a->heads), dim3(NT), 0, iris_stream(), *a);
     return iris_launch_check("v_transpose_kernel");
