@@ -7,11 +7,12 @@
  * iris_kernels.c:737-1048; Z-Image's masked scalar loops
  * iris_transformer_zimage.c:689-761). Scores never leave registers.
  *
- * Block = 4 waves, 256 queries of one head (64 per wave, two 32-query
- * sub-tiles); one wave per SIMD. The block's Q tile sits in LDS; keys
- * stream through LDS in tiles of 64:
- *   S^T[key][q] = K Q^T          (K tile = MFMA A operand, Q = B operand,
- *                                 both read from LDS)
+ * Block = 8 waves, 256 queries of one head (32 per wave), two waves per SIMD:
+ * while one wave forms probabilities (VALU) the other's matrix products run.
+ * A wave's Q fragments, scores, probabilities and output accumulators all fit
+ * in its 256 registers. Keys stream through LDS in tiles of 64 (two stages):
+ *   S^T[key][q] = K Q^T          (K tile = MFMA A operand from LDS,
+ *                                 Q = B operand held in registers)
  *   online softmax per query column in the log2 domain, f32: the scale and
  *   log2(e) are folded into the exp2 argument, p = exp2(fma(s, c, -m))
  *   O^T[d][q] += V^T P^T         (V^T tile = A operand from LDS, P = B operand
@@ -20,16 +21,18 @@
  * layout of the PV product, so P never goes through LDS. V arrives already
  * transposed ([head][d][key], written by iris_hip_qk_prepare).
  *
- * Pipelining: while tile t's probabilities are formed (VALU) and multiplied
- * into O (MFMA), the scores of tile t+1 are already being computed (MFMA), so
- * the exp/sum work overlaps matrix work inside one wave. K tiles are staged two
- * tiles ahead and V tiles one ahead (two LDS buffers each).
- *
  * The running max is updated lazily: O and the row sums are rescaled only when
  * some query's tile max exceeds its running max by more than 8 (log2 units),
- * so probabilities stay <= 2^8 and most tiles skip the 128-register rescale.
- * Key masks (sequence end, padding ranges) cost one uniform branch per tile
- * and are applied only to tiles that are not fully valid.
+ * so probabilities stay <= 2^8 and most tiles skip the rescale. Key masks
+ * (sequence end, padding ranges) cost one uniform branch per tile and are
+ * applied only to tiles that are not fully valid.
+ *
+ * LDS rows are padded instead of swizzled, so every fragment address is one
+ * base register plus an immediate offset: K rows hold 128 + 8 elements (272 B:
+ * 16 consecutive rows start 4 banks apart, conflict-free 16-byte reads), V^T
+ * rows 64 + 4 (136 B: 32 consecutive rows start 2 banks apart, conflict-free
+ * 8-byte reads). Global loads go through buffer descriptors; K's range ends at
+ * its last valid row so rows past the end read as zero.
  *
  * Blocks are ordered head-major and mapped XCD-major (block b runs on XCD
  * b % 8 and takes a contiguous range of the work list), so the query blocks
@@ -39,23 +42,16 @@
 
 namespace {
 
-constexpr int QB = 256, KB = 64, HD = 128, NT = 256;
+constexpr int QB = 256, KB = 64, HD = 128, NT = 512, NW = NT / 64, QW = QB / NW;
 constexpr float RESCALE_LOG2 = 8.0f;
-/* LDS rows are padded instead of swizzled, so every fragment address is one
- * base register plus an immediate offset: K and Q rows hold 128 + 8 elements
- * (272 B: 8 consecutive rows start 4 banks apart, conflict-free 16-byte
- * reads), V^T rows 64 + 4 (136 B: 16 consecutive rows start 2 banks apart,
- * conflict-free 8-byte reads). K tiles 2 x 17 KB, V^T tiles 2 x 17 KB, Q 68 KB. */
 constexpr int KSTR = HD + 8, VSTR = KB + 4;
-constexpr int KS_ELEMS = KB * KSTR, VS_ELEMS = HD * VSTR, QS_ELEMS = QB * KSTR;
-constexpr size_t SMEM_BYTES = (size_t)(2 * KS_ELEMS + 2 * VS_ELEMS + QS_ELEMS) * 2;
-
-typedef f32x16 stile[2][2];    /* [key sub-tile][query sub-tile] */
+constexpr int KS_ELEMS = KB * KSTR, VS_ELEMS = HD * VSTR;
+constexpr size_t SMEM_BYTES = (size_t)(2 * KS_ELEMS + 2 * VS_ELEMS) * 2;
+static_assert(QW == 32, "one 32-query MFMA column block per wave");
 
 __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a, float scale_log2, int nqb,
                                                         int per_xcd, int total) {
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-    uint16_t *const Qs = smem + 2 * KS_ELEMS + 2 * VS_ELEMS;
 #define KBUF(b) (smem + (b) * KS_ELEMS)
 #define VBUF(b) (smem + 2 * KS_ELEMS + (b) * VS_ELEMS)
 
@@ -71,91 +67,78 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     const int sq = a.sq, sk = a.sk;
     const int nkt = (sk + KB - 1) / KB;
 
-    /* Q tile into LDS (rows past the end are zero) */
-#pragma unroll 4
-    for (int i = 0; i < QB * 16 / NT; i++) {
-        const int c = tid + NT * i;
-        const int row = c >> 4, ch = c & 15, q = qblk * QB + row;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (q < sq) v = *(const uint4 *)(Q + (size_t)q * a.ld_q + ch * 8);
-        *(uint4 *)(&Qs[row * KSTR + ch * 8]) = v;
+    /* Q fragments (B operand): lane holds query lr of the wave's 32, d = ds*16 + lg*8 .. +7 */
+    const int q_row = qblk * QB + wave * QW + lr;
+    bf16x8 qf[8];
+#pragma unroll
+    for (int ds = 0; ds < 8; ds++) {
+        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (q_row < sq) v = *(const u16x8 *)(Q + (size_t)q_row * a.ld_q + ds * 16 + lg * 8);
+        qf[ds] = __builtin_bit_cast(bf16x8, v);
     }
 
-    f32x16 o[4][2];
+    f32x16 o[4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) o[i][j][r] = 0.0f;
-    /* running max per query column (identical in the two lanes of a column) and
-     * this lane's partial row sum over its half of each tile's keys */
-    float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.0f, 0.0f};
+        for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+    /* running max of the lane's query column (same in both lanes of the column)
+     * and this lane's partial row sum over its half of each tile's keys */
+    float m_run = -1e30f, l_run = 0.0f;
 
-    /* staging registers: 4 K chunks (16B) and 4 V^T chunks per thread per tile,
-     * loaded through buffer resources: K's range ends at its last valid row so
-     * rows past the end read as zero */
+    /* staging: 2 K chunks (16B) and 2 V^T chunks per thread per tile */
     const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)K, (short)0, (int)(((size_t)(sk - 1) * a.ld_k + HD) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)VT, (short)0, (int)((size_t)HD * a.ld_vt * 2), 0x00020000);
-    const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
-    const int v_off = ((tid >> 3) * a.ld_vt + (tid & 7) * 8) * 2;
-    uint4 rk[4], rv[4];
-    auto gload_k = [&](int kt) {
+    const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;     /* rows tid/16 (+32) */
+    const int v_off = ((tid >> 3) * a.ld_vt + (tid & 7) * 8) * 2;     /* d rows tid/8 (+64) */
+    uint4 rk[2], rv[2];
+    auto gload = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++) {
             rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  k_rsrc, k_off, (kt * KB + 16 * i) * a.ld_k * 2, 0));
-    };
-    auto gload_v = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < 4; i++)
+                                                  k_rsrc, k_off, (kt * KB + 32 * i) * a.ld_k * 2, 0));
             rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  v_rsrc, v_off, (32 * i * a.ld_vt + kt * KB) * 2, 0));
+                                                  v_rsrc, v_off, (64 * i * a.ld_vt + kt * KB) * 2, 0));
+        }
     };
-    auto sstore_k = [&](int buf) {
-        uint16_t *dst = KBUF(buf) + (tid >> 4) * KSTR + (tid & 15) * 8;
+    auto sstore = [&](int buf) {
+        uint16_t *kd = KBUF(buf) + (tid >> 4) * KSTR + (tid & 15) * 8;
+        uint16_t *vd = VBUF(buf) + (tid >> 3) * VSTR + (tid & 7) * 8;
 #pragma unroll
-        for (int i = 0; i < 4; i++) *(uint4 *)(dst + 16 * i * KSTR) = rk[i];
-    };
-    auto sstore_v = [&](int buf) {
-        uint16_t *dst = VBUF(buf) + (tid >> 3) * VSTR + (tid & 7) * 8;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            *(uint2 *)(dst + 32 * i * VSTR) = make_uint2(rv[i].x, rv[i].y);
-            *(uint2 *)(dst + 32 * i * VSTR + 4) = make_uint2(rv[i].z, rv[i].w);
+        for (int i = 0; i < 2; i++) {
+            *(uint4 *)(kd + 32 * i * KSTR) = rk[i];
+            *(uint2 *)(vd + 64 * i * VSTR) = make_uint2(rv[i].x, rv[i].y);
+            *(uint2 *)(vd + 64 * i * VSTR + 4) = make_uint2(rv[i].z, rv[i].w);
         }
     };
 
-    /* S^T of one tile from Ks[buf] */
-    auto scores = [&](int buf, stile &s) {
+    gload(0);
+    sstore(0);
+    if (nkt > 1) gload(1);
+    __syncthreads();
+
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int cur = kt & 1, k0 = kt * KB;
+        /* S^T for the tile: 2 key sub-tiles of 32 x the wave's 32 queries */
+        f32x16 s[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-            for (int qs = 0; qs < 2; qs++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) s[ks][qs][r] = 0.0f;
+            for (int r = 0; r < 16; r++) s[ks][r] = 0.0f;
 #pragma unroll
         for (int ds = 0; ds < 8; ds++) {
-            bf16x8 qf[2];
-#pragma unroll
-            for (int qs = 0; qs < 2; qs++)
-                qf[qs] = *(const bf16x8 *)(&Qs[(wave * 64 + qs * 32 + lr) * KSTR + (ds * 2 + lg) * 8]);
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                const bf16x8 kf = *(const bf16x8 *)(&KBUF(buf)[(ks * 32 + lr) * KSTR + (ds * 2 + lg) * 8]);
-#pragma unroll
-                for (int qs = 0; qs < 2; qs++)
-                    s[ks][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[qs], s[ks][qs], 0, 0, 0);
+                const bf16x8 kf = *(const bf16x8 *)(&KBUF(cur)[(ks * 32 + lr) * KSTR + (ds * 2 + lg) * 8]);
+                s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[ks], 0, 0, 0);
             }
         }
-    };
+        /* the stage read in step kt-1 is free: tile kt+1 goes there, tile kt+2's loads start */
+        if (kt + 1 < nkt) sstore(cur ^ 1);
+        if (kt + 2 < nkt) gload(kt + 2);
 
-    /* keys past the end or outside [lo0, hi0) U [lo1, hi1) get -inf (uniform branch per tile);
-     * then the lazy running-max update for the tile */
-    auto finish_scores = [&](int kt, stile &s) {
-        const int k0 = kt * KB;
         const bool full = k0 + KB <= sk && ((k0 >= a.kv_lo0 && k0 + KB <= a.kv_hi0) ||
                                             (k0 >= a.kv_lo1 && k0 + KB <= a.kv_hi1));
         if (!full) {
@@ -166,107 +149,58 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
                     const int key = k0 + ks * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     const bool ok = (key < sk) & (((key >= a.kv_lo0) & (key < a.kv_hi0)) |
                                                   ((key >= a.kv_lo1) & (key < a.kv_hi1)));
-#pragma unroll
-                    for (int qs = 0; qs < 2; qs++) s[ks][qs][r] = ok ? s[ks][qs][r] : -INFINITY;
+                    s[ks][r] = ok ? s[ks][r] : -INFINITY;
                 }
         }
-        float mx[2];
+        float mx = -INFINITY;
 #pragma unroll
-        for (int qs = 0; qs < 2; qs++) {
-            float m = -INFINITY;
+        for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++)
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[ks][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        if (__any(mx > m_run + RESCALE_LOG2)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
 #pragma unroll
-                for (int r = 0; r < 16; r++) m = fmaxf(m, s[ks][qs][r]);
-            mx[qs] = fmaxf(m, __shfl_xor(m, 32, 64)) * scale_log2;
+            for (int dsub = 0; dsub < 4; dsub++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) o[dsub][r] *= alpha;
         }
-        const bool need = mx[0] > m_run[0] + RESCALE_LOG2 || mx[1] > m_run[1] + RESCALE_LOG2;
-        if (__any(need)) {
-#pragma unroll
-            for (int qs = 0; qs < 2; qs++) {
-                const float m_new = fmaxf(m_run[qs], mx[qs]);
-                const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - m_new);
-                m_run[qs] = m_new;
-                l_run[qs] *= alpha;
-#pragma unroll
-                for (int dsub = 0; dsub < 4; dsub++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) o[dsub][qs][r] *= alpha;
-            }
-        }
-    };
 
-    /* P = exp2(S - m) as bf16 B-operand fragments, row sums, then O^T += V^T P^T from Vs[buf] */
-    auto accumulate = [&](int buf, stile &s) {
-        bf16x8 pf[2][4];
+        /* P = exp2(S - m) as bf16 B-operand fragments; O^T += V^T P^T */
+        bf16x8 pf[4];
+        float rs = 0.0f;
 #pragma unroll
-        for (int qs = 0; qs < 2; qs++) {
-            float rs = 0.0f;
+        for (int j = 0; j < 4; j++) {
+            bf16x8 v;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                bf16x8 v;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[j >> 1][qs][(j & 1) * 8 + e], scale_log2, -m_run[qs]));
-                    rs += p;
-                    v[e] = (__bf16)p;
-                }
-                pf[qs][j] = v;
+            for (int e = 0; e < 8; e++) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[j >> 1][(j & 1) * 8 + e], scale_log2, -m_run));
+                rs += p;
+                v[e] = (__bf16)p;
             }
-            l_run[qs] += rs;
+            pf[j] = v;
         }
+        l_run += rs;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
 #pragma unroll
             for (int dsub = 0; dsub < 4; dsub++) {
                 const int d = dsub * 32 + lr;
-                const uint2 lo = *(const uint2 *)(&VBUF(buf)[d * VSTR + (4 * j + lg) * 4]);
-                const uint2 hi = *(const uint2 *)(&VBUF(buf)[d * VSTR + (4 * j + 2 + lg) * 4]);
+                const uint2 lo = *(const uint2 *)(&VBUF(cur)[d * VSTR + (4 * j + lg) * 4]);
+                const uint2 hi = *(const uint2 *)(&VBUF(cur)[d * VSTR + (4 * j + 2 + lg) * 4]);
                 const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                for (int qs = 0; qs < 2; qs++)
-                    o[dsub][qs] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[qs][j], o[dsub][qs], 0, 0, 0);
+                o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[dsub], 0, 0, 0);
             }
         }
-    };
-
-    /* one key tile: scores of tile kt are in sc; computes tile kt+1's scores into sn.
-     * Loads past the last tile are clamped to it (in bounds, results unused). */
-    auto step = [&](int kt, stile &sc, stile &sn) {
-        const int last = nkt - 1;
-        gload_k(min(kt + 2, last));
-        gload_v(min(kt + 1, last));
-        scores((kt + 1) & 1, sn);
-        accumulate(kt & 1, sc);
-        sstore_k(kt & 1);
-        sstore_v((kt + 1) & 1);
         __syncthreads();
-        if (kt + 1 < nkt) finish_scores(kt + 1, sn);
-    };
-
-    /* prologue: K0, V0, K1 staged; scores of tile 0 */
-    gload_k(0);
-    gload_v(0);
-    sstore_k(0);
-    sstore_v(0);
-    gload_k(min(1, nkt - 1));
-    sstore_k(1);
-    __syncthreads();
-    stile sA, sB;
-    scores(0, sA);
-    finish_scores(0, sA);
-
-    for (int kt = 0; kt < nkt; kt += 2) {
-        step(kt, sA, sB);
-        if (kt + 1 < nkt) step(kt + 1, sB, sA);
     }
 
     /* normalise and store O[q][d]: lane holds query lr, d = dsub*32 + (r>>2)*8 + lg*4 + (r&3) */
-#pragma unroll
-    for (int qs = 0; qs < 2; qs++) {
-        const int q = qblk * QB + wave * 64 + qs * 32 + lr;
-        const float l = l_run[qs] + __shfl_xor(l_run[qs], 32, 64);
-        if (q >= sq) continue;
+    const float l = l_run + __shfl_xor(l_run, 32, 64);
+    if (q_row < sq) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int dsub = 0; dsub < 4; dsub++)
@@ -275,14 +209,13 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
                 const int d = dsub * 32 + rb * 8 + lg * 4;
                 u16x4 v;
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = f2bf(o[dsub][qs][rb * 4 + e] * inv);
-                *(u16x4 *)(O + (size_t)q * a.ld_o + d) = v;
+                for (int e = 0; e < 4; e++) v[e] = f2bf(o[dsub][rb * 4 + e] * inv);
+                *(u16x4 *)(O + (size_t)q_row * a.ld_o + d) = v;
             }
     }
-}
-
 #undef KBUF
 #undef VBUF
+}
 
 }  // namespace
 
