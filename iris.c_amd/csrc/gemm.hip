@@ -177,7 +177,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                         const size_t o = (size_t)(row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3)) * ldo + col;
                         const float x = acc[mi][ni][r];
                         if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
-                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf(x + v);
+                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf_hw(x + v);
                         else ((float *)pr.out)[o] += v * x;
                     }
             }
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                     for (int r = 0; r < 16; r++) {
                         const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                         const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
-                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(gt) * up);
+                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
                     }
             }
             return;
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                     const size_t o = (size_t)row * ldo + col;
                     const float x = acc[mi][ni][r];
                     if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
-                    else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf(x + v);
+                    else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf_hw(x + v);
                     else ((float *)pr.out)[o] += v * x;
                 }
         }
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                     const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     if (row >= M) continue;
                     const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
-                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf(silu_f(gt) * up);
+                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
                 }
         }
         break;

@@ -56,3 +56,10 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 }
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+
+/* SiLU with the hardware reciprocal (~1 ulp) instead of an IEEE division;
+ * for results rounded to bf16 next */
+__device__ __forceinline__ float silu_fast(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+/* hardware round-to-nearest-even f32 -> bf16 (v_cvt_pk_bf16_f32; NaN stays NaN) */
+__device__ __forceinline__ uint16_t f2bf_hw(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
