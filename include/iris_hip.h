@@ -146,6 +146,42 @@ int iris_hip_unpatchify(float *d_latent, const float *d_patches, int C, int H, i
 /* copy one f32 row vector into rows [r0, r1) of a [*, cols] matrix */
 int iris_hip_fill_rows(float *d_x, const float *d_row, int r0, int r1, int cols);
 
+/* ---- f32 kernel API support (iris_kernels.h) ---- */
+/* f32 -> bf16 hi/lo split for f32-accurate GEMMs: the destination row holds
+ * nseg (1..3) segments of K_pad columns (zero padded past the data), segment s
+ * = lo(x) if bit s of lo_mask is set else hi(x), hi = bf16(x), lo = bf16(x - hi).
+ * A = [hi|hi|lo] (mask 4) against W = [hi|lo|hi] (mask 2) over K = 3 * K_pad
+ * sums Ahi.Whi + Ahi.Wlo + Alo.Whi in one GEMM. */
+int iris_hip_split_rows(uint16_t *d_dst, const float *d_src, int rows, int cols, int ld_src, int K_pad, int nseg,
+                        int lo_mask);
+/* src [K][N] -> dst [N][nseg * K_pad] (transposed) */
+int iris_hip_split_transpose(uint16_t *d_dst, const float *d_src, int K, int N, int K_pad, int nseg, int lo_mask);
+/* bf16 [rows][cols] -> nseg zero-padded copies side by side [rows][nseg * K_pad] */
+int iris_hip_pad_bf16(uint16_t *d_dst, const uint16_t *d_src, int rows, int cols, int K_pad, int nseg);
+/* im2col rows for output pixels [pix0, pix0 + npix) of one [C][H][W] image,
+ * columns (ic, kh, kw), split as above into [npix][nseg * K_pad] */
+int iris_hip_im2col_split(uint16_t *d_dst, const float *d_in, int C, int H, int W, int kH, int kW, int stride,
+                          int pad, int outW, int pix0, int npix, int K_pad, int nseg, int lo_mask);
+/* op: 0 out = a + b, 1 out = a * b, 2 out = a + s * b, 3 out = silu(a), 4 out = silu(a) * b */
+int iris_hip_elementwise(int op, float *d_out, const float *d_a, const float *d_b, float s, size_t n);
+/* out[r][c] += bias[r] for c < cols */
+int iris_hip_add_row_bias(float *d_out, const float *d_bias, int rows, int cols, int ld);
+int iris_hip_rms_rows(float *d_out, const float *d_x, const float *d_w, int rows, int cols, float eps);
+int iris_hip_softmax_rows(float *d_x, int rows, int cols);
+/* x [batch][channels][spatial]; gamma / beta [channels] */
+int iris_hip_group_norm(float *d_out, const float *d_x, const float *d_gamma, const float *d_beta, int batch,
+                        int channels, int spatial, int groups, float eps);
+int iris_hip_batch_norm(float *d_out, const float *d_x, const float *d_mean, const float *d_var,
+                        const float *d_gamma, const float *d_beta, int batch, int channels, int spatial, float eps);
+int iris_hip_upsample_nearest(float *d_out, const float *d_in, int planes, int H, int W, int sh, int sw);
+/* [B][C][H][W] <-> [B][C*p*p][H/p][W/p], channel c*p*p + pi*p + pj = pixel (ph*p + pi, pw*p + pj) */
+int iris_hip_space_to_depth(float *d_out, const float *d_in, int batch, int C, int H, int W, int p, int inverse);
+/* f32 attention for head_dim <= 512, keys <= 12288: row r of q / o for
+ * (batch b, head h) at b*q_sb + h*q_sh + r*ld, of k / v at b*k_sb + h*k_sh + r*ld */
+int iris_hip_attention_f32(float *d_o, const float *d_q, const float *d_k, const float *d_v, int batch, int heads,
+                           int sq, int sk, int hd, float scale, long long q_sb, long long q_sh, long long k_sb,
+                           long long k_sh, int ld);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,7 @@
 #include "../../include/iris_transformer.h"
 #include "../../include/iris_hip.h"
 #include "../../include/iris_synth.h"
+#include "../../include/iris_kernels.h"
 #include "iris_st.h"
 #include "iris_tables.h"
 
@@ -701,6 +702,14 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
     if (iris_hip_graph_launch(w->graph)) return -1;
+    /* per-block progress (iris_transformer_flux.c:4085-4086, :4185-4186,
+     * :4315-4316); the blocks run inside one graph, so these fire once the
+     * step has been enqueued */
+    if (iris_substep_callback) {
+        for (int i = 0; i < tf->n_double; i++) iris_substep_callback(IRIS_SUBSTEP_DOUBLE_BLOCK, i, tf->n_double);
+        for (int i = 0; i < tf->n_single; i++) iris_substep_callback(IRIS_SUBSTEP_SINGLE_BLOCK, i, tf->n_single);
+        iris_substep_callback(IRIS_SUBSTEP_FINAL_LAYER, 0, 1);
+    }
     return 0;
 }
 

@@ -9,6 +9,7 @@
  */
 #include "../../include/iris_sample.h"
 #include "../../include/iris_hip.h"
+#include "../../include/iris_kernels.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -125,6 +126,8 @@ static float *flux_loop(iris_transformer_t *tf, const float *z, int channels, in
     (void)channels;
     if (iris_flux_prepare(tf, h, w, refs, nrefs, T, B) || iris_flux_upload(tf, z, refs, txt)) return NULL;
     for (int i = 0; i < n; i++) {
+        /* step callback, then the cancel check (iris_sample.c:345-348) */
+        if (iris_step_callback) iris_step_callback(i + 1, n);
         if (iris_cancel_requested) return NULL;
         if (iris_flux_step(tf, sched[i], sched[i + 1], g)) return NULL;
         if (cb) cb(i + 1, n);
@@ -170,20 +173,36 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
         free(both);
         return r;
     }
-    /* different text lengths: two sequential forwards per step, as the reference */
+    /* different text lengths: two sequential forwards per step, as the
+     * reference; the guided Euler update runs on the device */
     size_t n = (size_t)channels * h * w;
     float *zc = (float *)malloc(n * sizeof(float));
-    if (!zc) return NULL;
-    memcpy(zc, z, n * sizeof(float));
-    for (int i = 0; i < num_steps; i++) {
-        if (iris_cancel_requested) { free(zc); return NULL; }
+    float *dz = (float *)iris_hip_malloc(3 * n * sizeof(float));
+    if (!zc || !dz) {
+        free(zc);
+        iris_hip_free(dz);
+        return NULL;
+    }
+    float *dvu = dz + n, *dvc = dz + 2 * n;
+    int ok = iris_hip_memcpy_h2d(dz, z, n * sizeof(float)) == 0;
+    for (int i = 0; ok && i < num_steps; i++) {
+        if (iris_step_callback) iris_step_callback(i + 1, num_steps);
+        if (iris_cancel_requested || iris_hip_memcpy_d2h(zc, dz, n * sizeof(float))) { ok = 0; break; }
         float *vu = iris_transformer_forward(tf, zc, h, w, text_emb_uncond, text_seq_uncond, schedule[i]);
         float *vc = vu ? iris_transformer_forward(tf, zc, h, w, text_emb_cond, text_seq_cond, schedule[i]) : NULL;
-        if (!vu || !vc) { free(vu); free(vc); free(zc); return NULL; }
-        float dt = schedule[i + 1] - schedule[i];
-        for (size_t j = 0; j < n; j++) zc[j] += dt * (vu[j] + guidance_scale * (vc[j] - vu[j]));
-        free(vu); free(vc);
-        if (progress_callback) progress_callback(i + 1, num_steps);
+        ok = vu && vc && !iris_hip_memcpy_h2d(dvu, vu, n * sizeof(float)) &&
+             !iris_hip_memcpy_h2d(dvc, vc, n * sizeof(float)) &&
+             !iris_hip_euler(dz, dvu, dvc, guidance_scale, schedule[i + 1] - schedule[i], 1.0f, n) &&
+             !iris_hip_sync();
+        free(vu);
+        free(vc);
+        if (ok && progress_callback) progress_callback(i + 1, num_steps);
+    }
+    if (ok && iris_hip_memcpy_d2h(zc, dz, n * sizeof(float))) ok = 0;
+    iris_hip_free(dz);
+    if (!ok) {
+        free(zc);
+        return NULL;
     }
     return zc;
 }
@@ -206,6 +225,7 @@ float *iris_sample_euler_zimage(void *transformer, float *z, int batch, int chan
     }
     if (zi_prepare(tf, h, w, cap_seq) || zi_upload(tf, z, cap_feats)) return NULL;
     for (int i = 0; i < num_steps; i++) {
+        if (iris_step_callback) iris_step_callback(i + 1, num_steps);
         if (iris_cancel_requested) return NULL;
         if (zi_step(tf, schedule[i], schedule[i + 1])) return NULL;
         if (progress_callback) progress_callback(i + 1, num_steps);

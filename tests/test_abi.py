@@ -22,13 +22,21 @@ def declared_functions():
         text = re.sub(r"^\s*#[^\n]*", " ", text, flags=re.M)
         # statements at file scope: the C++ linkage wrapper, then struct/enum bodies removed
         text = text.replace('extern "C" {', " ")
-        text = re.sub(r"\{[^{}]*\}", " ", text)
+        while True:
+            stripped = re.sub(r"\{[^{}]*\}", ";", text)     # a body ends a statement
+            if stripped == text:
+                break
+            text = stripped
         text = text.replace("}", " ")
         for stmt in text.split(";"):
             s = " ".join(stmt.split())
-            if not s or s.startswith("typedef") or s.startswith("extern \"C\""):
+            if not s or s.startswith(("typedef", "static", "extern \"C\"")):
                 continue
             m = re.match(r"^(?:extern\s+)?[A-Za-z_][\w\s\*]*?[\s\*](\w+)\s*\((.*)\)$", s)
+            if m:
+                names.setdefault(fn, []).append(m.group(1))
+                continue
+            m = re.match(r"^extern\s+[A-Za-z_][\w\s\*]*?[\s\*](\w+)$", s)   # exported variables
             if m:
                 names.setdefault(fn, []).append(m.group(1))
     return names
@@ -42,7 +50,9 @@ def test_headers_parsed():
     assert "iris_hip_gemm" in DECLS["iris_hip.h"]
     assert "iris_transformer_forward" in DECLS["iris_transformer.h"]
     assert "zi_transformer_forward" in DECLS["iris_transformer.h"]
-    assert sum(len(v) for v in DECLS.values()) > 60
+    assert "iris_conv2d" in DECLS["iris_kernels.h"] and "iris_substep_callback" in DECLS["iris_kernels.h"]
+    assert "fast_expf" not in DECLS["iris_kernels.h"]          # static inline, not exported
+    assert sum(len(v) for v in DECLS.values()) > 90
 
 
 @pytest.mark.parametrize("header", sorted(DECLS))
