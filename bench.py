@@ -87,8 +87,8 @@ def time_launches(lib, fn, n=30, warm=3):
     return lib.iris_hip_event_elapsed_ms(2, 3) / n
 
 
-def kernel_entry(name, ms, flops, per_step):
-    return {"kernel": name, "launch_ms": round(ms, 4), "flop_per_launch": flops,
+def kernel_entry(name, ms, flops, per_step, key=None):
+    return {"kernel": name, "key": key, "launch_ms": round(ms, 4), "flop_per_launch": flops,
             "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4), "launches_per_step": per_step,
             "ms_per_step": round(ms * per_step, 3)}
@@ -140,9 +140,9 @@ def run_flux(lib, c, args):
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
     wdev.close()
     kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_ms,
-                            2.0 * BS * h * (3 * h + 2 * mlp), c["ns"]),
+                            2.0 * BS * h * (3 * h + 2 * mlp), c["ns"], f"gemm_fused_{args.config}"),
                kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_ms, 4.0 * B * S * S * h,
-                            c["nd"] + c["ns"])]
+                            c["nd"] + c["ns"], f"attn_{args.config}")]
     lib.iris_transformer_free(tf)
     cfg = {"workload": c["workload"], "hidden": h, "heads": H, "double_blocks": c["nd"], "single_blocks": c["ns"],
            "image_tokens": I0, "reference_tokens": S - I0 - c["T"], "text_tokens": c["T"], "seq": S, "batch": B,
@@ -203,6 +203,67 @@ def run_zimage(lib, c, args):
     return ms_step, wall, zimage_flops(c), kernels, cfg, t_load
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_rocprof_pmc.md")
+
+
+def measured_traffic(key):
+    """HBM-side bytes per launch of a kernel class, from the committed
+    FETCH_SIZE / WRITE_SIZE counter runs (lines `traffic <key>: <bytes>`), or
+    None when that class has not been measured."""
+    if not key or not os.path.exists(TRAFFIC_FILE):
+        return None
+    for line in open(TRAFFIC_FILE):
+        line = line.strip().strip("`")
+        if line.startswith(f"traffic {key}:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def probe(kind, n):
+    """Launch one kernel class n times on synthetic NS-shaped buffers (the
+    program that the counter runs profile): `gemm` = the single-block fused
+    projection GEMM, `attn` = the joint attention, `copy` = a 1 GiB
+    device-to-device copy (the calibration kernel of known size)."""
+    lib = tl.hip()
+    c = CONFIGS["ns"]
+    h, H, mlp = c["h"], c["H"], 3 * c["h"]
+    S = c["ih"] * c["iw"] + c["T"]
+    S_pad = (S + 63) // 64 * 64
+    bufs = []
+
+    def dev(nbytes, seed=None, scale=1.0):
+        d = tl.Dev(nbytes)
+        if seed is not None:
+            d.put(tl.to_bf16(tl.synth_f32((nbytes // 2,), seed, 0, scale)))
+        bufs.append(d)
+        return d.ptr
+
+    if kind == "gemm":
+        a, w = dev(S * h * 2, 3), dev((3 * h + 2 * mlp) * h * 2, 9, 0.02)
+        qkv, cat = dev(S * 3 * h * 2), dev(S * (h + mlp) * 2)
+        P = tl.GemmProblem
+        probs = (P * 2)(P(a, w, qkv, None, S, 3 * h, h, h, h, 3 * h, 1),
+                        P(a, w + 3 * h * h * 2, cat + h * 2, None, S, 2 * mlp, h, h, h, h + mlp, 3))
+        fn = lambda: lib.iris_hip_gemm(probs, 2)  # noqa: E731
+        alg = 2 * S * h + 2 * (3 * h + 2 * mlp) * h + 2 * S * (3 * h + mlp)
+    elif kind == "attn":
+        q, k = dev(S * h * 2, 11), dev(S * h * 2, 12)
+        vt, o = dev(H * 128 * S_pad * 2, 13), dev(S * (h + mlp) * 2)
+        at = tl.AttnArgs(q, k, vt, o, h, h, S_pad, h + mlp, S, S, H, 1, 0, 0, 0, 0, 1.0 / np.sqrt(128.0), 0, S, 0, 0)
+        fn = lambda: lib.iris_hip_attention(ctypes.byref(at))  # noqa: E731
+        alg = 2 * 4 * S * h
+    else:
+        nb = 1 << 30
+        src, dst = dev(nb), dev(nb)
+        lib.iris_hip_memcpy_d2d.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+        fn = lambda: lib.iris_hip_memcpy_d2d(dst, src, nb)  # noqa: E731
+        alg = 2 * nb
+    for _ in range(n):
+        assert fn() == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    print(json.dumps({"probe": kind, "launches": n, "algorithmic_bytes_per_launch": alg}))
+
+
 def timed_steps(lib, step, args):
     for i in range(args.warmup):
         step(i)
@@ -224,11 +285,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="ns", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--probe", choices=["gemm", "attn", "copy"],
+                    help="only launch one kernel class a few times (for counter runs)")
+    ap.add_argument("--probe-launches", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(multi-GPU sharding is a design, not a code path, here)", file=sys.stderr)
         sys.exit(2)
+    if args.probe:
+        probe(args.probe, args.probe_launches)
+        return
     c = CONFIGS[args.config]
     lib = tl.hip()
     run = run_flux if c["kind"] == "flux" else run_zimage
@@ -256,7 +323,8 @@ def main():
         "wall_ms_per_step": round(wall_ms, 4),
         "model_create_s": round(t_load, 1),
         "roofline": {"kernel": dom["kernel"], "bound": "mfma", "achieved": dom["achieved_tflops"],
-                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": dom["frac"], "traffic": None,
+                     "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s", "frac": dom["frac"],
+                     "traffic": measured_traffic(dom["key"]),
                      "launch_ms": dom["launch_ms"], "flop_per_launch": dom["flop_per_launch"]},
         "kernels": kernels,
         "device": lib.iris_hip_device_name().decode(),
