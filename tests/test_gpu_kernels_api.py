@@ -319,3 +319,112 @@ def test_progress_callbacks(lib):
     assert steps == [(1, 2), (2, 2)]
     one = [(0, i, 2) for i in range(2)] + [(1, i, 3) for i in range(3)] + [(2, 0, 1)]
     assert seen == one * 2
+
+
+# ---------------------------------------------------------------- the reference's own known answers
+
+def test_reference_known_answers(lib):
+    """The known-answer cases of debug/test_kernels.c:54-305 (inputs, expected
+    values and tolerances as the reference states them), through the HIP build."""
+    keep = []
+
+    def a(*v):
+        """a float32 array kept alive for the whole test (its address is passed to C)"""
+        keep.append(np.array(v, np.float32))
+        return keep[-1]
+
+    x = a(1, 2, 3, 4)                                        # :54-64
+    lib.iris_softmax_cpu(p(x), 1, 4)
+    assert abs(x.sum() - 1) < 1e-5 and np.all(x > 0) and x[3] > x[2] > x[1] > x[0]
+    x = a(5, 5, 5, 5)                                        # :66-74
+    lib.iris_softmax_cpu(p(x), 1, 4)
+    np.testing.assert_allclose(x, 0.25, atol=1e-5)
+    x = a(1000, 1001, 1002)                                  # :76-83
+    lib.iris_softmax_cpu(p(x), 1, 3)
+    assert abs(x.sum() - 1) < 1e-5 and np.all(np.isfinite(x))
+    x = a(1, 2, 3, 1)                                        # :85-94
+    lib.iris_softmax_cpu(p(x), 2, 2)
+    assert abs(x[0] + x[1] - 1) < 1e-5 and abs(x[2] + x[3] - 1) < 1e-5 and x[2] > x[3]
+    x = a(0, 1)                                              # :96-103
+    lib.iris_softmax_cpu(p(x), 1, 2)
+    e = np.exp(np.float32(1))
+    np.testing.assert_allclose(x, [1 / (1 + e), e / (1 + e)], atol=1e-5)
+
+    out = np.empty(2, np.float32)                            # :109-120
+    lib.iris_rms_norm(p(out), p(a(3, 4)), p(a(1, 1)), 1, 2, 1e-6)
+    rms = np.sqrt(np.float32(12.5) + np.float32(1e-6))
+    np.testing.assert_allclose(out, [3 / rms, 4 / rms], atol=1e-5)
+    out = np.empty(4, np.float32)                            # :122-131
+    lib.iris_rms_norm(p(out), p(a(1, 1, 1, 1)), p(a(2, 2, 2, 2)), 1, 4, 1e-6)
+    np.testing.assert_allclose(out, 2.0, atol=1e-4)
+    out = np.empty(2, np.float32)                            # :133-142
+    lib.iris_rms_norm(p(out), p(a(0, 0)), p(a(1, 1)), 1, 2, 1e-5)
+    assert np.all(np.isfinite(out))
+    out = np.empty(4, np.float32)                            # :144-159
+    lib.iris_rms_norm(p(out), p(a(3, 4, 1, 0)), p(a(1, 1)), 2, 2, 1e-6)
+    r0, r1 = np.sqrt(12.5 + 1e-6), np.sqrt(0.5 + 1e-6)
+    np.testing.assert_allclose(out, [3 / r0, 4 / r0, 1 / r1, 0], atol=1e-4)
+
+    C = np.empty(4, np.float32)                              # :165-177
+    lib.iris_matmul(p(C), p(a(1, 2, 3, 4)), p(a(1, 0, 0, 1)), 2, 2, 2)
+    np.testing.assert_allclose(C, [1, 2, 3, 4], atol=1e-5)
+    C1 = np.empty(1, np.float32)                             # :179-186
+    lib.iris_matmul(p(C1), p(a(1, 2)), p(a(5, 6)), 1, 2, 1)
+    assert abs(C1[0] - 17) < 1e-4
+    lib.iris_matmul(p(C), p(a(1, 2, 3, 4, 5, 6)), p(a(7, 8, 9, 10, 11, 12)), 2, 3, 2)   # :188-202
+    np.testing.assert_allclose(C, [58, 64, 139, 154], atol=1e-3)
+    lib.iris_matmul_t(p(C), p(a(1, 0, 0, 0, 1, 0)), p(a(1, 0, 0, 0, 1, 0)), 2, 3, 2)   # :204-217
+    np.testing.assert_allclose(C, [1, 0, 0, 1], atol=1e-5)
+
+    x = a(0, 1, -1)                                          # :223-232
+    lib.iris_silu(p(x), 3)
+    np.testing.assert_allclose(x, [0, 0.7310586, -0.2689414], atol=1e-4)
+    g = a(1, 0)                                              # :234-240
+    lib.iris_silu_mul(p(g), p(a(2, 3)), 2)
+    np.testing.assert_allclose(g, [0.7310586 * 2, 0], atol=1e-4)
+
+    x = a(1, 2, 3)                                           # :246-254
+    lib.iris_axpy(p(x), 2.0, p(a(4, 5, 6)), 3)
+    np.testing.assert_allclose(x, [9, 12, 15], atol=1e-5)
+    out = np.empty(2, np.float32)                            # :256-263
+    lib.iris_add(p(out), p(a(1, 2)), p(a(3, 4)), 2)
+    np.testing.assert_allclose(out, [4, 6], atol=1e-5)
+
+    src = np.arange(32, dtype=np.float32)                    # :269-292
+    pt, back = np.empty(32, np.float32), np.empty(32, np.float32)
+    lib.iris_patchify(p(pt), p(src), 1, 2, 4, 4, 2)
+    lib.iris_unpatchify(p(back), p(pt), 1, 2, 2, 2, 2)
+    np.testing.assert_array_equal(back, src)
+    src = np.arange(1, 13, dtype=np.float32)                 # :294-305
+    out = np.empty(12, np.float32)
+    lib.iris_patchify(p(out), p(src), 1, 3, 2, 2, 1)
+    np.testing.assert_array_equal(out, src)
+
+
+def test_reference_attention_parity_cases(lib):
+    """debug/test_kernels.c:392-524: naive (iris_attention) and seq-major
+    (iris_flash_attention) layouts agree (mean < 1e-3, max < 5e-3), on the
+    reference's shapes and seeds, plus the identity-V case."""
+    for heads, sq, sk, hd, seed in ((1, 8, 12, 16, 12345), (4, 16, 16, 8, 99999), (1, 96, 128, 8, 77777)):
+        lib.iris_rng_seed(seed)
+        q = np.empty(sq * heads * hd, np.float32)
+        k = np.empty(sk * heads * hd, np.float32)
+        v = np.empty(sk * heads * hd, np.float32)
+        for arr in (q, k, v):
+            lib.iris_randn(p(arr), arr.size)
+        scale = 1.0 / np.sqrt(hd)
+        to_naive = lambda t, s: np.ascontiguousarray(t.reshape(s, heads, hd).transpose(1, 0, 2))  # noqa: E731
+        qn, kn, vn = to_naive(q, sq), to_naive(k, sk), to_naive(v, sk)
+        out_n = np.empty(heads * sq * hd, np.float32)
+        out_f = np.empty(sq * heads * hd, np.float32)
+        lib.iris_attention(p(out_n), p(qn), p(kn), p(vn), 1, heads, sq, sk, hd, scale)
+        lib.iris_flash_attention(p(out_f), p(q), p(k), p(v), sq, sk, heads, hd, scale)
+        d = np.abs(out_n - to_naive(out_f, sq).ravel())
+        assert d.mean() < 1e-3 and d.max() < 5e-3
+        ref = attn_ref(qn, kn, vn, scale).ravel()
+        np.testing.assert_allclose(out_n, ref, rtol=1e-4, atol=2e-6)
+    eye = np.eye(4, dtype=np.float32).ravel()
+    on, of = np.empty(16, np.float32), np.empty(16, np.float32)
+    lib.iris_attention(p(on), p(eye), p(eye), p(eye), 1, 1, 4, 4, 4, 0.5)
+    lib.iris_flash_attention(p(of), p(eye), p(eye), p(eye), 4, 4, 1, 4, 0.5)
+    assert np.abs(on - of).mean() < 1e-5 and of[0] > of[1] and of[5] > of[4]
