@@ -7,19 +7,21 @@
  * iris_kernels.c:626-638, the split/concat copies :3833-3840, :3897-3902).
  *
  * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
- * a 4x2 arrangement (2 waves per SIMD); each wave owns 64x128 as 2x4
+ * a 4x2 arrangement (2 waves per SIMD, so one wave's MFMAs run while the other
+ * waits on LDS or on a load's issue); each wave owns 64x128 as 2x4
  * v_mfma_f32_32x32x16_bf16 tiles and reads the next 16-wide K slice's operand
  * fragments from LDS while the current slice's MFMAs run.
  *
- * A and W stream through two 64 KiB LDS stages. Each thread stages 4 16-byte
- * chunks per operand in registers: in K-step t, after the first half of the
- * MFMAs, it writes the chunks of tile t+1 (loaded during step t-1) into the
- * stage that step t-1 read, then reloads the registers with tile t+2, so
- * global latency is covered by a whole K-step and the LDS writes overlap
- * matrix work. LDS serves a 16-byte-per-lane read 16 lanes at a time over 64
- * banks: a group reads rows r..r+15 at one logical 16-byte chunk, and XOR with
- * (row / 2) mod 8 puts those rows on 16 distinct (row parity, chunk) bank
- * groups.
+ * A and W stream through two 64 KiB LDS stages filled by LDS-DMA
+ * (buffer_load ... lds): global data goes straight into LDS, with no staging
+ * registers and no ds_write, whose data FIFO limited the register-staged
+ * version. Each row of a stage is a full 128-byte line of the operand, so
+ * every request to HBM fetches whole lines. The stages are separate
+ * __shared__ objects, which lets the compiler wait only for the DMA of the
+ * stage it reads. LDS serves a 16-byte-per-lane read 16 lanes at a time over
+ * 64 banks: a group reads rows r..r+15 at one logical 16-byte chunk, and XOR
+ * with (row / 2) mod 8 puts those rows on 16 distinct (row parity, chunk)
+ * bank groups.
  *
  * Loads use buffer resources whose range ends at the operand's last valid row,
  * so rows past M (or N) read as zero without predicates. Blocks are mapped
@@ -37,9 +39,9 @@ constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M, TW_N = BN / WAVES_N;
 constexpr int FM = TW_M / 32, FN = TW_N / 32;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
-constexpr size_t SMEM_BYTES = 2 * 2 * TILE_ELEMS * sizeof(uint16_t);
-constexpr int CH = BM * (BK / 8) / NT;              /* 16-byte chunks per operand per thread = 4 */
-constexpr int ROWS_PER = NT / 8;                    /* rows covered by one chunk sweep = 64 */
+constexpr int NWAVES = NT / 64;
+constexpr int DMA_ROWS = 8;                         /* rows of one 64-lane x 16-byte LDS-DMA load */
+constexpr int DMA_PER_OPND = BM / DMA_ROWS / NWAVES; /* per wave per operand per K-step = 4 */
 constexpr int GROUP_M = 8;
 constexpr int MAXP = 4;
 
@@ -53,8 +55,18 @@ __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in 
     return row * BK + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
 
+/* s_waitcnt immediate: vmcnt in bits 3:0 and 15:14, expcnt 6:4 (no wait),
+ * lgkmcnt 11:8 */
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+    /* two stages, each an A tile then a W tile; separate objects so the
+     * compiler tracks the LDS-DMA writes of one stage apart from reads of
+     * the other */
+    __shared__ __attribute__((aligned(16))) uint16_t lds0[2 * TILE_ELEMS];
+    __shared__ __attribute__((aligned(16))) uint16_t lds1[2 * TILE_ELEMS];
     const int b = blockIdx.x;
     const int L = (b & 7) * P.per_xcd + (b >> 3);
     if (L >= P.total) return;
@@ -73,13 +85,16 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int lr = lane & 31, lg = lane >> 5;
 
-    /* 32-bit byte offsets relative to the tile's first row: one VGPR offset
-     * per operand plus a uniform per-chunk row step */
-    const int ld_row = tid >> 3, ld_ch = tid & 7;
+    /* LDS-DMA: load j of an operand covers tile rows 8j..8j+7 and writes
+     * 1 KiB at byte j*1024 of the operand's tile, lane l at + 16l, i.e. row
+     * 8j + l/8, stored chunk l%8. The lane fetches the global chunk that the
+     * swizzle puts there: chunk (l%8) ^ ((row >> 1) & 7), which depends on j
+     * only through j's parity. Rows past M (N) read as zero through the
+     * buffer range. */
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
     const int a_rows = min(BM, pr.M - m0), w_rows = min(BN, pr.N - n0);
@@ -87,26 +102,25 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         (void *)a_base, (short)0, a_rows * pr.lda * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)w_base, (short)0, w_rows * pr.ldw * 2, 0x00020000);
-    const int a_off = (ld_row * pr.lda + ld_ch * 8) * 2, w_off = (ld_row * pr.ldw + ld_ch * 8) * 2;
-    const int a_step = ROWS_PER * pr.lda * 2, w_step = ROWS_PER * pr.ldw * 2;
-    uint4 ra[CH], rw[CH];
-
-    auto gload = [&](int kt) {
+    const int drow = lane >> 3, dch = lane & 7;
+    int a_voff[2], w_voff[2];
+#pragma unroll
+    for (int par = 0; par < 2; par++) {
+        const int c = dch ^ ((4 * par + (drow >> 1)) & 7);
+        const int row = wave * DMA_PER_OPND * DMA_ROWS + drow;    /* first load of this wave */
+        a_voff[par] = (row * pr.lda + c * 8) * 2;
+        w_voff[par] = (row * pr.ldw + c * 8) * 2;
+    }
+    const int a_step = DMA_ROWS * pr.lda * 2, w_step = DMA_ROWS * pr.ldw * 2;
+    auto dma = [&](uint16_t *stage, int kt) {
         const int k0 = kt * BK * 2;
 #pragma unroll
-        for (int i = 0; i < CH; i++) {
-            ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off + k0, i * a_step, 0));
-            rw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off + k0, i * w_step, 0));
-        }
-    };
-    auto sstore = [&](int buf) {
-        uint16_t *As = smem + buf * 2 * TILE_ELEMS;
-        uint16_t *Ws = As + TILE_ELEMS;
-#pragma unroll
-        for (int i = 0; i < CH; i++) {
-            const int r = ld_row + ROWS_PER * i;
-            *(uint4 *)(As + swz(r, ld_ch)) = ra[i];
-            *(uint4 *)(Ws + swz(r, ld_ch)) = rw[i];
+        for (int i = 0; i < DMA_PER_OPND; i++) {
+            const int j = wave * DMA_PER_OPND + i;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + j * 512), 16,
+                                                     a_voff[i & 1] + i * a_step, k0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void *)(stage + TILE_ELEMS + j * 512), 16,
+                                                     w_voff[i & 1] + i * w_step, k0, 0, 0);
         }
     };
 
@@ -119,41 +133,78 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
     const int nk = pr.K / BK;
-    gload(0);
-    sstore(0);
-    if (nk > 1) gload(1);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const uint16_t *As = smem + (kt & 1) * 2 * TILE_ELEMS;
-        const uint16_t *Ws = As + TILE_ELEMS;
-        bf16x8 a[2][FM], w[2][FN];
-        auto frag = [&](int kk, int buf) {
-            const int ch = kk * 2 + lg;
+    bf16x8 a[2][FM], w[2][FN];
+    auto frag = [&](const uint16_t *stage, int kk, int buf) {
+        const uint16_t *As = stage;
+        const uint16_t *Ws = stage + TILE_ELEMS;
+        const int ch = kk * 2 + lg;
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++)
-                a[buf][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch));
+        for (int mi = 0; mi < FM; mi++) a[buf][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch));
+#pragma unroll
+        for (int ni = 0; ni < FN; ni++) w[buf][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch));
+    };
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int mi = 0; mi < FM; mi++)
 #pragma unroll
             for (int ni = 0; ni < FN; ni++)
-                w[buf][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch));
-        };
-        frag(0, 0);
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[buf][mi], w[buf][ni], acc[mi][ni], 0, 0, 0);
+    };
+    /* FM + FN fragment reads spread over FM * FN MFMAs */
+    auto sched_reads = [&]() {
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            if (kk + 1 < BK / 16) frag(kk + 1, (kk + 1) & 1);
-#pragma unroll
-            for (int mi = 0; mi < FM; mi++)
-#pragma unroll
-                for (int ni = 0; ni < FN; ni++)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][mi], w[kk & 1][ni],
-                                                                          acc[mi][ni], 0, 0, 0);
-            if (kk == 1) {
-                /* the stage read in step kt-1 is free (barrier); tile kt+1 goes there */
-                if (kt + 1 < nk) sstore((kt + 1) & 1);
-                if (kt + 2 < nk) gload(kt + 2);
-            }
+        for (int i = 0; i < FM + FN; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
-        __syncthreads();
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
+    };
+
+    /* K-step t reads stage t&1. Slice 0 of the step is read during slice 3
+     * of the previous step; slices 1..3 one slice ahead of their MFMAs. The
+     * DMA of tile t+1 into the other stage was issued in slice 3 of step t-1;
+     * before slice 3 each wave waits for its own DMA and its LDS reads, and the
+     * barrier makes the whole tile visible and the current stage free, so
+     * slice 3 issues the DMA of tile t+2 into the current stage and reads
+     * slice 0 of tile t+1. Past the last tile the DMA repeats tile nk-1 into a
+     * stage nothing reads. */
+    auto kstep = [&](uint16_t *cur, uint16_t *nxt, int kt) {
+        frag(cur, 1, 1);
+        mfmas(0);
+        sched_reads();
+        frag(cur, 2, 0);
+        mfmas(1);
+        sched_reads();
+        frag(cur, 3, 1);
+        mfmas(0);
+        sched_reads();
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        __builtin_amdgcn_s_barrier();
+        dma(cur, min(kt + 2, nk - 1));
+        frag(nxt, 0, 0);
+        mfmas(1);
+#pragma unroll
+        for (int i = 0; i < FM + FN; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x020, 2 * DMA_PER_OPND - (FM + FN), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
+    };
+
+    dma(lds0, 0);
+    dma(lds1, min(1, nk - 1));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * DMA_PER_OPND, 15));   /* tile 0 landed */
+    __builtin_amdgcn_s_barrier();
+    frag(lds0, 0, 0);
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+        kstep(lds0, lds1, kt);
+        kstep(lds1, lds0, kt + 1);
     }
+    if (kt < nk) kstep(lds0, lds1, kt);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));   /* no DMA outstanding at exit */
 
     /* ---- epilogue: lane holds column lr of each 32x32 tile, rows
      *      (r>>2)*8 + lg*4 + (r&3) ---- */
@@ -267,8 +318,6 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
 }
 
-bool g_attr_set = false;
-
 }  // namespace
 
 extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
@@ -302,13 +351,6 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    if (!g_attr_set) {
-        if (iris_check(hipFuncSetAttribute((const void *)gemm_bf16_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_BYTES),
-                       "gemm smem attribute"))
-            return -1;
-        g_attr_set = true;
-    }
-    hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), SMEM_BYTES, iris_stream(), P);
+    hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
 }
