@@ -183,6 +183,11 @@ void iris_linear_nobias_bf16(float *y, const float *x, const uint16_t *W_bf16, i
  *      with the pixel range cut into chunks that bound the im2col buffer ---- */
 void iris_conv2d(float *out, const float *in, const float *weight, const float *bias, int batch, int in_ch,
                  int out_ch, int H, int W, int kH, int kW, int stride, int padding) {
+    if (stride <= 0 || kH <= 0 || kW <= 0 || in_ch <= 0 || padding < 0) {
+        fprintf(stderr, "iris_kernels (HIP): iris_conv2d: invalid geometry (in_ch %d, kernel %dx%d, stride %d, "
+                        "padding %d)\n", in_ch, kH, kW, stride, padding);
+        return;
+    }
     const int oH = (H + 2 * padding - kH) / stride + 1, oW = (W + 2 * padding - kW) / stride + 1;
     if (batch <= 0 || out_ch <= 0 || oH <= 0 || oW <= 0) return;
     const int npix = oH * oW, K = in_ch * kH * kW, Kp = pad64(K);
@@ -243,8 +248,8 @@ void iris_rms_norm(float *out, const float *x, const float *weight, int seq_len,
 
 void iris_group_norm(float *out, const float *x, const float *gamma, const float *beta, int batch, int channels,
                      int H, int W, int num_groups, float eps) {
+    if (batch <= 0 || channels <= 0 || H <= 0 || W <= 0) return;
     const size_t n = (size_t)batch * channels * H * W;
-    if (!n) return;
     float *dx = up(SLOT_A, x, n), *dg = up(SLOT_B, gamma, (size_t)channels), *db = up(SLOT_D, beta, (size_t)channels);
     float *dout = (float *)slot(SLOT_C, n * sizeof(float));
     if (!dx || !dg || !db || !dout ||
@@ -254,8 +259,8 @@ void iris_group_norm(float *out, const float *x, const float *gamma, const float
 
 void iris_batch_norm(float *out, const float *x, const float *running_mean, const float *running_var,
                      const float *gamma, const float *beta, int batch, int channels, int H, int W, float eps) {
+    if (batch <= 0 || channels <= 0 || H <= 0 || W <= 0) return;
     const size_t n = (size_t)batch * channels * H * W;
-    if (!n) return;
     float *dx = up(SLOT_A, x, n);
     /* the four per-channel vectors share one slot */
     float *dv = (float *)slot(SLOT_B, (size_t)4 * channels * sizeof(float));
@@ -281,8 +286,8 @@ void iris_softmax_cpu(float *x, int rows, int cols) { softmax_rows("iris_softmax
 /* ---- attention ---- */
 void iris_attention(float *out, const float *Q, const float *K, const float *V, int batch, int heads, int seq_q,
                     int seq_k, int head_dim, float scale) {
+    if (batch <= 0 || heads <= 0 || seq_q <= 0 || seq_k <= 0 || head_dim <= 0) return;
     const size_t nq = (size_t)batch * heads * seq_q * head_dim, nk = (size_t)batch * heads * seq_k * head_dim;
-    if (!nq) return;
     float *dq = up(SLOT_A, Q, nq), *dk = up(SLOT_B, K, nk), *dv = up(SLOT_D, V, nk);
     float *dout = (float *)slot(SLOT_C, nq * sizeof(float));
     const long long q_sh = (long long)seq_q * head_dim, k_sh = (long long)seq_k * head_dim;
@@ -295,8 +300,8 @@ void iris_attention(float *out, const float *Q, const float *K, const float *V, 
 
 void iris_flash_attention(float *out, const float *Q, const float *K, const float *V, int seq_q, int seq_k,
                           int heads, int head_dim, float scale) {
+    if (heads <= 0 || seq_q <= 0 || seq_k <= 0 || head_dim <= 0) return;
     const size_t nq = (size_t)seq_q * heads * head_dim, nk = (size_t)seq_k * heads * head_dim;
-    if (!nq) return;
     float *dq = up(SLOT_A, Q, nq), *dk = up(SLOT_B, K, nk), *dv = up(SLOT_D, V, nk);
     float *dout = (float *)slot(SLOT_C, nq * sizeof(float));
     if (!dq || !dk || !dv || !dout ||
@@ -309,8 +314,8 @@ void iris_flash_attention(float *out, const float *Q, const float *K, const floa
 /* ---- reshapes ---- */
 void iris_upsample_nearest(float *out, const float *in, int batch, int channels, int H, int W, int scale_h,
                            int scale_w) {
+    if (batch <= 0 || channels <= 0 || H <= 0 || W <= 0 || scale_h <= 0 || scale_w <= 0) return;
     const size_t nin = (size_t)batch * channels * H * W, nout = nin * scale_h * scale_w;
-    if (!nout) return;
     float *din = up(SLOT_A, in, nin);
     float *dout = (float *)slot(SLOT_C, nout * sizeof(float));
     if (!din || !dout || iris_hip_upsample_nearest(dout, din, batch * channels, H, W, scale_h, scale_w) ||
@@ -319,8 +324,8 @@ void iris_upsample_nearest(float *out, const float *in, int batch, int channels,
 }
 
 void iris_patchify(float *out, const float *in, int batch, int channels, int H, int W, int patch_size) {
+    if (batch <= 0 || channels <= 0 || H <= 0 || W <= 0) return;
     const size_t n = (size_t)batch * channels * H * W;
-    if (!n) return;
     float *din = up(SLOT_A, in, n);
     float *dout = (float *)slot(SLOT_C, n * sizeof(float));
     if (!din || !dout || iris_hip_space_to_depth(dout, din, batch, channels, H, W, patch_size, 0) ||
@@ -330,6 +335,7 @@ void iris_patchify(float *out, const float *in, int batch, int channels, int H, 
 
 void iris_unpatchify(float *out, const float *in, int batch, int channels, int H, int W, int patch_size) {
     const int p = patch_size;
+    if (p <= 0 || batch <= 0 || channels <= 0 || H <= 0 || W <= 0) return;
     const size_t n = (size_t)batch * channels * p * p * H * W;
     if (!n) return;
     float *din = up(SLOT_A, in, n);
