@@ -314,6 +314,42 @@ def test_9b_cfg_step_reduced_depth(lib, orc):
     orc.orc_flux_free(m)
 
 
+@pytest.mark.parametrize("h,w,T", [(6, 10, 77), (3, 5, 1), (13, 7, 130)])
+def test_ragged_geometry_vs_oracle(lib, orc, tiny, tiny_orc, h, w, T):
+    """Non-square latents and text lengths that are not multiples of 4, 8 or 64
+    (sequence ends inside a key tile, a GEMM row tile and a V^T 4-row group),
+    down to one text token: forward vs the oracle."""
+    lat, txt = tl.synth_f32((128, h, w), 90 + h), tl.synth_f32((T, 256), 91 + T)
+    n = 128 * h * w
+    got = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), h, w, tl.fptr(txt), T, F(0.45)), n)
+    ref = tl.take_f32(orc, orc.orc_flux_forward(tiny_orc, tl.fptr(lat), h, w, tl.fptr(txt), T, F(0.45)), n)
+    assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+
+
+def test_4b_large_geometry_properties(lib):
+    """4B widths, 1 double + 1 single block, at 2048x2048 (16384 image tokens +
+    512 text, S = 16896): sizes where the oracle would take minutes, checked
+    through properties that hold at any size: finite, deterministic (two
+    forwards bit-identical), and the batch-2 CFG pass with equal texts equal
+    to z + dt * v of the single pass (rows of the two batch slots never mix)."""
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 1, 7680, 128, 3.0, 2000.0, 123))
+    assert tf.value, lib.iris_hip_last_error()
+    lat, txt = tl.synth_f32((128, 128, 128), 92), tl.synth_f32((512, 7680), 93)
+    n = 128 * 128 * 128
+    a = take(lib, lib.iris_transformer_forward(tf, tl.fptr(lat), 128, 128, tl.fptr(txt), 512, F(0.6)), n)
+    b = take(lib, lib.iris_transformer_forward(tf, tl.fptr(lat), 128, 128, tl.fptr(txt), 512, F(0.6)), n)
+    assert np.all(np.isfinite(a)) and a.std() > 0.1
+    np.testing.assert_array_equal(a, b)
+    sched = np.array([0.6, 0.35], np.float32)
+    lib.iris_sample_euler_cfg.argtypes = [ctypes.c_void_p, ctypes.c_void_p, tl.FP] + [ctypes.c_int] * 4 + [
+        tl.FP, ctypes.c_int, tl.FP, ctypes.c_int, ctypes.c_float, tl.FP, ctypes.c_int, ctypes.c_void_p]
+    z = take(lib, lib.iris_sample_euler_cfg(tf, None, tl.fptr(lat), 1, 128, 128, 128, tl.fptr(txt), 512, tl.fptr(txt),
+                                            512, 2.5, tl.fptr(sched), 1, None), n)
+    lib.iris_transformer_free(tf)
+    want = lat.ravel() + np.float32(0.35 - 0.6) * a
+    assert tl.rel_l2(z, want) < 1e-6
+
+
 def test_adapters_fail_loudly(lib, tiny):
     """Adapter setters link and take ownership; an attached adapter makes the
     forward fail (the HIP denoiser applies none) instead of being ignored."""
