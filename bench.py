@@ -290,8 +290,8 @@ def main():
     ap.add_argument("--probe-launches", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is a design, not a code path, here)", file=sys.stderr)
+        print(f"bench.py: runs on one GPU; --gpus {args.gpus} is not supported "
+              "(sharding across GPUs is designed, not implemented)", file=sys.stderr)
         sys.exit(2)
     if args.probe:
         probe(args.probe, args.probe_launches)

@@ -1,6 +1,6 @@
 """Flux.2-Klein denoiser parity: HIP build vs the oracle and the reference goldens.
 
-Bars (BASELINE north star): RoPE tables and token layout bit-exact; each
+Bars: RoPE tables and token layout bit-exact; each
 block's output within rel-L2 1e-2 of the f32 reference; final latents cosine
 >= 0.999. Blocks are also checked on their residual delta (out - in), which is
 the part the block computes, at rel-L2 3e-2.

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/liboracle.so) before it is trusted as the checker.
+"""Pins the oracle (oracle/liboracle.so) before the parity tests trust it.
 
 Three kinds of evidence, chosen so a plausible mistake fails one of them:
   * the reference's own outputs on identical seeded inputs (tests/golden/, made
