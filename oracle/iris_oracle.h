@@ -1,7 +1,7 @@
 /*
  * iris_oracle.h - CPU f32 restatement of the reference denoiser forward.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the parity checker and the CPU
+ * TEST INFRASTRUCTURE ONLY. This library is the parity oracle and the CPU
  * baseline: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it. The product (iris.c_amd/) never links or calls it.
  *

@@ -28,7 +28,7 @@ _libs = {}
 
 
 def oracle():
-    """The CPU checker (test infrastructure)."""
+    """The oracle: CPU restatement of the reference path (test infrastructure)."""
     if "oracle" not in _libs:
         lib = ctypes.CDLL(ORACLE_SO)
         lib.orc_flux_load.restype = ctypes.c_void_p
