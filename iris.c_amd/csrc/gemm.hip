@@ -7,21 +7,26 @@
  * iris_kernels.c:626-638, the split/concat copies :3833-3840, :3897-3902).
  *
  * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
- * a 4x2 arrangement (2 waves per SIMD, so one wave's MFMAs run while the other
- * waits on LDS or on a load's issue); each wave owns 64x128 as 2x4
- * v_mfma_f32_32x32x16_bf16 tiles and reads the next 16-wide K slice's operand
- * fragments from LDS while the current slice's MFMAs run.
+ * a 4x2 arrangement; each wave owns 64x128 as 4x8 v_mfma_f32_16x16x32_bf16
+ * tiles. The 16x16x32 form does the same work per LDS byte as 32x32x16 and,
+ * with the chip at its power limit on random data, sustains about 10 % more
+ * MFMA throughput.
+ *
+ * Waves w and w+4 share a SIMD. The two groups (waves 0..3, waves 4..7) run
+ * ping-pong: separated by block barriers, one group reads a whole 64-wide K
+ * step of operand fragments from LDS and issues loads while the other runs
+ * that step's 64 MFMAs, so every SIMD always has a wave issuing MFMAs and no
+ * MFMA waits behind a load that is waiting for the address unit.
  *
  * A and W stream through two 64 KiB LDS stages filled by LDS-DMA
  * (buffer_load ... lds): global data goes straight into LDS, with no staging
- * registers and no ds_write, whose data FIFO limited the register-staged
- * version. Each row of a stage is a full 128-byte line of the operand, so
- * every request to HBM fetches whole lines. The stages are separate
- * __shared__ objects, which lets the compiler wait only for the DMA of the
- * stage it reads. LDS serves a 16-byte-per-lane read 16 lanes at a time over
- * 64 banks: a group reads rows r..r+15 at one logical 16-byte chunk, and XOR
- * with (row / 2) mod 8 puts those rows on 16 distinct (row parity, chunk)
- * bank groups.
+ * registers and no ds_write. Each row of a stage is a full 128-byte line of
+ * the operand, so every request to HBM fetches whole lines. The stages are
+ * separate __shared__ objects, which lets the compiler wait only for the DMA
+ * of the stage it reads. LDS serves a 16-byte-per-lane read 16 lanes at a
+ * time over 64 banks: a group reads rows r..r+15 at one logical 16-byte chunk,
+ * and XOR with (row / 2) mod 8 puts those rows on 16 distinct (row parity,
+ * chunk) bank groups.
  *
  * Loads use buffer resources whose range ends at the operand's last valid row,
  * so rows past M (or N) read as zero without predicates. Blocks are mapped
@@ -37,11 +42,10 @@ namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
 constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M, TW_N = BN / WAVES_N;
-constexpr int FM = TW_M / 32, FN = TW_N / 32;
+constexpr int FM = TW_M / 16, FN = TW_N / 16;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
-constexpr int NWAVES = NT / 64;
 constexpr int DMA_ROWS = 8;                         /* rows of one 64-lane x 16-byte LDS-DMA load */
-constexpr int DMA_PER_OPND = BM / DMA_ROWS / NWAVES; /* per wave per operand per K-step = 4 */
+constexpr int DMA_PER_WAVE = BM / DMA_ROWS / 4;     /* loads per wave for one operand tile = 8 */
 constexpr int GROUP_M = 8;
 constexpr int MAXP = 4;
 
@@ -86,15 +90,18 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    /* waves w and w + 4 share SIMD w: group 0 (waves 0..3) and group 1
+     * (waves 4..7) alternate between an LDS phase and an MFMA phase */
+    const int grp = wave >> 2, gw = wave & 3;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int lr = lane & 31, lg = lane >> 5;
+    const int lr = lane & 15, lg = lane >> 4;
 
     /* LDS-DMA: load j of an operand covers tile rows 8j..8j+7 and writes
      * 1 KiB at byte j*1024 of the operand's tile, lane l at + 16l, i.e. row
-     * 8j + l/8, stored chunk l%8. The lane fetches the global chunk that the
-     * swizzle puts there: chunk (l%8) ^ ((row >> 1) & 7), which depends on j
-     * only through j's parity. Rows past M (N) read as zero through the
-     * buffer range. */
+     * 8j + l/8, stored chunk l%8; the lane fetches global chunk
+     * (l%8) ^ ((row >> 1) & 7), which depends on j only through its parity.
+     * Group 0 loads the A tiles and group 1 the W tiles; wave gw of a group
+     * issues loads j = 8gw..8gw+7. */
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
     const int a_rows = min(BM, pr.M - m0), w_rows = min(BN, pr.N - n0);
@@ -107,167 +114,154 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
     for (int par = 0; par < 2; par++) {
         const int c = dch ^ ((4 * par + (drow >> 1)) & 7);
-        const int row = wave * DMA_PER_OPND * DMA_ROWS + drow;    /* first load of this wave */
+        const int row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
         a_voff[par] = (row * pr.lda + c * 8) * 2;
         w_voff[par] = (row * pr.ldw + c * 8) * 2;
     }
     const int a_step = DMA_ROWS * pr.lda * 2, w_step = DMA_ROWS * pr.ldw * 2;
-    auto dma = [&](uint16_t *stage, int kt) {
-        const int k0 = kt * BK * 2;
+    auto dma_a = [&](uint16_t *stage, int kt) {
 #pragma unroll
-        for (int i = 0; i < DMA_PER_OPND; i++) {
-            const int j = wave * DMA_PER_OPND + i;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + j * 512), 16,
-                                                     a_voff[i & 1] + i * a_step, k0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void *)(stage + TILE_ELEMS + j * 512), 16,
-                                                     w_voff[i & 1] + i * w_step, k0, 0, 0);
-        }
+        for (int i = 0; i < DMA_PER_WAVE; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
+                                                     a_voff[i & 1] + i * a_step, kt * BK * 2, 0, 0);
+    };
+    auto dma_w = [&](uint16_t *stage, int kt) {
+#pragma unroll
+        for (int i = 0; i < DMA_PER_WAVE; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512), 16,
+                                                     w_voff[i & 1] + i * w_step, kt * BK * 2, 0, 0);
     };
 
-    f32x16 acc[FM][FN];
+    f32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
     const int nk = pr.K / BK;
+    /* fragments of one K-step: two 32-wide slices */
     bf16x8 a[2][FM], w[2][FN];
-    auto frag = [&](const uint16_t *stage, int kk, int buf) {
+    auto frags = [&](const uint16_t *stage) {
         const uint16_t *As = stage;
         const uint16_t *Ws = stage + TILE_ELEMS;
-        const int ch = kk * 2 + lg;
 #pragma unroll
-        for (int mi = 0; mi < FM; mi++) a[buf][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 32 + lr, ch));
+        for (int kk = 0; kk < 2; kk++) {
+            const int ch = kk * 4 + lg;
 #pragma unroll
-        for (int ni = 0; ni < FN; ni++) w[buf][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 32 + lr, ch));
-    };
-    auto mfmas = [&](int buf) {
+            for (int mi = 0; mi < FM; mi++) a[kk][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 16 + lr, ch));
 #pragma unroll
-        for (int mi = 0; mi < FM; mi++)
-#pragma unroll
-            for (int ni = 0; ni < FN; ni++)
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[buf][mi], w[buf][ni], acc[mi][ni], 0, 0, 0);
-    };
-    /* FM + FN fragment reads spread over FM * FN MFMAs */
-    auto sched_reads = [&]() {
-#pragma unroll
-        for (int i = 0; i < FM + FN; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int ni = 0; ni < FN; ni++) w[kk][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 16 + lr, ch));
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
     };
-
-    /* K-step t reads stage t&1. Slice 0 of the step is read during slice 3
-     * of the previous step; slices 1..3 one slice ahead of their MFMAs. The
-     * DMA of tile t+1 into the other stage was issued in slice 3 of step t-1;
-     * before slice 3 each wave waits for its own DMA and its LDS reads, and the
-     * barrier makes the whole tile visible and the current stage free, so
-     * slice 3 issues the DMA of tile t+2 into the current stage and reads
-     * slice 0 of tile t+1. Past the last tile the DMA repeats tile nk-1 into a
-     * stage nothing reads. */
-    auto kstep = [&](uint16_t *cur, uint16_t *nxt, int kt) {
-        frag(cur, 1, 1);
-        mfmas(0);
-        sched_reads();
-        frag(cur, 2, 0);
-        mfmas(1);
-        sched_reads();
-        frag(cur, 3, 1);
-        mfmas(0);
-        sched_reads();
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    auto mfmas = [&]() {
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+                for (int ni = 0; ni < FN; ni++)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kk][mi], w[kk][ni], acc[mi][ni], 0, 0, 0);
+    };
+/* explicit waits and barriers stay where they are written */
+#define WAIT(vm, lgkm)                                              \
+    do {                                                            \
+        __builtin_amdgcn_sched_barrier(0);                          \
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(vm, lgkm));          \
+        __builtin_amdgcn_sched_barrier(0);                          \
+    } while (0)
+    auto barrier = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_barrier();
-        dma(cur, min(kt + 2, nk - 1));
-        frag(nxt, 0, 0);
-        mfmas(1);
-#pragma unroll
-        for (int i = 0; i < FM + FN; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(0x020, 2 * DMA_PER_OPND - (FM + FN), 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - (FM + FN), 0);
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-    dma(lds0, 0);
-    dma(lds1, min(1, nk - 1));
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(2 * DMA_PER_OPND, 15));   /* tile 0 landed */
-    __builtin_amdgcn_s_barrier();
-    frag(lds0, 0, 0);
-    int kt = 0;
-    for (; kt + 1 < nk; kt += 2) {
-        kstep(lds0, lds1, kt);
-        kstep(lds1, lds0, kt + 1);
-    }
-    if (kt < nk) kstep(lds0, lds1, kt);
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));   /* no DMA outstanding at exit */
+    /* Barrier-separated phases; group 0 runs L(t), C(t) in phases 2t, 2t+1,
+     * group 1 runs L(t), C(t) in phases 2t+1, 2t+2. L(t) reads tile t (stage
+     * t&1) into registers, C(t) runs its MFMAs, so on every SIMD one wave
+     * issues MFMAs while the other reads LDS. Loads are issued only in L
+     * phases (a load waiting for the address unit holds up the instructions
+     * behind it) and each group issues half of every tile:
+     *  - group 0 issues A of tile t+1 in L(t): stage (t+1)&1 last held tile
+     *    t-1, read by both groups before phase 2t; it waits for the loads at
+     *    the end of C(t), before phase 2t+2 where tile t+1 is first read;
+     *  - group 1 issues W of tile t+2 in L(t) once its own reads of tile t
+     *    are done (group 0 read tile t in phase 2t), into the same stage, and
+     *    waits for them at the end of L(t+1), before phase 2t+4.
+     * Past the last tile the loads repeat tile nk-1 into a stage nothing
+     * reads again. */
+    auto step0 = [&](uint16_t *cur, uint16_t *nxt, int kt) {
+        frags(cur);
+        dma_a(nxt, min(kt + 1, nk - 1));
+        /* spread the loads over the fragment reads */
+#pragma unroll
+        for (int i = 0; i < DMA_PER_WAVE; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        WAIT(63, 0);
+        barrier();
+        mfmas();
+        WAIT(0, 15);
+        barrier();
+    };
+    auto step1 = [&](uint16_t *cur, int kt) {
+        frags(cur);
+        WAIT(63, 0);
+        dma_w(cur, min(kt + 2, nk - 1));
+        WAIT(DMA_PER_WAVE, 15);
+        barrier();
+        mfmas();
+        if (kt + 1 < nk) barrier();
+    };
 
-    /* ---- epilogue: lane holds column lr of each 32x32 tile, rows
-     *      (r>>2)*8 + lg*4 + (r&3) ---- */
+    if (grp) {
+        dma_w(lds0, 0);
+        dma_w(lds1, min(1, nk - 1));
+        WAIT(DMA_PER_WAVE, 15);
+        barrier();
+        barrier();
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            step1(lds0, kt);
+            step1(lds1, kt + 1);
+        }
+        if (kt < nk) step1(lds0, kt);
+    } else {
+        dma_a(lds0, 0);
+        WAIT(0, 15);
+        barrier();
+        int kt = 0;
+        for (; kt + 1 < nk; kt += 2) {
+            step0(lds0, lds1, kt);
+            step0(lds1, lds0, kt + 1);
+        }
+        if (kt < nk) step0(lds0, lds1, kt);
+    }
+    WAIT(0, 0);   /* no DMA outstanding at exit */
+#undef WAIT
+
+    /* ---- epilogue: lane holds column lr of each 16x16 tile, rows lg*4 + r ---- */
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
-    const int row0 = m0 + wm * TW_M;
-    /* interior tiles skip the per-element bounds checks */
-    if (m0 + BM <= M && n0 + BN <= N) {
-        switch (pr.epi) {
-        case IRIS_EPI_F32:
-        case IRIS_EPI_BF16:
-        case IRIS_EPI_GATED_ADD: {
-#pragma unroll
-            for (int ni = 0; ni < FN; ni++) {
-                const int col = n0 + wn * TW_N + ni * 32 + lr;
-                const float v = vec ? vec[col] : (pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f);
-#pragma unroll
-                for (int mi = 0; mi < FM; mi++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const size_t o = (size_t)(row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3)) * ldo + col;
-                        const float x = acc[mi][ni][r];
-                        if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
-                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf_hw(x + v);
-                        else ((float *)pr.out)[o] += v * x;
-                    }
-            }
-            return;
-        }
-        case IRIS_EPI_SWIGLU: {
-#pragma unroll
-            for (int g = 0; g < FN / 2; g++) {
-                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + lr;
-#pragma unroll
-                for (int mi = 0; mi < FM; mi++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-                        const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
-                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
-                    }
-            }
-            return;
-        }
-        default:
-            break;
-        }
-    }
+    const int row0 = m0 + wm * TW_M + lg * 4;
+    const bool interior = m0 + BM <= M && n0 + BN <= N;
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
     case IRIS_EPI_GATED_ADD: {
 #pragma unroll
         for (int ni = 0; ni < FN; ni++) {
-            const int col = n0 + wn * TW_N + ni * 32 + lr;
-            if (col >= N) continue;
+            const int col = n0 + wn * TW_N + ni * 16 + lr;
+            if (!interior && col >= N) continue;
             const float v = vec ? vec[col] : (pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f);
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-                    if (row >= M) continue;
+                for (int r = 0; r < 4; r++) {
+                    const int row = row0 + mi * 16 + r;
+                    if (!interior && row >= M) continue;
                     const size_t o = (size_t)row * ldo + col;
                     const float x = acc[mi][ni][r];
                     if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
@@ -278,36 +272,38 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         break;
     }
     case IRIS_EPI_SWIGLU: {
-        /* each 64 columns of the wave are one interleaved group: tile 2g = 32
-         * gate rows, tile 2g+1 = the matching 32 up rows; output column =
-         * group * 32 + lr */
+        /* each 64 columns of the wave are one interleaved group: tiles 4g,
+         * 4g+1 = 32 gate rows, tiles 4g+2, 4g+3 = the matching 32 up rows;
+         * output column = group * 32 + h * 16 + lr */
 #pragma unroll
-        for (int g = 0; g < FN / 2; g++) {
-            const int col = ((n0 + wn * TW_N + g * 64) >> 1) + lr;
-            if (col >= (N >> 1)) continue;
+        for (int g = 0; g < FN / 4; g++)
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++)
+            for (int h = 0; h < 2; h++) {
+                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + h * 16 + lr;
+                if (!interior && col >= (N >> 1)) continue;
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-                    if (row >= M) continue;
-                    const float gt = acc[mi][2 * g][r], up = acc[mi][2 * g + 1][r];
-                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
-                }
-        }
+                for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int row = row0 + mi * 16 + r;
+                        if (!interior && row >= M) continue;
+                        const float gt = acc[mi][4 * g + h][r], up = acc[mi][4 * g + 2 + h][r];
+                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
+                    }
+            }
         break;
     }
     case IRIS_EPI_F32_T: {
 #pragma unroll
         for (int ni = 0; ni < FN; ni++) {
-            const int col = n0 + wn * TW_N + ni * 32 + lr;
+            const int col = n0 + wn * TW_N + ni * 16 + lr;
             if (col >= N) continue;
             const float v = vec ? vec[col] : 0.0f;
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = row0 + mi * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                for (int r = 0; r < 4; r++) {
+                    const int row = row0 + mi * 16 + r;
                     if (row < M) ((float *)pr.out)[(size_t)col * ldo + row] = acc[mi][ni][r] + v;
                 }
         }
