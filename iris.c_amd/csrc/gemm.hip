@@ -155,14 +155,12 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             for (int ni = 0; ni < FN; ni++) w[kk][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 16 + lr, ch));
         }
     };
-    auto mfmas = [&]() {
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
+    auto mfmas = [&](int kk) {
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
                 for (int ni = 0; ni < FN; ni++)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[kk][mi], w[kk][ni], acc[mi][ni], 0, 0, 0);
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[kk][ni], a[kk][mi], acc[mi][ni], 0, 0, 0);
     };
 /* explicit waits and barriers stay where they are written */
 #define WAIT(vm, lgkm)                                              \
@@ -186,11 +184,16 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      *  - group 0 issues A of tile t+1 in L(t): stage (t+1)&1 last held tile
      *    t-1, read by both groups before phase 2t; it waits for the loads at
      *    the end of C(t), before phase 2t+2 where tile t+1 is first read;
-     *  - group 1 issues W of tile t+2 in L(t) once its own reads of tile t
-     *    are done (group 0 read tile t in phase 2t), into the same stage, and
-     *    waits for them at the end of L(t+1), before phase 2t+4.
-     * Past the last tile the loads repeat tile nk-1 into a stage nothing
-     * reads again. */
+     *  - group 1 issues W of tile t+2 in L(t), into the stage it has just
+     *    read. Two waves of the group read each W row, so the loads wait for
+     *    a barrier in the middle of phase 2t+1 that every wave of the group
+     *    reaches only after its reads of tile t have returned (group 0 read
+     *    tile t in phase 2t and meets this barrier between the two halves of
+     *    C(t)). Group 1 waits for the loads in L(t+1), before phase 2t+4.
+     * Every wait is for all of a wave's loads: completions of LDS-DMA loads
+     * are not ordered, so a partial count does not mean the oldest loads are
+     * done. Past the last tile the loads repeat tile nk-1 into a stage
+     * nothing reads again. */
     auto step0 = [&](uint16_t *cur, uint16_t *nxt, int kt) {
         frags(cur);
         dma_a(nxt, min(kt + 1, nk - 1));
@@ -202,25 +205,28 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         }
         WAIT(63, 0);
         barrier();
-        mfmas();
-        WAIT(0, 15);
+        mfmas(0);
+        barrier();   /* group 1's reads of tile kt are done */
+        mfmas(1);
+        WAIT(0, 0);
         barrier();
     };
     auto step1 = [&](uint16_t *cur, int kt) {
         frags(cur);
-        WAIT(63, 0);
+        WAIT(0, 0);
+        barrier();   /* every wave of the group has read tile kt */
         dma_w(cur, min(kt + 2, nk - 1));
-        WAIT(DMA_PER_WAVE, 15);
         barrier();
-        mfmas();
+        mfmas(0);
+        mfmas(1);
         if (kt + 1 < nk) barrier();
     };
 
     if (grp) {
         dma_w(lds0, 0);
-        dma_w(lds1, min(1, nk - 1));
-        WAIT(DMA_PER_WAVE, 15);
+        WAIT(0, 0);
         barrier();
+        dma_w(lds1, min(1, nk - 1));
         barrier();
         int kt = 0;
         for (; kt + 1 < nk; kt += 2) {
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         if (kt < nk) step1(lds0, kt);
     } else {
         dma_a(lds0, 0);
-        WAIT(0, 15);
+        WAIT(0, 0);
         barrier();
         int kt = 0;
         for (; kt + 1 < nk; kt += 2) {
@@ -242,71 +248,107 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     WAIT(0, 0);   /* no DMA outstanding at exit */
 #undef WAIT
 
-    /* ---- epilogue: lane holds column lr of each 16x16 tile, rows lg*4 + r ---- */
+    /* ---- epilogue: W is the MFMAs' first operand, so lane l holds row lr of
+     *      each 16x16 tile at the 4 consecutive columns lg*4 .. lg*4+3 ---- */
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
-    const int row0 = m0 + wm * TW_M + lg * 4;
-    const bool interior = m0 + BM <= M && n0 + BN <= N;
+    const int rowb = m0 + wm * TW_M + lr;
+    const int colb = n0 + wn * TW_N + lg * 4;
+    /* whole tile in range and 4-wide accesses aligned: one 8- or 16-byte
+     * access per lane and 16x16 tile */
+    const bool full = m0 + BM <= M && n0 + BN <= N && (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 &&
+                      ((uintptr_t)vec & 15) == 0;
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
     case IRIS_EPI_GATED_ADD: {
+        const float vdef = pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f;
 #pragma unroll
         for (int ni = 0; ni < FN; ni++) {
-            const int col = n0 + wn * TW_N + ni * 16 + lr;
-            if (!interior && col >= N) continue;
-            const float v = vec ? vec[col] : (pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f);
+            const int col = colb + ni * 16;
+            float v[4];
+            if (full && vec) {
+                const float4 t = *(const float4 *)(vec + col);
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            } else {
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++)
+                for (int r = 0; r < 4; r++) v[r] = vec && col + r < N ? vec[col + r] : vdef;
+            }
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = row0 + mi * 16 + r;
-                    if (!interior && row >= M) continue;
-                    const size_t o = (size_t)row * ldo + col;
-                    const float x = acc[mi][ni][r];
-                    if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o] = x + v;
-                    else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o] = f2bf_hw(x + v);
-                    else ((float *)pr.out)[o] += v * x;
+            for (int mi = 0; mi < FM; mi++) {
+                const int row = rowb + mi * 16;
+                const f32x4 x = acc[mi][ni];
+                const size_t o = (size_t)row * ldo + col;
+                if (full) {
+                    if (pr.epi == IRIS_EPI_F32) {
+                        *(float4 *)((float *)pr.out + o) = make_float4(x[0] + v[0], x[1] + v[1], x[2] + v[2], x[3] + v[3]);
+                    } else if (pr.epi == IRIS_EPI_BF16) {
+                        uint2 p;
+                        p.x = (uint32_t)f2bf_hw(x[0] + v[0]) | ((uint32_t)f2bf_hw(x[1] + v[1]) << 16);
+                        p.y = (uint32_t)f2bf_hw(x[2] + v[2]) | ((uint32_t)f2bf_hw(x[3] + v[3]) << 16);
+                        *(uint2 *)((uint16_t *)pr.out + o) = p;
+                    } else {
+                        float4 *dst = (float4 *)((float *)pr.out + o);
+                        float4 y = *dst;
+                        y.x += v[0] * x[0]; y.y += v[1] * x[1]; y.z += v[2] * x[2]; y.w += v[3] * x[3];
+                        *dst = y;
+                    }
+                } else if (row < M) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if (col + r >= N) continue;
+                        if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o + r] = x[r] + v[r];
+                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o + r] = f2bf_hw(x[r] + v[r]);
+                        else ((float *)pr.out)[o + r] += v[r] * x[r];
+                    }
                 }
+            }
         }
         break;
     }
     case IRIS_EPI_SWIGLU: {
         /* each 64 columns of the wave are one interleaved group: tiles 4g,
          * 4g+1 = 32 gate rows, tiles 4g+2, 4g+3 = the matching 32 up rows;
-         * output column = group * 32 + h * 16 + lr */
+         * output columns = group * 32 + h * 16 + lg * 4 + (0..3) */
 #pragma unroll
         for (int g = 0; g < FN / 4; g++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + h * 16 + lr;
-                if (!interior && col >= (N >> 1)) continue;
+                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + h * 16 + lg * 4;
 #pragma unroll
-                for (int mi = 0; mi < FM; mi++)
+                for (int mi = 0; mi < FM; mi++) {
+                    const int row = rowb + mi * 16;
+                    const f32x4 gt = acc[mi][4 * g + h], up = acc[mi][4 * g + 2 + h];
+                    uint16_t y[4];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int row = row0 + mi * 16 + r;
-                        if (!interior && row >= M) continue;
-                        const float gt = acc[mi][4 * g + h][r], up = acc[mi][4 * g + 2 + h][r];
-                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = f2bf_hw(silu_fast(gt) * up);
+                    for (int r = 0; r < 4; r++) y[r] = f2bf_hw(silu_fast(gt[r]) * up[r]);
+                    uint16_t *dst = (uint16_t *)pr.out + (size_t)row * ldo + col;
+                    if (full) {
+                        *(uint2 *)dst = make_uint2((uint32_t)y[0] | ((uint32_t)y[1] << 16),
+                                                   (uint32_t)y[2] | ((uint32_t)y[3] << 16));
+                    } else if (row < M) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            if (col + r < (N >> 1)) dst[r] = y[r];
                     }
+                }
             }
         break;
     }
     case IRIS_EPI_F32_T: {
 #pragma unroll
-        for (int ni = 0; ni < FN; ni++) {
-            const int col = n0 + wn * TW_N + ni * 16 + lr;
-            if (col >= N) continue;
-            const float v = vec ? vec[col] : 0.0f;
+        for (int ni = 0; ni < FN; ni++)
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++)
+            for (int r = 0; r < 4; r++) {
+                const int col = colb + ni * 16 + r;
+                if (col >= N) continue;
+                const float v = vec ? vec[col] : 0.0f;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int row = row0 + mi * 16 + r;
+                for (int mi = 0; mi < FM; mi++) {
+                    const int row = rowb + mi * 16;
                     if (row < M) ((float *)pr.out)[(size_t)col * ldo + row] = acc[mi][ni][r] + v;
                 }
-        }
+            }
         break;
     }
     default:

@@ -31,8 +31,11 @@ def run_gemm(lib, problems):
     assert lib.iris_hip_sync() == 0
 
 
+# The launcher picks a 256x256 or 288x192 block tile per launch from the tile
+# count; (4096, 4096) and (4608, 9216) take 256x256, the others 288x192.
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (384, 3072, 3072), (1000, 520, 128), (64, 27648, 256),
-                                   (4608, 256, 12288), (17, 33 * 8, 192)])
+                                   (4608, 256, 12288), (17, 33 * 8, 192), (4096, 4096, 128), (4608, 3072, 1024),
+                                   (4608, 9216, 192)])
 def test_gemm_f32(lib, M, N, K):
     rng = np.random.default_rng(M * 7 + N)
     A = rng.standard_normal((M, K), np.float32)
@@ -84,6 +87,32 @@ def test_gemm_epilogues_and_grouping(lib):
     assert tl.rel_l2(tl.bf16_to_f32(dSw.get(np.uint16, (T + I, mlp))), ref_sw) < 4e-3
     ref_t = (a64[T:] @ bf(W1).astype(np.float64).T + gate).T
     assert tl.rel_l2(dT.get(np.float32, (N, I)), ref_t) < 1e-5
+
+
+def test_gemm_repeat_bitwise_mixed_k(lib):
+    """One launch of a long-K and a short-K problem (the embedders' shapes:
+    K 7680 over 512 rows, K 128 over 16384 rows), repeated: every launch
+    bit-identical to the first. Blocks of the short problem turn over quickly
+    next to the long ones, which exposes LDS reuse races between the wave
+    groups of a block."""
+    h, T, I, td, C = 3072, 512, 16384, 7680, 128
+    rng = np.random.default_rng(5)
+    txt = tl.Dev.of(tl.to_bf16(rng.standard_normal(T * td, np.float32)))
+    tok = tl.Dev.of(tl.to_bf16(rng.standard_normal(I * C, np.float32)))
+    Wt = tl.Dev.of(tl.to_bf16(rng.standard_normal(h * td, np.float32) * 0.02))
+    Wi = tl.Dev.of(tl.to_bf16(rng.standard_normal(h * C, np.float32) * 0.02))
+    x = tl.Dev((T + I) * h * 4)
+    P = tl.GemmProblem
+    probs = [P(txt.ptr, Wt.ptr, x.ptr, None, T, h, td, td, td, h, EPI_F32),
+             P(tok.ptr, Wi.ptr, x.ptr + T * h * 4, None, I, h, C, C, C, h, EPI_F32)]
+    first = None
+    for rep in range(12):
+        run_gemm(lib, probs)
+        got = x.get(np.uint32, ((T + I) * h,))
+        if first is None:
+            first = got
+        else:
+            assert np.array_equal(first, got), f"launch {rep} differs from the first"
 
 
 def attention_ref(q, k, v, scale, valid=None):
