@@ -105,8 +105,9 @@ int iris_hip_rms_gated_add(float *d_x, const float *d_y, const float *d_w, const
 /* Per (row, head) RMSNorm of Q and K (x w_q / w_k, rows < split use set A) and
  * rotary embedding from per-row cos/sin tables [rows][128] (pairs 2i, 2i+1).
  * qkv: bf16 rows holding Q at column 0, K at col_k, V at col_v (ld_qkv).
- * Writes Q', K' as bf16 [rows][heads*128] and V transposed to
- * vt[head][d][ld_vt] (columns rows..ld_vt-1 zero-filled). */
+ * Writes Q' as bf16 [rows][heads*128], K' as [rows][kv_heads*128] and V
+ * transposed to vt[kv head][d][ld_vt] (columns rows..ld_vt-1 zero-filled).
+ * kv_heads 0 means heads (no grouped-query attention). */
 typedef struct {
     const uint16_t *qkv; int ld_qkv, col_k, col_v;
     uint16_t *q_out, *k_out, *vt_out; int ld_vt;
@@ -115,13 +116,17 @@ typedef struct {
     const float *cos_t, *sin_t;       /* [rows][128]; NULL = no rotation */
     int period;                       /* 0: none; else split and table row use row % period */
     float eps;
+    int kv_heads;                     /* K / V heads; 0: same as heads */
 } iris_qkprep_args_t;
 int iris_hip_qk_prepare(const iris_qkprep_args_t *a);
 
 /* Flash attention over head_dim 128: O = softmax(Q K^T * scale) V per head.
  * Q [sq][ld_q], K [sk][ld_k] (head h at column h*128), Vt [h][128][ld_vt],
  * O [sq][ld_o]. Keys outside [kv_lo0, kv_hi0) U [kv_lo1, kv_hi1) are masked
- * (pass 0, sk, 0, 0 for none). batch / *_bstride run independent sequences. */
+ * (pass 0, sk, 0, 0 for none); with causal set, so are keys after the query's
+ * own index. Query head h reads K / V head h / kv_group (grouped-query
+ * attention; 0 means 1). batch / *_bstride run independent sequences. A query
+ * with no unmasked key gets zeros. */
 typedef struct {
     const uint16_t *q; const uint16_t *k; const uint16_t *vt; uint16_t *o;
     int ld_q, ld_k, ld_vt, ld_o;
@@ -129,6 +134,8 @@ typedef struct {
     long long q_bstride, k_bstride, vt_bstride, o_bstride;
     float scale;
     int kv_lo0, kv_hi0, kv_lo1, kv_hi1;
+    int causal;                       /* 1: key j is masked for query i < j */
+    int kv_group;                     /* query heads per K / V head; 0: 1 */
 } iris_attn_args_t;
 int iris_hip_attention(const iris_attn_args_t *a);
 
@@ -145,6 +152,11 @@ int iris_hip_patchify(uint16_t *d_out, const float *d_latent, int C, int H, int 
 int iris_hip_unpatchify(float *d_latent, const float *d_patches, int C, int H, int W, int ps);
 /* copy one f32 row vector into rows [r0, r1) of a [*, cols] matrix */
 int iris_hip_fill_rows(float *d_x, const float *d_row, int r0, int r1, int cols);
+/* out[r][c] = table[ids[r]][c] (bf16 table [vocab][cols] -> f32), zeros for
+ * ids outside [0, vocab) */
+int iris_hip_embed_rows(float *d_out, const uint16_t *d_table, const int *d_ids, int rows, int cols, int vocab);
+/* f32 block copy: dst[r][c] = src[r][c] for r < rows, c < cols */
+int iris_hip_copy_rows(float *d_dst, int ld_dst, const float *d_src, int ld_src, int rows, int cols);
 
 /* ---- f32 kernel API support (iris_kernels.h) ---- */
 /* f32 -> bf16 hi/lo split for f32-accurate GEMMs: the destination row holds

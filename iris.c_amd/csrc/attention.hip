@@ -21,6 +21,10 @@
  * layout of the PV product, so P never goes through LDS. V arrives already
  * transposed ([head][d][key], written by iris_hip_qk_prepare).
  *
+ * Grouped-query attention reads K / V head h / kv_group for query head h.
+ * With causal set a block stops at the key tile of its last query and tiles
+ * past a wave's first query are masked per element (key <= query).
+ *
  * The running max is updated lazily: O and the row sums are rescaled only when
  * some query's tile max exceeds its running max by more than 8 (log2 units),
  * so probabilities stay <= 2^8 and most tiles skip the rescale. Key masks
@@ -59,13 +63,16 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     if (L >= total) return;
     const int qblk = L % nqb, hb = L / nqb;
     const int head = hb % a.heads, bz = hb / a.heads;
+    const int kv_head = a.kv_group > 1 ? head / a.kv_group : head;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, lg = lane >> 5;
     const uint16_t *Q = a.q + (size_t)bz * a.q_bstride + head * HD;
-    const uint16_t *K = a.k + (size_t)bz * a.k_bstride + head * HD;
-    const uint16_t *VT = a.vt + (size_t)bz * a.vt_bstride + (size_t)head * HD * a.ld_vt;
+    const uint16_t *K = a.k + (size_t)bz * a.k_bstride + kv_head * HD;
+    const uint16_t *VT = a.vt + (size_t)bz * a.vt_bstride + (size_t)kv_head * HD * a.ld_vt;
     uint16_t *O = a.o + (size_t)bz * a.o_bstride + head * HD;
     const int sq = a.sq, sk = a.sk;
-    const int nkt = (sk + KB - 1) / KB;
+    /* causal: the block's last query needs keys up to its own index */
+    const int nkt = a.causal ? (min(sk, min(sq, (qblk + 1) * QB)) + KB - 1) / KB : (sk + KB - 1) / KB;
+    const int wave_q0 = qblk * QB + wave * QW;
 
     /* Q fragments (B operand): lane holds query lr of the wave's 32, d = ds*16 + lg*8 .. +7 */
     const int q_row = qblk * QB + wave * QW + lr;
@@ -140,7 +147,8 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
         if (kt + 2 < nkt) gload(kt + 2);
 
         const bool full = k0 + KB <= sk && ((k0 >= a.kv_lo0 && k0 + KB <= a.kv_hi0) ||
-                                            (k0 >= a.kv_lo1 && k0 + KB <= a.kv_hi1));
+                                            (k0 >= a.kv_lo1 && k0 + KB <= a.kv_hi1)) &&
+                          !(a.causal && k0 + KB - 1 > wave_q0);
         if (!full) {
 #pragma unroll
             for (int ks = 0; ks < 2; ks++)
@@ -148,7 +156,8 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
                 for (int r = 0; r < 16; r++) {
                     const int key = k0 + ks * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
                     const bool ok = (key < sk) & (((key >= a.kv_lo0) & (key < a.kv_hi0)) |
-                                                  ((key >= a.kv_lo1) & (key < a.kv_hi1)));
+                                                  ((key >= a.kv_lo1) & (key < a.kv_hi1))) &
+                                    (!a.causal | (key <= q_row));
                     s[ks][r] = ok ? s[ks][r] : -INFINITY;
                 }
         }
@@ -225,6 +234,8 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
         return iris_set_error("attention: leading dimensions must be multiples of 8");
     if (a->ld_vt < ((a->sk + KB - 1) / KB) * KB)
         return iris_set_error("attention: ld_vt %d < padded key count", a->ld_vt);
+    if (a->kv_group < 0 || (a->kv_group > 1 && a->heads % a->kv_group))
+        return iris_set_error("attention: %d heads not a multiple of kv_group %d", a->heads, a->kv_group);
     if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt) & 15)
         return iris_set_error("attention: operands must be 16-byte aligned");
     const int nqb = (a->sq + QB - 1) / QB;

@@ -157,11 +157,12 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
         const float *wsel = which ? (use_b ? a.wkB : a.wkA) : (use_b ? a.wqB : a.wqA);
         const float4 w0 = *(const float4 *)(wsel + d0), w1 = *(const float4 *)(wsel + d0 + 4);
         const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        const int nh = which && a.kv_heads ? a.kv_heads : a.heads;
         const uint16_t *src = a.qkv + (size_t)row * a.ld_qkv + (which ? a.col_k : 0) + d0;
-        uint16_t *dst = (which ? a.k_out : a.q_out) + (size_t)row * a.heads * 128 + d0;
-        for (int hb = 0; hb < a.heads; hb += 4) {
+        uint16_t *dst = (which ? a.k_out : a.q_out) + (size_t)row * nh * 128 + d0;
+        for (int hb = 0; hb < nh; hb += 4) {
             const int head = hb + hq;
-            const bool on = head < a.heads;                   /* uniform per 16-lane group */
+            const bool on = head < nh;                        /* uniform per 16-lane group */
             u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
             if (on) raw = *(const u16x8 *)(src + head * 128);
             float x[8];
@@ -296,6 +297,34 @@ __global__ void fill_rows_kernel(float *x, const float *row, int r0, int r1, int
         x[(size_t)r0 * cols + i] = row[i % cols];
 }
 
+/* Token embedding lookup (iris_qwen3.c:1080-1091): one block row per token,
+ * 8 bf16 per thread per step; ids outside the table give a zero row. */
+__global__ void embed_rows_kernel(float *out, const uint16_t *table, const int *ids, int rows, int cols, int vocab) {
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    const int id = ids[r];
+    float *o = out + (size_t)r * cols;
+    const bool ok = id >= 0 && id < vocab;
+    const uint16_t *t = table + (size_t)(ok ? id : 0) * cols;
+    for (int c = threadIdx.x * 8; c < cols; c += NT * 8) {
+        if (c + 8 <= cols) {
+            u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (ok) v = *(const u16x8 *)(t + c);
+            ((float4 *)(o + c))[0] = make_float4(bf2f(v[0]), bf2f(v[1]), bf2f(v[2]), bf2f(v[3]));
+            ((float4 *)(o + c))[1] = make_float4(bf2f(v[4]), bf2f(v[5]), bf2f(v[6]), bf2f(v[7]));
+        } else {
+            for (int j = c; j < cols; j++) o[j] = ok ? bf2f(t[j]) : 0.0f;
+        }
+    }
+}
+
+/* f32 block copy, one block row per row */
+__global__ void copy_rows_kernel(float *dst, int ld_dst, const float *src, int ld_src, int rows, int cols) {
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    for (int c = threadIdx.x; c < cols; c += NT) dst[(size_t)r * ld_dst + c] = src[(size_t)r * ld_src + c];
+}
+
 int grid1d(size_t n) {
     size_t b = (n + NT - 1) / NT;
     return (int)(b < 8192 ? (b ? b : 1) : 8192);
@@ -352,12 +381,15 @@ int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
     if (a->rows <= 0) return 0;
     if (a->ld_qkv % 8 || a->col_k % 8 || a->col_v % 8) return iris_set_error("qk_prepare: layout not 16-byte aligned");
     if (a->ld_vt < a->rows || a->ld_vt % 64) return iris_set_error("qk_prepare: ld_vt=%d", a->ld_vt);
+    if (a->heads <= 0 || a->kv_heads < 0 || a->kv_heads > a->heads)
+        return iris_set_error("qk_prepare: heads=%d kv_heads=%d", a->heads, a->kv_heads);
     if (((uintptr_t)a->qkv | (uintptr_t)a->q_out | (uintptr_t)a->k_out | (uintptr_t)a->vt_out) & 15)
         return iris_set_error("qk_prepare: buffers must be 16-byte aligned");
     hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
                        iris_stream(), *a);
     if (iris_launch_check("qk_norm_rope_kernel")) return -1;
-    hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, a->heads), dim3(NT), 0, iris_stream(), *a);
+    const int kvh = a->kv_heads ? a->kv_heads : a->heads;
+    hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
     return iris_launch_check("v_transpose_kernel");
 }
 
@@ -412,6 +444,22 @@ int iris_hip_fill_rows(float *x, const float *row, int r0, int r1, int cols) {
     size_t n = (size_t)(r1 - r0) * cols;
     hipLaunchKernelGGL(fill_rows_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), x, row, r0, r1, cols);
     return iris_launch_check("fill_rows_kernel");
+}
+
+int iris_hip_embed_rows(float *out, const uint16_t *table, const int *ids, int rows, int cols, int vocab) {
+    if (rows <= 0) return 0;
+    if (cols <= 0 || vocab <= 0) return iris_set_error("embed_rows: cols=%d vocab=%d", cols, vocab);
+    if (cols % 8 || ((uintptr_t)out | (uintptr_t)table) & 15)
+        return iris_set_error("embed_rows: cols %% 8 and 16-byte aligned buffers required");
+    hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), out, table, ids, rows, cols, vocab);
+    return iris_launch_check("embed_rows_kernel");
+}
+
+int iris_hip_copy_rows(float *dst, int ld_dst, const float *src, int ld_src, int rows, int cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    if (ld_dst < cols || ld_src < cols) return iris_set_error("copy_rows: ld_dst=%d ld_src=%d < cols=%d", ld_dst, ld_src, cols);
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), dst, ld_dst, src, ld_src, rows, cols);
+    return iris_launch_check("copy_rows_kernel");
 }
 
 }  /* extern "C" */

@@ -283,10 +283,11 @@ int iris_st_read_bf16(const iris_st_file_t *f, const iris_st_tensor_t *t, uint16
 
 /* Shard discovery: the index json's weight_map values name the shard files
  * (iris_transformer_flux.c:473-557); otherwise a single file. */
-int iris_st_set_open(iris_st_set_t *s, const char *model_dir) {
+int iris_st_set_open_files(iris_st_set_t *s, const char *dir, const char *index_name, const char *const *fallback,
+                           int n_fallback) {
     memset(s, 0, sizeof(*s));
-    char path[2048];
-    snprintf(path, sizeof(path), "%s/transformer/diffusion_pytorch_model.safetensors.index.json", model_dir);
+    char path[4096];
+    snprintf(path, sizeof(path), "%.2047s/%.1023s", dir, index_name);
     FILE *fp = fopen(path, "rb");
     if (fp) {
         fseek(fp, 0, SEEK_END);
@@ -315,7 +316,7 @@ int iris_st_set_open(iris_st_set_t *s, const char *model_dir) {
         }
         free(json);
         for (int i = 0; i < nn; i++) {
-            snprintf(path, sizeof(path), "%s/transformer/%s", model_dir, names[i]);
+            snprintf(path, sizeof(path), "%.2047s/%.1023s", dir, names[i]);
             s->f[s->n] = iris_st_open(path);
             if (!s->f[s->n]) {
                 fprintf(stderr, "iris_st: failed to open shard %s\n", path);
@@ -326,11 +327,28 @@ int iris_st_set_open(iris_st_set_t *s, const char *model_dir) {
         }
         if (s->n > 0) return 0;
     }
-    snprintf(path, sizeof(path), "%s/transformer/diffusion_pytorch_model.safetensors", model_dir);
-    s->f[0] = iris_st_open(path);
-    if (!s->f[0]) return -1;
-    s->n = 1;
-    return 0;
+    /* no index: the fallback names, all of one group present; groups are
+     * separated by NULL entries */
+    for (int i = 0; i < n_fallback; i++) {
+        int j = i, ok = 1;
+        while (j < n_fallback && fallback[j]) {
+            snprintf(path, sizeof(path), "%.2047s/%.1023s", dir, fallback[j]);
+            if (ok && s->n < IRIS_ST_MAX_SHARDS && (s->f[s->n] = iris_st_open(path))) s->n++;
+            else ok = 0;
+            j++;
+        }
+        if (ok && s->n > 0) return 0;
+        iris_st_set_close(s);
+        i = j;
+    }
+    return -1;
+}
+
+int iris_st_set_open(iris_st_set_t *s, const char *model_dir) {
+    char dir[2048];
+    snprintf(dir, sizeof(dir), "%s/transformer", model_dir);
+    static const char *const fb[] = {"diffusion_pytorch_model.safetensors"};
+    return iris_st_set_open_files(s, dir, "diffusion_pytorch_model.safetensors.index.json", fb, 1);
 }
 
 void iris_st_set_close(iris_st_set_t *s) {

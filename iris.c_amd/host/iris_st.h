@@ -64,6 +64,11 @@ typedef struct {
 /* Opens <dir>/transformer/diffusion_pytorch_model.safetensors[.index.json]
  * (the shard discovery of iris_transformer_flux.c:470-570). Returns 0 on success. */
 int iris_st_set_open(iris_st_set_t *s, const char *model_dir);
+/* Opens the shards that <dir>/<index_name> lists in its weight_map, or, with
+ * no index, the first group of fallback names (groups separated by NULL)
+ * whose files all open. Returns 0 on success. */
+int iris_st_set_open_files(iris_st_set_t *s, const char *dir, const char *index_name, const char *const *fallback,
+                           int n_fallback);
 void iris_st_set_close(iris_st_set_t *s);
 const iris_st_tensor_t *iris_st_set_find(const iris_st_set_t *s, const char *name,
                                          const iris_st_file_t **owner);

@@ -42,6 +42,7 @@
 
 typedef struct orc_flux orc_flux_t;
 typedef struct orc_zi orc_zi_t;
+typedef struct orc_qwen3 orc_qwen3_t;
 
 typedef struct {
     const float *latent;
@@ -111,5 +112,18 @@ void orc_zi_block(orc_zi_t *m, int kind, int idx, float *x, const int *pos, cons
 float *orc_official_schedule(int n, int image_seq_len);
 float *orc_zimage_schedule(int n, float shift);
 float *orc_init_noise(int batch, int ch, int h, int w, int64_t seed);
+
+/* Qwen3 text encoder (orc_qwen3.c, iris_qwen3.c): config.json + safetensors
+ * directory, or the seeded synthetic weights of iris_synth.h. mode 0 = Flux
+ * (layers 8, 17, 26 concatenated), 1 = Z-Image (layer num_layers-2).
+ * forward: malloc'd [seq][text_dim]; with last_limit >= 0 below the mode's
+ * last layer it stops after that layer and returns the hidden state [seq][h]. */
+orc_qwen3_t *orc_qwen3_load(const char *dir);
+orc_qwen3_t *orc_qwen3_create_synth(int hidden, int inter, int heads, int kv_heads, int layers, int vocab,
+                                    uint64_t seed);
+void orc_qwen3_free(orc_qwen3_t *m);
+void orc_qwen3_set_mode(orc_qwen3_t *m, int mode);
+int orc_qwen3_dims(const orc_qwen3_t *m, int *out4);   /* hidden, layers, text_dim, head_dim */
+float *orc_qwen3_forward(orc_qwen3_t *m, const int *ids, const int *mask, int seq, int last_limit);
 
 #endif

@@ -43,6 +43,14 @@ def oracle():
         lib.orc_zimage_schedule.restype = ctypes.c_void_p
         lib.orc_init_noise.restype = ctypes.c_void_p
         lib.orc_blas_info.restype = ctypes.c_char_p
+        lib.orc_qwen3_load.restype = ctypes.c_void_p
+        lib.orc_qwen3_load.argtypes = [ctypes.c_char_p]
+        lib.orc_qwen3_create_synth.restype = ctypes.c_void_p
+        lib.orc_qwen3_create_synth.argtypes = [ctypes.c_int] * 6 + [ctypes.c_uint64]
+        lib.orc_qwen3_free.argtypes = [ctypes.c_void_p]
+        lib.orc_qwen3_set_mode.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        lib.orc_qwen3_forward.restype = ctypes.c_void_p
+        lib.orc_qwen3_forward.argtypes = [ctypes.c_void_p, IP, IP, ctypes.c_int, ctypes.c_int]
         lib.iris_synth_seed.restype = ctypes.c_uint64
         lib.iris_synth_seed.argtypes = [ctypes.c_uint64, ctypes.c_char_p]
         lib.iris_synth_fill_bf16.argtypes = [U16P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
@@ -74,7 +82,7 @@ class QkPrepArgs(ctypes.Structure):
                 ("ld_vt", ctypes.c_int), ("rows", ctypes.c_int), ("heads", ctypes.c_int),
                 ("wqA", ctypes.c_void_p), ("wkA", ctypes.c_void_p), ("wqB", ctypes.c_void_p), ("wkB", ctypes.c_void_p),
                 ("split", ctypes.c_int), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
-                ("period", ctypes.c_int), ("eps", ctypes.c_float)]
+                ("period", ctypes.c_int), ("eps", ctypes.c_float), ("kv_heads", ctypes.c_int)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -84,7 +92,8 @@ class AttnArgs(ctypes.Structure):
                 ("q_bstride", ctypes.c_longlong), ("k_bstride", ctypes.c_longlong),
                 ("vt_bstride", ctypes.c_longlong), ("o_bstride", ctypes.c_longlong),
                 ("scale", ctypes.c_float), ("kv_lo0", ctypes.c_int), ("kv_hi0", ctypes.c_int),
-                ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int)]
+                ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int), ("causal", ctypes.c_int),
+                ("kv_group", ctypes.c_int)]
 
 
 class IrisRef(ctypes.Structure):
@@ -128,6 +137,17 @@ def hip():
                    "iris_sample_euler_zimage", "iris_zimage_schedule"):
             if hasattr(lib, fn):
                 getattr(lib, fn).restype = vp
+        lib.qwen3_model_load.restype = vp
+        lib.qwen3_model_load.argtypes = [ctypes.c_char_p]
+        lib.qwen3_model_create_synthetic.restype = vp
+        lib.qwen3_model_create_synthetic.argtypes = [ctypes.c_int] * 6 + [ctypes.c_uint64]
+        lib.qwen3_model_free.argtypes = [vp]
+        lib.qwen3_model_set_extraction_mode.argtypes = [vp, ctypes.c_int]
+        lib.qwen3_model_text_dim.argtypes = [vp]
+        lib.qwen3_forward.restype = vp
+        lib.qwen3_forward.argtypes = [vp, IP, IP, ctypes.c_int]
+        lib.iris_hip_embed_rows.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_copy_rows.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_flux_device_buffer.restype = vp
         lib.iris_flux_device_buffer.argtypes = [vp, ctypes.c_char_p]
         for fn in ("iris_flux_prepare", "iris_flux_upload", "iris_flux_velocity", "iris_flux_step",
@@ -247,6 +267,12 @@ def ref():
         lib.iris_zimage_schedule.restype = ctypes.c_void_p
         lib.iris_init_noise.restype = ctypes.c_void_p
         lib.iris_sample_euler.restype = ctypes.c_void_p
+        lib.qwen3_model_load.restype = ctypes.c_void_p
+        lib.qwen3_model_load.argtypes = [ctypes.c_char_p]
+        lib.qwen3_model_free.argtypes = [ctypes.c_void_p]
+        lib.qwen3_forward.restype = ctypes.c_void_p
+        lib.qwen3_forward.argtypes = [ctypes.c_void_p, IP, IP, ctypes.c_int]
+        lib.qwen3_set_extraction_mode.argtypes = [ctypes.c_void_p, ctypes.c_int]
         _libs["ref"] = lib
     return _libs["ref"]
 
@@ -426,3 +452,49 @@ def fingerprint(x, stride=97):
     x = np.asarray(x, np.float32).ravel()
     return {"sub": x[::stride].copy(), "sum": np.float64(x.astype(np.float64).sum()),
             "sumsq": np.float64((x.astype(np.float64) ** 2).sum())}
+
+
+# ---------------------------------------------------------------- Qwen3 files
+
+def write_qwen3_dir(d, hidden=256, inter=512, heads=4, kv_heads=2, layers=28, vocab=300, seed=0):
+    """A random-init Qwen3 directory in the HuggingFace layout the reference
+    loads (config.json, model.safetensors.index.json, one bf16 shard)."""
+    os.makedirs(d, exist_ok=True)
+    rng = np.random.default_rng(seed)
+    hd = 128
+    cfg = {"hidden_size": hidden, "intermediate_size": inter, "num_attention_heads": heads,
+           "num_key_value_heads": kv_heads, "head_dim": hd, "vocab_size": vocab, "num_hidden_layers": layers,
+           "rope_theta": 1000000.0}
+    with open(os.path.join(d, "config.json"), "w") as f:
+        json.dump(cfg, f)
+
+    def w(*shape, scale=0.02):
+        return to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+    def nrm(n):
+        return to_bf16((1.0 + rng.standard_normal(n) * 0.1).astype(np.float32))
+
+    t = {"model.embed_tokens.weight": w(vocab, hidden, scale=0.5), "model.norm.weight": nrm(hidden)}
+    for i in range(layers):
+        p = f"model.layers.{i}."
+        t[p + "input_layernorm.weight"] = nrm(hidden)
+        t[p + "post_attention_layernorm.weight"] = nrm(hidden)
+        t[p + "self_attn.q_proj.weight"] = w(heads * hd, hidden, scale=0.05)
+        t[p + "self_attn.k_proj.weight"] = w(kv_heads * hd, hidden, scale=0.05)
+        t[p + "self_attn.v_proj.weight"] = w(kv_heads * hd, hidden, scale=0.05)
+        t[p + "self_attn.o_proj.weight"] = w(hidden, heads * hd)
+        t[p + "self_attn.q_norm.weight"] = nrm(hd)
+        t[p + "self_attn.k_norm.weight"] = nrm(hd)
+        t[p + "mlp.gate_proj.weight"] = w(inter, hidden, scale=0.05)
+        t[p + "mlp.up_proj.weight"] = w(inter, hidden, scale=0.05)
+        t[p + "mlp.down_proj.weight"] = w(hidden, inter)
+    shard = "model-00001-of-00001.safetensors"
+    write_safetensors(os.path.join(d, shard), list(t.items()))
+    with open(os.path.join(d, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {}, "weight_map": {k: shard for k in t}}, f)
+    return cfg
+
+
+class Qwen3Encoder(ctypes.Structure):
+    """The reference's qwen3_encoder_t (tokenizer, model) for its mode setter."""
+    _fields_ = [("tokenizer", ctypes.c_void_p), ("model", ctypes.c_void_p)]

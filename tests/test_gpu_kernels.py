@@ -165,6 +165,37 @@ def test_flash_attention(lib, S, H, batch, mask, qscale, kramp):
             assert tl.rel_l2(got[b, :, sl], ref) < 1e-2, (b, h)
 
 
+@pytest.mark.parametrize("S,H,group,n_real", [(300, 4, 2, 250), (512, 8, 4, 512), (70, 2, 1, 70), (1, 4, 4, 1)])
+def test_flash_attention_causal_gqa(lib, S, H, group, n_real):
+    """Causal mask (key j hidden from query i < j) with a padding key range
+    and grouped-query heads (query head h reads K / V head h // group)."""
+    rng = np.random.default_rng(S * 7 + H)
+    kvh = H // group
+    S_pad = (S + 63) // 64 * 64
+    q = rng.standard_normal((S, H * 128), np.float32) * np.float32(2.0)
+    k = rng.standard_normal((S, kvh * 128), np.float32)
+    v = rng.standard_normal((S, kvh * 128), np.float32)
+    vt = np.zeros((kvh, 128, S_pad), np.float32)
+    for h in range(kvh):
+        vt[h, :, :S] = v[:, h * 128:(h + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(q)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    do = tl.Dev(S * H * 128 * 2)
+    a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, do.ptr, H * 128, kvh * 128, S_pad, H * 128, S, S, H, 1, 0, 0, 0, 0,
+                    1 / math.sqrt(128), 0, n_real, 0, 0, 1, group)
+    assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(do.get(np.uint16, (S, H * 128)))
+    scale = 1 / math.sqrt(128)
+    allowed = np.tril(np.ones((S, S), bool)) & (np.arange(S) < n_real)[None, :]
+    for h in range(H):
+        sl, kl = slice(h * 128, (h + 1) * 128), slice((h // group) * 128, (h // group + 1) * 128)
+        sc = bf(q[:, sl]).astype(np.float64) @ bf(k[:, kl]).astype(np.float64).T * scale
+        sc = np.where(allowed, sc, -np.inf)
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        ref = (p / p.sum(1, keepdims=True)) @ bf(v[:, kl]).astype(np.float64)
+        assert tl.rel_l2(got[:, sl], ref) < 1e-2, h
+
+
 def test_rownorm_modes(lib):
     rng = np.random.default_rng(3)
     rows, cols, split = 50, 3072, 20
