@@ -7,7 +7,8 @@ Default workload (--config ns): Flux.2-Klein-4B-shaped denoiser (5 double +
 synthetic inputs. A step = one transformer forward + the Euler update, with
 latent, text and weights resident in HBM (captured hipGraph replay + update
 kernel). Other configs: c2 (512x512), c3 (2 reference images, 12800 tokens),
-c4 (9B-shaped, CFG as batch 2), c5 (Z-Image-Turbo-6B-shaped, 8 NFE).
+c4 (9B-shaped, CFG as batch 2), c5 (Z-Image-Turbo-6B-shaped, 8 NFE), qwen3
+(the Qwen3-4B-shaped text encoder at 512 tokens; a "step" is one encode).
 
 Prints one JSON line. `value` is images/s; ms_per_step is per denoise step.
 `roofline` is the kernel class with the largest share of the step (the fused
@@ -44,6 +45,11 @@ CONFIGS = {
                workload="Flux.2-Klein-4B-shaped, 1024x1024 + 2 references (T offsets 1, 2), 12800 tokens"),
     "c4": dict(kind="flux", h=4096, H=32, nd=8, ns=24, td=12288, ih=64, iw=64, T=512, steps=50, refs=[], B=2,
                workload="Flux.2-Klein-9B-base-shaped, 1024x1024, CFG 4.0 as batch 2, 50-step schedule"),
+    "qwen3": dict(kind="qwen3", h=2560, inter=9728, H=32, KV=8, layers=36, vocab=151936, seq=512, n_real=512,
+                  steps=1, metric="ms per text encode + encodes/s @Qwen3-4B-shape 512 tokens; % of bf16 MFMA peak",
+                  unit="encodes/s", data="synthetic (seeded random-init bf16 weights, random token ids)",
+                  workload="Qwen3-4B-shaped text encoder, Flux mode (hidden states after layers 8, 17, 26), "
+                           "512 tokens"),
     "c5": dict(kind="zimage", d=3840, H=30, layers=30, refiners=2, cap_dim=2560, ffn=10240, t_mid=1024, lh=128,
                lw=128, cap=512, steps=8,
                workload="Z-Image-Turbo-6B-shaped S3-DiT, 1024x1024 (4096 img + 512 caption tokens), 8 NFE"),
@@ -278,6 +284,73 @@ def timed_steps(lib, step, args):
     return lib.iris_hip_event_elapsed_ms(0, 1) / args.steps, wall * 1000 / args.steps
 
 
+def qwen3_flops(c, layers=27):
+    """Per layer 2 S h (q + 2 kv) + 2 S q h + 2 S h 2I + 2 S I h for the
+    linears and 2 S^2 d H for causal attention (half of QK^T + PV)."""
+    S, h, I = c["seq"], c["h"], c["inter"]
+    qd, kd = c["H"] * 128, c["KV"] * 128
+    lin = 2 * S * h * (qd + 2 * kd) + 2 * S * qd * h + 2 * S * h * 2 * I + 2 * S * I * h
+    return layers * (lin + 2 * S * S * 128 * c["H"])
+
+
+def run_qwen3(lib, c, args):
+    t0 = time.time()
+    m = ctypes.c_void_p(lib.qwen3_model_create_synthetic(c["h"], c["inter"], c["H"], c["KV"], c["layers"],
+                                                        c["vocab"], 20250101))
+    assert m.value, lib.iris_hip_last_error().decode()
+    t_load = time.time() - t0
+    S = c["seq"]
+    rng = np.random.default_rng(1)
+    ids = rng.integers(0, c["vocab"], S).astype(np.int32)
+    mask = np.zeros(S, np.int32)
+    mask[:c["n_real"]] = 1
+
+    def step(i):
+        p = lib.qwen3_forward(m, ids.ctypes.data_as(tl.IP), mask.ctypes.data_as(tl.IP), S)
+        assert p, lib.iris_hip_last_error()
+        ctypes.CDLL(None).free(ctypes.c_void_p(p))
+
+    ms_step, wall = timed_steps(lib, step, args)
+    lib.qwen3_model_free(m)
+    # the dominant launch, on buffers of its shape: gate/up with the SwiGLU epilogue
+    h, I = c["h"], c["inter"]
+    a = tl.Dev(S * h * 2)
+    a.put(tl.to_bf16(tl.synth_f32((S * h,), 3)))
+    w = tl.Dev(2 * I * h * 2)
+    w.put(tl.to_bf16(tl.synth_f32((2 * I * h,), 9, 0, 0.02)))
+    o = tl.Dev(S * I * 2)
+    P = tl.GemmProblem
+    pr = (P * 1)(P(a.ptr, w.ptr, o.ptr, None, S, 2 * I, h, h, h, I, 3))
+    g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(pr, 1))
+    for d in (a, w, o):
+        d.close()
+    kernels = [kernel_entry("gemm_bf16_kernel: gate/up (SwiGLU epilogue), M 512", g_ms, 2.0 * S * h * 2 * I, 27,
+                            "gemm_qwen3_gateup")]
+    cfg = {"workload": c["workload"], "hidden": h, "intermediate": I, "heads": c["H"], "kv_heads": c["KV"],
+           "layers": c["layers"], "layers_run": 27, "tokens": S, "real_tokens": c["n_real"], "vocab": c["vocab"]}
+    return ms_step, wall, qwen3_flops(c), kernels, cfg, t_load
+
+
+def cpu_baseline_qwen3(c):
+    """Oracle on the host cores: one layer at 512 tokens, extrapolated to 27."""
+    orc = tl.oracle()
+    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+    tl.bind_blas(orc, threads)
+    m = ctypes.c_void_p(orc.orc_qwen3_create_synth(c["h"], c["inter"], c["H"], c["KV"], 2, 4096, 20250101))
+    S = c["seq"]
+    ids = np.random.default_rng(1).integers(0, 4096, S).astype(np.int32)
+    t0 = time.perf_counter()
+    p = orc.orc_qwen3_forward(m, ids.ctypes.data_as(tl.IP), None, S, 0)
+    t1 = time.perf_counter() - t0
+    tl.take_f32(orc, p, S * c["h"])
+    orc.orc_qwen3_free(m)
+    ms = t1 * 27 * 1000
+    return {"value": round(1000.0 / ms, 6), "unit": "encodes/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(ms, 1),
+            "sample": f"oracle (C restatement of the reference qwen3_forward, {orc.orc_blas_info().decode()}): "
+                      f"1 layer {t1:.2f} s at 512 tokens, hidden {c['h']}, extrapolated x27"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -298,14 +371,14 @@ def main():
         return
     c = CONFIGS[args.config]
     lib = tl.hip()
-    run = run_flux if c["kind"] == "flux" else run_zimage
+    run = {"flux": run_flux, "zimage": run_zimage, "qwen3": run_qwen3}[c["kind"]]
     ms_step, wall_ms, flops, kernels, cfg, t_load = run(lib, c, args)
     images_per_s = 1000.0 / (ms_step * c["steps"])   # one image per pass (CFG: both branches in one)
     dom = max(kernels, key=lambda k: k["ms_per_step"])
     result = {
-        "metric": METRIC,
+        "metric": c.get("metric", METRIC),
         "value": round(images_per_s, 4),
-        "unit": "images/s",
+        "unit": c.get("unit", "images/s"),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -315,7 +388,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded random-init bf16 weights, N(0,1) text embeddings, seeded noise latent)",
+        "data": c.get("data", "synthetic (seeded random-init bf16 weights, N(0,1) text embeddings, "
+                              "seeded noise latent)"),
         "config": cfg,
         "step_tflop": round(flops / 1e12, 3),
         "mfma_frac_step": round(flops / (ms_step * 1e-3) / PEAK_BF16, 4),
@@ -330,7 +404,7 @@ def main():
         "device": lib.iris_hip_device_name().decode(),
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(c)
+        result["cpu_baseline"] = cpu_baseline_qwen3(c) if c["kind"] == "qwen3" else cpu_baseline(c)
     print(json.dumps(result))
 
 

@@ -73,6 +73,13 @@ typedef struct {
 /* Up to 4 independent problems in one launch (e.g. the txt and img streams). */
 int iris_hip_gemm(const iris_gemm_problem_t *problems, int n_problems);
 
+/* No counterpart in the reference: one problem with K cut into `splits`
+ * chunks, for outputs with too few 256x256 tiles to fill the chip (a
+ * 512-token text encoder's N 2560 products make 20). Each chunk's f32 partial
+ * product goes to the caller's workspace (splits * M * N floats), then one
+ * kernel sums the chunks in order (deterministic) and applies the epilogue. */
+int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *d_workspace, size_t workspace_bytes);
+
 /* y[n] = act_out( sum_k W[n][k] * act_in(x[k]) + bias[n] ), W bf16 [N][K], x f32.
  * act_in: 0 none, 1 SiLU (expf). Used for the timestep MLP and modulation. */
 int iris_hip_gemv(float *d_y, const uint16_t *d_W, const float *d_x, const float *d_bias,

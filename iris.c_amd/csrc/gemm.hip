@@ -53,6 +53,11 @@ struct GemmParams {
     iris_gemm_problem_t p[MAXP];
     int tiles_m[MAXP], tiles_n[MAXP], tile_start[MAXP + 1];
     int nprob, total, per_xcd;
+    /* split-K (one problem): block t works on K chunk t / (tiles) and writes
+     * its f32 partial product to ws + chunk * ws_stride */
+    int splits, kchunk;
+    float *ws;
+    long long ws_stride;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in a tile */
@@ -78,8 +83,21 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
     for (int i = 1; i < MAXP; i++)
         if (i < P.nprob && L >= P.tile_start[i]) pi = i;
-    const iris_gemm_problem_t pr = P.p[pi];
-    const int t = L - P.tile_start[pi];
+    iris_gemm_problem_t pr = P.p[pi];
+    int t = L - P.tile_start[pi];
+    if (P.splits > 1) {
+        const int per = P.tiles_m[0] * P.tiles_n[0];
+        const int chunk = t / per;
+        const int k0 = chunk * P.kchunk;
+        t -= chunk * per;
+        pr.A += k0;
+        pr.W += k0;
+        pr.K = min(P.kchunk, pr.K - k0);
+        pr.out = P.ws + chunk * P.ws_stride;
+        pr.ldo = pr.N;
+        pr.vec = nullptr;
+        pr.epi = IRIS_EPI_F32;
+    }
     const int tmc = P.tiles_m[pi], tnc = P.tiles_n[pi];
     const int group = t / (GROUP_M * tnc);
     const int first_m = group * GROUP_M;
@@ -356,6 +374,51 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
 }
 
+/* Sum of the split-K partials in chunk order (deterministic), then the
+ * problem's epilogue. One thread per output element. */
+__global__ void splitk_reduce_kernel(const iris_gemm_problem_t p, const float *ws, long long stride, int splits) {
+    const int nout = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.N;
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)p.M * nout) return;
+    const int m = (int)(i / nout), c = (int)(i % nout);
+    if (p.epi == IRIS_EPI_SWIGLU) {
+        /* W rows interleaved in 32-row gate / up groups */
+        const int gc = (c >> 5) * 64 + (c & 31);
+        float g = 0.0f, u = 0.0f;
+        for (int k = 0; k < splits; k++) {
+            g += ws[k * stride + (size_t)m * p.N + gc];
+            u += ws[k * stride + (size_t)m * p.N + gc + 32];
+        }
+        ((uint16_t *)p.out)[(size_t)m * p.ldo + c] = f2bf_hw(silu_fast(g) * u);
+        return;
+    }
+    float s = 0.0f;
+    for (int k = 0; k < splits; k++) s += ws[k * stride + (size_t)m * p.N + c];
+    switch (p.epi) {
+    case IRIS_EPI_F32: ((float *)p.out)[(size_t)m * p.ldo + c] = s + (p.vec ? p.vec[c] : 0.0f); break;
+    case IRIS_EPI_BF16: ((uint16_t *)p.out)[(size_t)m * p.ldo + c] = f2bf_hw(s + (p.vec ? p.vec[c] : 0.0f)); break;
+    case IRIS_EPI_GATED_ADD: ((float *)p.out)[(size_t)m * p.ldo + c] += (p.vec ? p.vec[c] : 1.0f) * s; break;
+    case IRIS_EPI_F32_T: ((float *)p.out)[(size_t)c * p.ldo + m] = s + (p.vec ? p.vec[c] : 0.0f); break;
+    default: break;
+    }
+}
+
+int check_problem(const iris_gemm_problem_t &p) {
+    if (p.K <= 0 || p.K % BK) return iris_set_error("gemm: K=%d must be a positive multiple of %d", p.K, BK);
+    if (p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
+        return iris_set_error("gemm: lda=%d ldw=%d must be multiples of 8 and >= K=%d", p.lda, p.ldw, p.K);
+    if (((uintptr_t)p.A | (uintptr_t)p.W) & 15) return iris_set_error("gemm: A/W must be 16-byte aligned");
+    if (!p.A || !p.W || !p.out) return iris_set_error("gemm: null operand");
+    if (p.epi == IRIS_EPI_SWIGLU && (p.N % 64)) return iris_set_error("gemm: SwiGLU needs N %% 64 == 0");
+    if (p.epi < 0 || p.epi > IRIS_EPI_F32_T) return iris_set_error("gemm: epilogue %d", p.epi);
+    const int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
+    if (p.ldo < ldo_need) return iris_set_error("gemm: ldo=%d < %d", p.ldo, ldo_need);
+    /* 32-bit buffer offsets: one tile's rows must span < 2 GiB */
+    if ((long long)BM * p.lda * 2 >= (1LL << 31) || (long long)BN * p.ldw * 2 >= (1LL << 31))
+        return iris_set_error("gemm: leading dimension too large");
+    return 0;
+}
+
 }  // namespace
 
 extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
@@ -369,18 +432,7 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
         P.p[i] = p;
         P.tile_start[i] = total;
         if (p.M <= 0 || p.N <= 0) { P.tiles_m[i] = P.tiles_n[i] = 0; continue; }
-        if (p.K <= 0 || p.K % BK) return iris_set_error("gemm: K=%d must be a positive multiple of %d", p.K, BK);
-        if (p.lda % 8 || p.ldw % 8 || p.lda < p.K || p.ldw < p.K)
-            return iris_set_error("gemm: lda=%d ldw=%d must be multiples of 8 and >= K=%d", p.lda, p.ldw, p.K);
-        if (((uintptr_t)p.A | (uintptr_t)p.W) & 15) return iris_set_error("gemm: A/W must be 16-byte aligned");
-        if (!p.A || !p.W || !p.out) return iris_set_error("gemm: null operand");
-        if (p.epi == IRIS_EPI_SWIGLU && (p.N % 64)) return iris_set_error("gemm: SwiGLU needs N %% 64 == 0");
-        if (p.epi < 0 || p.epi > IRIS_EPI_F32_T) return iris_set_error("gemm: epilogue %d", p.epi);
-        const int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
-        if (p.ldo < ldo_need) return iris_set_error("gemm: ldo=%d < %d", p.ldo, ldo_need);
-        /* 32-bit buffer offsets: one tile's rows must span < 2 GiB */
-        if ((long long)BM * p.lda * 2 >= (1LL << 31) || (long long)BN * p.ldw * 2 >= (1LL << 31))
-            return iris_set_error("gemm: leading dimension too large");
+        if (check_problem(p)) return -1;
         P.tiles_m[i] = (p.M + BM - 1) / BM;
         P.tiles_n[i] = (p.N + BN - 1) / BN;
         total += P.tiles_m[i] * P.tiles_n[i];
@@ -391,4 +443,36 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     P.per_xcd = (total + 7) / 8;
     hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
+}
+
+extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, float *ws, size_t ws_bytes) {
+    if (splits <= 1) return iris_hip_gemm(p, 1);
+    if (p->M <= 0 || p->N <= 0) return 0;
+    if (check_problem(*p)) return -1;
+    const int nk = p->K / BK;
+    const int kchunk = (nk + splits - 1) / splits * BK;
+    const int chunks = (p->K + kchunk - 1) / kchunk;
+    const long long stride = (long long)p->M * p->N;
+    if (!ws || ((uintptr_t)ws & 15) || (size_t)chunks * stride * sizeof(float) > ws_bytes)
+        return iris_set_error("gemm_splitk: workspace of %zu bytes for %d x %d x %d f32", ws_bytes, chunks, p->M,
+                              p->N);
+    GemmParams P;
+    memset(&P, 0, sizeof(P));
+    P.nprob = 1;
+    P.p[0] = *p;
+    P.tiles_m[0] = (p->M + BM - 1) / BM;
+    P.tiles_n[0] = (p->N + BN - 1) / BN;
+    P.total = P.tiles_m[0] * P.tiles_n[0] * chunks;
+    for (int i = 1; i <= MAXP; i++) P.tile_start[i] = P.total;
+    P.per_xcd = (P.total + 7) / 8;
+    P.splits = chunks;
+    P.kchunk = kchunk;
+    P.ws = ws;
+    P.ws_stride = stride;
+    hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    if (iris_launch_check("gemm_bf16_kernel")) return -1;
+    const size_t n_out = (size_t)p->M * (p->epi == IRIS_EPI_SWIGLU ? p->N / 2 : p->N);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
+                       ws, stride, chunks);
+    return iris_launch_check("splitk_reduce_kernel");
 }

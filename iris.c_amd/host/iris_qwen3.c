@@ -53,6 +53,8 @@ struct qwen3_model {
     float *x, *out;           /* x [S][h] residual stream; out [S][3h] */
     uint16_t *a, *qkv, *q, *k, *vt, *attn, *mlp;
     float *rope_cos, *rope_sin;   /* [S][128], value of pair p at 2p and 2p+1 */
+    float *ws;                    /* split-K partial products */
+    size_t ws_bytes;
 };
 
 /* position of permuted dim j in the reference's head layout */
@@ -173,7 +175,7 @@ static void free_model(qwen3_model_t *m) {
     iris_hip_free(m->ids); iris_hip_free(m->x); iris_hip_free(m->out);
     iris_hip_free(m->a); iris_hip_free(m->qkv); iris_hip_free(m->q); iris_hip_free(m->k); iris_hip_free(m->vt);
     iris_hip_free(m->attn); iris_hip_free(m->mlp);
-    iris_hip_free(m->rope_cos); iris_hip_free(m->rope_sin);
+    iris_hip_free(m->rope_cos); iris_hip_free(m->rope_sin); iris_hip_free(m->ws);
     free(m);
 }
 
@@ -228,6 +230,8 @@ static int alloc_work(qwen3_model_t *m) {
     QA(m->vt, kd * S * 2);
     QA(m->attn, S * qd * 2);
     QA(m->mlp, S * (size_t)m->inter * 2);
+    m->ws_bytes = (size_t)64 << 20;
+    QA(m->ws, m->ws_bytes);
 #undef QA
     return 0;
 }
@@ -365,6 +369,18 @@ static iris_gemm_problem_t prob(const uint16_t *A, int lda, const uint16_t *W, i
     return p;
 }
 
+/* At 512 tokens the N 2560 products are 20 tiles of 256x256 and the QKV
+ * product 48: K is split so about 256 blocks run, up to what the workspace
+ * holds, with at least 8 K-steps per chunk. */
+static int gemm(qwen3_model_t *m, const iris_gemm_problem_t *p) {
+    const int tiles = ((p->M + 255) / 256) * ((p->N + 255) / 256);
+    int splits = tiles >= 128 ? 1 : 256 / tiles;
+    if (splits > p->K / 64 / 8) splits = p->K / 64 / 8;
+    while (splits > 1 && (size_t)splits * p->M * p->N * sizeof(float) > m->ws_bytes) splits--;
+    if (splits > 1) return iris_hip_gemm_splitk(p, splits, m->ws, m->ws_bytes);
+    return iris_hip_gemm(p, 1);
+}
+
 static int rms(const qwen3_model_t *m, const float *w, int S) {
     iris_norm_args_t a;
     memset(&a, 0, sizeof(a));
@@ -381,7 +397,7 @@ static int layer_forward(qwen3_model_t *m, const qlayer_t *l, int S, int n_real)
     iris_gemm_problem_t p;
     CK(rms(m, l->ln1, S));
     p = prob(m->a, h, l->qkv, h, m->qkv, qd + 2 * kd, S, qd + 2 * kd, h, IRIS_EPI_BF16);
-    CK(iris_hip_gemm(&p, 1));
+    CK(gemm(m, &p));
     iris_qkprep_args_t q;
     memset(&q, 0, sizeof(q));
     q.qkv = m->qkv; q.ld_qkv = qd + 2 * kd; q.col_k = qd; q.col_v = qd + kd;
@@ -401,12 +417,12 @@ static int layer_forward(qwen3_model_t *m, const qlayer_t *l, int S, int n_real)
     CK(iris_hip_attention(&at));
     /* o_proj + residual (:461-466, :514-517) */
     p = prob(m->attn, qd, l->o, qd, m->x, h, S, h, qd, IRIS_EPI_GATED_ADD);
-    CK(iris_hip_gemm(&p, 1));
+    CK(gemm(m, &p));
     CK(rms(m, l->ln2, S));
     p = prob(m->a, h, l->gate_up, h, m->mlp, I, S, 2 * I, h, IRIS_EPI_SWIGLU);
-    CK(iris_hip_gemm(&p, 1));
+    CK(gemm(m, &p));
     p = prob(m->mlp, I, l->down, I, m->x, h, S, h, I, IRIS_EPI_GATED_ADD);
-    CK(iris_hip_gemm(&p, 1));
+    CK(gemm(m, &p));
     return 0;
 }
 

@@ -174,7 +174,7 @@ float *orc_qwen3_forward(orc_qwen3_t *m, const int *ids, const int *mask, int se
     const int qd = nh * hd, kd = nkv * hd, half = hd / 2, group = nh / nkv;
     const int last = m->mode ? m->layers - 2 : 26;
     const int stop = last_limit >= 0 && last_limit < last ? last_limit : last;
-    if (last < 0 || last >= m->layers) return NULL;
+    if (stop < 0 || stop >= m->layers) return NULL;
     const int text_dim = (m->mode ? 1 : 3) * h;
     float *x = calloc((size_t)seq * h, 4), *res = malloc((size_t)seq * h * 4), *nrm = malloc((size_t)seq * h * 4);
     float *q = malloc((size_t)seq * qd * 4), *k = malloc((size_t)seq * kd * 4), *v = malloc((size_t)seq * kd * 4);

@@ -115,6 +115,52 @@ def test_gemm_repeat_bitwise_mixed_k(lib):
             assert np.array_equal(first, got), f"launch {rep} differs from the first"
 
 
+@pytest.mark.parametrize("M,N,K,splits", [(512, 2560, 4096, 8), (77, 640, 960, 7), (300, 384, 192, 3)])
+def test_gemm_splitk_epilogues(lib, M, N, K, splits):
+    """Split-K against the float64 product for every epilogue, and bitwise
+    repeatable (the chunks are summed in a fixed order)."""
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K), np.float32)
+    W = rng.standard_normal((N, K), np.float32) * 0.05
+    vec = rng.standard_normal(N).astype(np.float32)
+    x0 = rng.standard_normal((M, N), np.float32)
+    dA, dW, dV = tl.Dev.of(tl.to_bf16(A)), tl.Dev.of(tl.to_bf16(W)), tl.Dev.of(vec)
+    ws_bytes = splits * M * N * 4
+    ws = tl.Dev(ws_bytes)
+    ref = bf(A).astype(np.float64) @ bf(W).astype(np.float64).T
+    lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    P = tl.GemmProblem
+
+    def run(out, epi, ldo, v=None):
+        pr = P(dA.ptr, dW.ptr, out.ptr, v, M, N, K, K, K, ldo, epi)
+        assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+
+    o = tl.Dev(M * N * 4)
+    run(o, EPI_F32, N, dV.ptr)
+    first = o.get(np.float32, (M, N))
+    assert tl.rel_l2(first, ref + vec) < 1e-5
+    run(o, EPI_F32, N, dV.ptr)
+    assert np.array_equal(first, o.get(np.float32, (M, N)))
+    o16 = tl.Dev(M * N * 2)
+    run(o16, EPI_BF16, N)
+    assert tl.rel_l2(tl.bf16_to_f32(o16.get(np.uint16, (M, N))), ref) < 4e-3
+    ox = tl.Dev.of(x0)
+    run(ox, EPI_GATED_ADD, N, dV.ptr)
+    assert tl.rel_l2(ox.get(np.float32, (M, N)), x0 + vec * ref) < 1e-5
+    ot = tl.Dev(M * N * 4)
+    run(ot, EPI_F32_T, M, dV.ptr)
+    assert tl.rel_l2(ot.get(np.float32, (N, M)), (ref + vec).T) < 1e-5
+    if N % 64 == 0:
+        osw = tl.Dev(M * (N // 2) * 2)
+        run(osw, EPI_SWIGLU, N // 2)
+        g = np.concatenate([ref[:, c * 64:c * 64 + 32] for c in range(N // 64)], 1)
+        u = np.concatenate([ref[:, c * 64 + 32:c * 64 + 64] for c in range(N // 64)], 1)
+        assert tl.rel_l2(tl.bf16_to_f32(osw.get(np.uint16, (M, N // 2))), g / (1 + np.exp(-g)) * u) < 4e-3
+    pr = P(dA.ptr, dW.ptr, o.ptr, None, M, N, K, K, K, N, EPI_F32)
+    assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) != 0
+
+
 def attention_ref(q, k, v, scale, valid=None):
     s = q.astype(np.float64) @ k.astype(np.float64).T * scale
     if valid is not None:
