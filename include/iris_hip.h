@@ -57,7 +57,8 @@ enum {
     IRIS_EPI_GATED_ADD = 2,  /* out f32[M,ldo] += vec[n] * acc  (vec NULL: += acc)   */
     IRIS_EPI_SWIGLU = 3,     /* W rows interleaved in 32-row gate/up groups:
                                 out bf16[M,ldo] col j = silu(gate_j) * up_j         */
-    IRIS_EPI_F32_T = 4       /* out f32[n*ldo + m] = acc (+ vec[n] bias): transposed */
+    IRIS_EPI_F32_T = 4,      /* out f32[n*ldo + m] = acc (+ vec[n] bias): transposed */
+    IRIS_EPI_ADD = 5         /* out f32[M,ldo] += acc (+ vec[n] bias): residual add  */
 };
 
 typedef struct {
@@ -79,6 +80,60 @@ int iris_hip_gemm(const iris_gemm_problem_t *problems, int n_problems);
  * product goes to the caller's workspace (splits * M * N floats), then one
  * kernel sums the chunks in order (deterministic) and applies the epilogue. */
 int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *d_workspace, size_t workspace_bytes);
+
+/* 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM on the MFMA
+ * kernel above (replaces vae_conv2d -> iris_conv2d for the 3x3 convolutions,
+ * iris_vae.c:148-166, iris_kernels.c:363): the A tiles are gathered from the
+ * image by the loads themselves, no im2col buffer.
+ *   out[y*W + x][n] = sum_{tap, c} in[(y+dy) >> up][(x+dx) >> up][c] * wt[n][tap][c]
+ * with tap = 3 (dy + 1) + (dx + 1), then the epilogue (F32 / BF16 with bias,
+ * or ADD: out f32 += conv + bias). in bf16 NHWC [(H >> up)][(W >> up)][cin],
+ * cin a power of two >= 64; wt bf16 [cout][9][cin]; out [H*W][ldo].
+ * up = 1 reads the input through a nearest-neighbour 2x upsample
+ * (iris_upsample_nearest followed by the conv, iris_vae.c:957-965).
+ * splits > 1 splits K over blocks into the f32 workspace ws (splits * H*W *
+ * cout floats) and reduces in order (deterministic). */
+typedef struct {
+    const uint16_t *in;
+    const uint16_t *wt;
+    void *out;
+    const float *bias;
+    int H, W, cin, cout, up, ldo, epi;
+    int splits;
+    float *ws;
+    size_t ws_bytes;
+} iris_conv3x3_t;
+int iris_hip_conv3x3(const iris_conv3x3_t *c);
+
+/* ---- VAE decoder kernels (vae.hip), channels-last (NHWC) activations ---- */
+/* GroupNorm (iris_group_norm, iris_kernels.c:542) in three launches:
+ * per-block float64 channel sums of x (f32, or bf16 if is_bf16) over
+ * `pixels` rows of C channels into part (>= nblk * C * 2 doubles; returns the
+ * number of blocks used, < 0 on error), per-group finalize into
+ * ab[2][C] = (gamma / std, beta - mean * gamma / std), and the apply pass
+ * y = act(x * ab[0][c] + ab[1][c]) in bf16 with act = swish
+ * (iris_vae.c:195) or identity; raw, if not NULL, receives x in bf16. */
+int iris_hip_gn_stats(const void *d_x, int is_bf16, int pixels, int C, double *d_part, int nblk);
+int iris_hip_gn_finalize(const double *d_part, int nblk, int pixels, int C, int groups, const float *d_gamma,
+                         const float *d_beta, float eps, float *d_ab);
+int iris_hip_gn_apply(const void *d_x, int is_bf16, const float *d_ab, int pixels, int C, int swish, uint16_t *d_y,
+                      uint16_t *d_raw);
+/* Latent [4z][h][w] f32 -> bf16 [2h][2w][64]: denormalize (x * sc + sh, or
+ * x / sc + sh if divide), unpatchify 2x2, 1x1 post_quant_conv (pqw [z][z],
+ * NULL to skip), channels z..63 zero (iris_vae.c:860-897). z <= 32. */
+int iris_hip_vae_front(uint16_t *d_out, const float *d_latent, int z, int h, int w, const float *d_sc,
+                       const float *d_sh, int divide, const float *d_pqw, const float *d_pqb);
+/* Row softmax, f32 scores [rows][ld_s] -> bf16 [rows][ld_p], columns
+ * cols..cols_pad-1 zeroed (iris_softmax in attnblock_forward, iris_vae.c:335). */
+int iris_hip_softmax_bf16(uint16_t *d_p, int ld_p, int cols_pad, const float *d_s, int ld_s, int rows, int cols);
+/* dst[c][r] = src[r][c] (bf16), rows..rows_pad-1 zero-filled; rows_pad % 64 == 0 */
+int iris_hip_transpose_bf16(uint16_t *d_dst, int ld_dst, int rows_pad, const uint16_t *d_src, int ld_src, int rows,
+                            int cols);
+/* conv_out 3x3 cin -> 3 plus the [-1,1] -> uint8 conversion (iris_vae.c:968-994):
+ * g bf16 [H][W][cin], wt f32 [9][cin][4], bias f32[3]; rgb uint8 [H][W][3];
+ * f32 (or NULL) receives the conv output as [3][H][W]. */
+int iris_hip_vae_conv_out(uint8_t *d_rgb, float *d_f32, const uint16_t *d_g, int H, int W, int cin,
+                          const float *d_wt, const float *d_bias);
 
 /* y[n] = act_out( sum_k W[n][k] * act_in(x[k]) + bias[n] ), W bf16 [N][K], x f32.
  * act_in: 0 none, 1 SiLU (expf). Used for the timestep MLP and modulation. */

@@ -28,6 +28,9 @@ void iris_synth_fill_f32(float *dst, size_t n, uint64_t seed, uint64_t first, fl
 void iris_synth_fill_bf16(uint16_t *dst, size_t n, uint64_t seed, uint64_t first, float mean, float std);
 /* Stable per-tensor seed: FNV-1a of the tensor name mixed with a model seed. */
 uint64_t iris_synth_seed(uint64_t model_seed, const char *name);
+/* Mean and std of a random-init VAE tensor by name (norm scales ~1, biases
+ * small, conv weights 1 / sqrt(fan_in)). */
+void iris_synth_vae_stats(const char *name, int fan_in, float *mean, float *std);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,13 @@ struct GemmParams {
     int splits, kchunk;
     float *ws;
     long long ws_stride;
+    /* implicit 3x3 convolution (one problem, CONV kernels only): A is the bf16
+     * NHWC input of (conv_h >> up) x (conv_w >> up) pixels, 2^cin_bshift bytes
+     * per pixel; output row m is pixel (m / conv_w, m % conv_w) and K index
+     * tap * cin + c reads channel c of the pixel at offset
+     * (tap / 3 - 1, tap % 3 - 1) */
+    int conv_h, conv_w, conv_up, conv_cpt_shift, conv_cin_bshift;
+    unsigned conv_in_bytes;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in a tile */
@@ -70,6 +77,7 @@ constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+template <bool CONV>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
@@ -85,12 +93,14 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         if (i < P.nprob && L >= P.tile_start[i]) pi = i;
     iris_gemm_problem_t pr = P.p[pi];
     int t = L - P.tile_start[pi];
+    int kt0 = 0;   /* first K step of this block's chunk (split-K convolution) */
     if (P.splits > 1) {
         const int per = P.tiles_m[0] * P.tiles_n[0];
         const int chunk = t / per;
         const int k0 = chunk * P.kchunk;
         t -= chunk * per;
-        pr.A += k0;
+        if (CONV) kt0 = k0 / BK;
+        else pr.A += k0;
         pr.W += k0;
         pr.K = min(P.kchunk, pr.K - k0);
         pr.out = P.ws + chunk * P.ws_stride;
@@ -123,25 +133,57 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
     const int a_rows = min(BM, pr.M - m0), w_rows = min(BN, pr.N - n0);
-    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)a_base, (short)0, a_rows * pr.lda * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t a_rsrc =
+        CONV ? __builtin_amdgcn_make_buffer_rsrc((void *)pr.A, (short)0, (int)P.conv_in_bytes, 0x00020000)
+             : __builtin_amdgcn_make_buffer_rsrc((void *)a_base, (short)0, a_rows * pr.lda * 2, 0x00020000);
     const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)w_base, (short)0, w_rows * pr.ldw * 2, 0x00020000);
     const int drow = lane >> 3, dch = lane & 7;
-    int a_voff[2], w_voff[2];
+    int a_voff[2], w_voff[2], a_chunk[2];
 #pragma unroll
     for (int par = 0; par < 2; par++) {
         const int c = dch ^ ((4 * par + (drow >> 1)) & 7);
         const int row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
         a_voff[par] = (row * pr.lda + c * 8) * 2;
         w_voff[par] = (row * pr.ldw + c * 8) * 2;
+        a_chunk[par] = c * 16;
     }
     const int a_step = DMA_ROWS * pr.lda * 2, w_step = DMA_ROWS * pr.ldw * 2;
-    auto dma_a = [&](uint16_t *stage, int kt) {
+    /* convolution: the output pixel of each row this lane loads, y << 16 | x;
+     * rows past M get y = 0x4000, outside every image */
+    uint32_t pix[DMA_PER_WAVE];
+    if (CONV) {
 #pragma unroll
-        for (int i = 0; i < DMA_PER_WAVE; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
-                                                     a_voff[i & 1] + i * a_step, kt * BK * 2, 0, 0);
+        for (int i = 0; i < DMA_PER_WAVE; i++) {
+            const int m = m0 + gw * DMA_PER_WAVE * DMA_ROWS + i * DMA_ROWS + drow;
+            pix[i] = m < pr.M ? ((uint32_t)(m / P.conv_w) << 16) | (uint32_t)(m % P.conv_w) : 0x40000000u;
+        }
+    }
+    auto dma_a = [&](uint16_t *stage, int kt) {
+        if (CONV) {
+            /* K step kt covers channels 64 * (kt mod cin/64) .. +63 of tap kt / (cin/64);
+             * taps outside the image (zero padding) get an offset past the end of the
+             * buffer, which reads as zero */
+            const int kg = kt + kt0;
+            const int tap = kg >> P.conv_cpt_shift;
+            const int soff = (kg & ((1 << P.conv_cpt_shift) - 1)) * (BK * 2);
+            const int ty = tap / 3;
+            const int dy = ty - 1, dx = tap - 3 * ty - 1;
+            const int up = P.conv_up, win = P.conv_w >> up;
+#pragma unroll
+            for (int i = 0; i < DMA_PER_WAVE; i++) {
+                const int yy = (int)(pix[i] >> 16) + dy, xx = (int)(pix[i] & 0xffffu) + dx;
+                const bool ok = (unsigned)yy < (unsigned)P.conv_h && (unsigned)xx < (unsigned)P.conv_w;
+                const int src = ((((yy >> up) * win) + (xx >> up)) << P.conv_cin_bshift) + a_chunk[i & 1];
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
+                                                         ok ? src : (int)0x80000000u, soff, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < DMA_PER_WAVE; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512),
+                                                         16, a_voff[i & 1] + i * a_step, kt * BK * 2, 0, 0);
+        }
     };
     auto dma_w = [&](uint16_t *stage, int kt) {
 #pragma unroll
@@ -274,18 +316,21 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int colb = n0 + wn * TW_N + lg * 4;
     /* whole tile in range and 4-wide accesses aligned: one 8- or 16-byte
      * access per lane and 16x16 tile */
-    const bool full = m0 + BM <= M && n0 + BN <= N && (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 &&
-                      ((uintptr_t)vec & 15) == 0;
+    const bool aligned = (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 && ((uintptr_t)vec & 15) == 0;
+    const bool full = m0 + BM <= M && n0 + BN <= N && aligned;
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
-    case IRIS_EPI_GATED_ADD: {
+    case IRIS_EPI_GATED_ADD:
+    case IRIS_EPI_ADD: {
         const float vdef = pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f;
 #pragma unroll
         for (int ni = 0; ni < FN; ni++) {
             const int col = colb + ni * 16;
+            /* a lane's 4 columns are all in range or (N % 4 == 0 aside) all out */
+            const bool cols4 = full || (aligned && col + 3 < N);
             float v[4];
-            if (full && vec) {
+            if (cols4 && vec) {
                 const float4 t = *(const float4 *)(vec + col);
                 v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
             } else {
@@ -297,7 +342,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 const int row = rowb + mi * 16;
                 const f32x4 x = acc[mi][ni];
                 const size_t o = (size_t)row * ldo + col;
-                if (full) {
+                if (full || (cols4 && row < M)) {
                     if (pr.epi == IRIS_EPI_F32) {
                         *(float4 *)((float *)pr.out + o) = make_float4(x[0] + v[0], x[1] + v[1], x[2] + v[2], x[3] + v[3]);
                     } else if (pr.epi == IRIS_EPI_BF16) {
@@ -305,10 +350,15 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                         p.x = (uint32_t)f2bf_hw(x[0] + v[0]) | ((uint32_t)f2bf_hw(x[1] + v[1]) << 16);
                         p.y = (uint32_t)f2bf_hw(x[2] + v[2]) | ((uint32_t)f2bf_hw(x[3] + v[3]) << 16);
                         *(uint2 *)((uint16_t *)pr.out + o) = p;
-                    } else {
+                    } else if (pr.epi == IRIS_EPI_GATED_ADD) {
                         float4 *dst = (float4 *)((float *)pr.out + o);
                         float4 y = *dst;
                         y.x += v[0] * x[0]; y.y += v[1] * x[1]; y.z += v[2] * x[2]; y.w += v[3] * x[3];
+                        *dst = y;
+                    } else {
+                        float4 *dst = (float4 *)((float *)pr.out + o);
+                        float4 y = *dst;
+                        y.x += x[0] + v[0]; y.y += x[1] + v[1]; y.z += x[2] + v[2]; y.w += x[3] + v[3];
                         *dst = y;
                     }
                 } else if (row < M) {
@@ -317,7 +367,8 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                         if (col + r >= N) continue;
                         if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o + r] = x[r] + v[r];
                         else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o + r] = f2bf_hw(x[r] + v[r]);
-                        else ((float *)pr.out)[o + r] += v[r] * x[r];
+                        else if (pr.epi == IRIS_EPI_GATED_ADD) ((float *)pr.out)[o + r] += v[r] * x[r];
+                        else ((float *)pr.out)[o + r] += x[r] + v[r];
                     }
                 }
             }
@@ -399,6 +450,7 @@ __global__ void splitk_reduce_kernel(const iris_gemm_problem_t p, const float *w
     case IRIS_EPI_BF16: ((uint16_t *)p.out)[(size_t)m * p.ldo + c] = f2bf_hw(s + (p.vec ? p.vec[c] : 0.0f)); break;
     case IRIS_EPI_GATED_ADD: ((float *)p.out)[(size_t)m * p.ldo + c] += (p.vec ? p.vec[c] : 1.0f) * s; break;
     case IRIS_EPI_F32_T: ((float *)p.out)[(size_t)c * p.ldo + m] = s + (p.vec ? p.vec[c] : 0.0f); break;
+    case IRIS_EPI_ADD: ((float *)p.out)[(size_t)m * p.ldo + c] += s + (p.vec ? p.vec[c] : 0.0f); break;
     default: break;
     }
 }
@@ -410,7 +462,7 @@ int check_problem(const iris_gemm_problem_t &p) {
     if (((uintptr_t)p.A | (uintptr_t)p.W) & 15) return iris_set_error("gemm: A/W must be 16-byte aligned");
     if (!p.A || !p.W || !p.out) return iris_set_error("gemm: null operand");
     if (p.epi == IRIS_EPI_SWIGLU && (p.N % 64)) return iris_set_error("gemm: SwiGLU needs N %% 64 == 0");
-    if (p.epi < 0 || p.epi > IRIS_EPI_F32_T) return iris_set_error("gemm: epilogue %d", p.epi);
+    if (p.epi < 0 || p.epi > IRIS_EPI_ADD) return iris_set_error("gemm: epilogue %d", p.epi);
     const int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
     if (p.ldo < ldo_need) return iris_set_error("gemm: ldo=%d < %d", p.ldo, ldo_need);
     /* 32-bit buffer offsets: one tile's rows must span < 2 GiB */
@@ -441,7 +493,7 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
 }
 
@@ -469,10 +521,75 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     P.kchunk = kchunk;
     P.ws = ws;
     P.ws_stride = stride;
-    hipLaunchKernelGGL(gemm_bf16_kernel, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel")) return -1;
     const size_t n_out = (size_t)p->M * (p->epi == IRIS_EPI_SWIGLU ? p->N / 2 : p->N);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
                        ws, stride, chunks);
+    return iris_launch_check("splitk_reduce_kernel");
+}
+
+extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
+    if (!c || !c->in || !c->wt || !c->out) return iris_set_error("conv3x3: null operand");
+    if (c->cin < 64 || c->cin > 8192 || (c->cin & (c->cin - 1)))
+        return iris_set_error("conv3x3: cin=%d must be a power of two in 64..8192", c->cin);
+    if (c->up != 0 && c->up != 1) return iris_set_error("conv3x3: up=%d (0 or 1)", c->up);
+    if (c->H <= 0 || c->W <= 0 || c->H > 16000 || c->W > 16000 || (c->up && ((c->H | c->W) & 1)))
+        return iris_set_error("conv3x3: output %dx%d", c->H, c->W);
+    if (c->epi != IRIS_EPI_F32 && c->epi != IRIS_EPI_BF16 && c->epi != IRIS_EPI_ADD)
+        return iris_set_error("conv3x3: epilogue %d (F32, BF16 or ADD)", c->epi);
+    const size_t in_bytes = (size_t)(c->H >> c->up) * (size_t)(c->W >> c->up) * (size_t)c->cin * 2;
+    if (in_bytes >= (1ull << 31)) return iris_set_error("conv3x3: input of %zu bytes (< 2 GiB)", in_bytes);
+    if ((long long)c->H * c->W >= (1LL << 31)) return iris_set_error("conv3x3: too many pixels");
+    iris_gemm_problem_t p;
+    p.A = c->in;
+    p.W = c->wt;
+    p.out = c->out;
+    p.vec = c->bias;
+    p.M = c->H * c->W;
+    p.N = c->cout;
+    p.K = 9 * c->cin;
+    p.lda = p.ldw = p.K;
+    p.ldo = c->ldo;
+    p.epi = c->epi;
+    if (p.N <= 0) return 0;
+    if (check_problem(p)) return -1;
+    GemmParams P;
+    memset(&P, 0, sizeof(P));
+    P.nprob = 1;
+    P.p[0] = p;
+    P.tiles_m[0] = (p.M + BM - 1) / BM;
+    P.tiles_n[0] = (p.N + BN - 1) / BN;
+    P.conv_h = c->H;
+    P.conv_w = c->W;
+    P.conv_up = c->up;
+    P.conv_cpt_shift = __builtin_ctz((unsigned)c->cin) - 6;
+    P.conv_cin_bshift = __builtin_ctz((unsigned)c->cin) + 1;
+    P.conv_in_bytes = (unsigned)in_bytes;
+    int chunks = 1;
+    long long stride = 0;
+    if (c->splits > 1) {
+        const int nk = p.K / BK;
+        P.kchunk = (nk + c->splits - 1) / c->splits * BK;
+        chunks = (p.K + P.kchunk - 1) / P.kchunk;
+        stride = (long long)p.M * p.N;
+        if (!c->ws || ((uintptr_t)c->ws & 15) || (size_t)chunks * stride * sizeof(float) > c->ws_bytes)
+            return iris_set_error("conv3x3: split-K workspace of %zu bytes for %d x %d x %d f32", c->ws_bytes, chunks,
+                                  p.M, p.N);
+    }
+    P.total = P.tiles_m[0] * P.tiles_n[0] * chunks;
+    for (int i = 1; i <= MAXP; i++) P.tile_start[i] = P.total;
+    P.per_xcd = (P.total + 7) / 8;
+    if (chunks > 1) {
+        P.splits = chunks;
+        P.ws = c->ws;
+        P.ws_stride = stride;
+    }
+    hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    if (iris_launch_check("gemm_bf16_kernel<conv>")) return -1;
+    if (chunks == 1) return 0;
+    const size_t n_out = (size_t)p.M * p.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), p,
+                       c->ws, stride, chunks);
     return iris_launch_check("splitk_reduce_kernel");
 }

@@ -5,6 +5,7 @@
 #include "iris_st.h"
 
 #include <math.h>
+#include <string.h>
 
 static inline uint64_t splitmix64(uint64_t z) {
     z += 0x9e3779b97f4a7c15ULL;
@@ -38,4 +39,22 @@ uint64_t iris_synth_seed(uint64_t model_seed, const char *name) {
         h *= 0x100000001b3ULL;
     }
     return splitmix64(h ^ splitmix64(model_seed));
+}
+
+/* Mean and standard deviation of a random-init VAE tensor, from its name:
+ * norm scales ~1, biases and batch-norm means small, batch-norm variances
+ * ~1, convolution weights 1 / sqrt(fan_in) (half that for decoder.conv_out,
+ * which keeps most output pixels inside [-1, 1]). */
+void iris_synth_vae_stats(const char *name, int fan_in, float *mean, float *std) {
+    size_t n = strlen(name);
+#define ENDS(s) (n >= sizeof(s) - 1 && strcmp(name + n - (sizeof(s) - 1), s) == 0)
+    if (ENDS("running_var")) { *mean = 1.0f; *std = 0.1f; }
+    else if (ENDS("running_mean")) { *mean = 0.0f; *std = 0.1f; }
+    else if (ENDS(".bias")) { *mean = 0.0f; *std = 0.05f; }
+    else if (strstr(name, "norm") && ENDS(".weight")) { *mean = 1.0f; *std = 0.1f; }
+    else {
+        *mean = 0.0f;
+        *std = (strcmp(name, "decoder.conv_out.weight") == 0 ? 0.5f : 1.0f) / sqrtf((float)(fan_in > 0 ? fan_in : 1));
+    }
+#undef ENDS
 }

@@ -43,6 +43,7 @@
 typedef struct orc_flux orc_flux_t;
 typedef struct orc_zi orc_zi_t;
 typedef struct orc_qwen3 orc_qwen3_t;
+typedef struct orc_vae orc_vae_t;
 
 typedef struct {
     const float *latent;
@@ -125,5 +126,15 @@ void orc_qwen3_free(orc_qwen3_t *m);
 void orc_qwen3_set_mode(orc_qwen3_t *m, int mode);
 int orc_qwen3_dims(const orc_qwen3_t *m, int *out4);   /* hidden, layers, text_dim, head_dim */
 float *orc_qwen3_forward(orc_qwen3_t *m, const int *ids, const int *mask, int seq, int last_limit);
+
+/* VAE decoder (orc_vae.c, iris_vae.c): weights from a diffusers-layout
+ * safetensors file or synthetic (iris_synth_vae_stats); z_channels 32 or 16,
+ * scaling 0 = batch-norm denormalization. decode writes rgb [16lh][16lw][3]
+ * and the pre-quantization f32 [3][16lh][16lw]; stop_after >= 0 returns the
+ * channel count of the activation after that many stages, copied to f32. */
+orc_vae_t *orc_vae_load(const char *path, int z, float scaling, float shift);
+orc_vae_t *orc_vae_create_synth(int z, float scaling, float shift, uint64_t seed);
+void orc_vae_free(orc_vae_t *v);
+int orc_vae_decode(orc_vae_t *v, const float *latent, int lh, int lw, uint8_t *rgb, float *f32, int stop_after);
 
 #endif

@@ -57,6 +57,13 @@ def oracle():
                                              ctypes.c_float, ctypes.c_float]
         lib.iris_synth_fill_f32.argtypes = [FP, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64,
                                             ctypes.c_float, ctypes.c_float]
+        lib.orc_vae_load.restype = ctypes.c_void_p
+        lib.orc_vae_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        lib.orc_vae_create_synth.restype = ctypes.c_void_p
+        lib.orc_vae_create_synth.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]
+        lib.orc_vae_free.argtypes = [ctypes.c_void_p]
+        lib.orc_vae_decode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, FP,
+                                       ctypes.c_int]
         _libs["oracle"] = lib
         bind_blas(lib)
     return _libs["oracle"]
@@ -94,6 +101,12 @@ class AttnArgs(ctypes.Structure):
                 ("scale", ctypes.c_float), ("kv_lo0", ctypes.c_int), ("kv_hi0", ctypes.c_int),
                 ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int), ("causal", ctypes.c_int),
                 ("kv_group", ctypes.c_int)]
+
+
+class IrisImage(ctypes.Structure):
+    """iris_image (reference iris.h:73-78, include/iris_vae.h)"""
+    _fields_ = [("width", ctypes.c_int), ("height", ctypes.c_int), ("channels", ctypes.c_int),
+                ("data", ctypes.POINTER(ctypes.c_uint8))]
 
 
 class IrisRef(ctypes.Structure):
@@ -177,6 +190,19 @@ def hip():
         lib.zi_velocity.argtypes = [vp, ctypes.c_float]
         lib.zi_step.argtypes = [vp, ctypes.c_float, ctypes.c_float]
         lib.zi_download_latent.argtypes = [vp, vp]
+        lib.iris_vae_gpu_load.restype = vp
+        lib.iris_vae_gpu_load.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        lib.iris_vae_gpu_load_dir.restype = vp
+        lib.iris_vae_gpu_load_dir.argtypes = [ctypes.c_char_p]
+        lib.iris_vae_gpu_create_synthetic.restype = vp
+        lib.iris_vae_gpu_create_synthetic.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]
+        lib.iris_vae_gpu_free.argtypes = [vp]
+        lib.iris_vae_gpu_decode_to.argtypes = [vp, FP, ctypes.c_int, ctypes.c_int, vp, FP]
+        lib.iris_vae_gpu_decode_device.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, vp]
+        lib.iris_vae_gpu_decode.restype = ctypes.POINTER(IrisImage)
+        lib.iris_vae_gpu_decode.argtypes = [vp, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_image_free.argtypes = [ctypes.POINTER(IrisImage)]
+        lib.iris_vae_gpu_z_channels.argtypes = [vp]
         if lib.iris_hip_init(0) != 0:
             raise RuntimeError("iris_hip_init failed: " + lib.iris_hip_last_error().decode())
         _libs["hip"] = lib
@@ -273,6 +299,15 @@ def ref():
         lib.qwen3_forward.restype = ctypes.c_void_p
         lib.qwen3_forward.argtypes = [ctypes.c_void_p, IP, IP, ctypes.c_int]
         lib.qwen3_set_extraction_mode.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        lib.safetensors_open.restype = ctypes.c_void_p
+        lib.safetensors_open.argtypes = [ctypes.c_char_p]
+        lib.safetensors_close.argtypes = [ctypes.c_void_p]
+        lib.iris_vae_load_safetensors_ex.restype = ctypes.c_void_p
+        lib.iris_vae_load_safetensors_ex.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        lib.iris_vae_decode.restype = ctypes.POINTER(IrisImage)
+        lib.iris_vae_decode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_vae_free.argtypes = [ctypes.c_void_p]
+        lib.iris_image_free.argtypes = [ctypes.POINTER(IrisImage)]
         _libs["ref"] = lib
     return _libs["ref"]
 
@@ -313,11 +348,13 @@ def bf16_to_f32(a):
 
 
 def write_safetensors(path, tensors):
-    """tensors: list of (name, uint16 array) written as BF16."""
+    """tensors: list of (name, array): uint16 arrays are written as BF16,
+    float32 arrays as F32."""
     header, off, blobs = {}, 0, []
     for name, arr in tensors:
         b = np.ascontiguousarray(arr).tobytes()
-        header[name] = {"dtype": "BF16", "shape": list(arr.shape), "data_offsets": [off, off + len(b)]}
+        dt = "F32" if arr.dtype == np.float32 else "BF16"
+        header[name] = {"dtype": dt, "shape": list(arr.shape), "data_offsets": [off, off + len(b)]}
         off += len(b)
         blobs.append(b)
     h = json.dumps(header).encode()
@@ -498,3 +535,62 @@ def write_qwen3_dir(d, hidden=256, inter=512, heads=4, kv_heads=2, layers=28, vo
 class Qwen3Encoder(ctypes.Structure):
     """The reference's qwen3_encoder_t (tokenizer, model) for its mode setter."""
     _fields_ = [("tokenizer", ctypes.c_void_p), ("model", ctypes.c_void_p)]
+
+
+def vae_tensor_list(z, flux=True):
+    """(name, shape) of the VAE decoder tensors in the diffusers layout the
+    reference loads (iris_vae.c:1227-1386); Flux adds bn and post_quant_conv."""
+    t = [("decoder.conv_in.weight", (512, z, 3, 3)), ("decoder.conv_in.bias", (512,))]
+
+    def res(p, cin, cout):
+        r = [(p + ".norm1.weight", (cin,)), (p + ".norm1.bias", (cin,)), (p + ".conv1.weight", (cout, cin, 3, 3)),
+             (p + ".conv1.bias", (cout,)), (p + ".norm2.weight", (cout,)), (p + ".norm2.bias", (cout,)),
+             (p + ".conv2.weight", (cout, cout, 3, 3)), (p + ".conv2.bias", (cout,))]
+        if cin != cout:
+            r += [(p + ".conv_shortcut.weight", (cout, cin, 1, 1)), (p + ".conv_shortcut.bias", (cout,))]
+        return r
+
+    t += res("decoder.mid_block.resnets.0", 512, 512) + res("decoder.mid_block.resnets.1", 512, 512)
+    a = "decoder.mid_block.attentions.0."
+    t += [(a + "group_norm.weight", (512,)), (a + "group_norm.bias", (512,))]
+    for n in ("to_q", "to_k", "to_v", "to_out.0"):
+        t += [(a + n + ".weight", (512, 512)), (a + n + ".bias", (512,))]
+    mult = [1, 2, 4, 4]
+    for i in range(4):
+        level = 3 - i
+        ch = 128 * mult[level]
+        prev = 512 if level == 3 else 128 * mult[level + 1]
+        for r in range(3):
+            t += res(f"decoder.up_blocks.{i}.resnets.{r}", prev if r == 0 else ch, ch)
+        if i < 3:
+            t += [(f"decoder.up_blocks.{i}.upsamplers.0.conv.weight", (ch, ch, 3, 3)),
+                  (f"decoder.up_blocks.{i}.upsamplers.0.conv.bias", (ch,))]
+    t += [("decoder.conv_norm_out.weight", (128,)), ("decoder.conv_norm_out.bias", (128,)),
+          ("decoder.conv_out.weight", (3, 128, 3, 3)), ("decoder.conv_out.bias", (3,))]
+    if flux:
+        t += [("bn.running_mean", (4 * z,)), ("bn.running_var", (4 * z,)),
+              ("post_quant_conv.weight", (z, z, 1, 1)), ("post_quant_conv.bias", (z,))]
+    return t
+
+
+def write_vae_file(path, z=32, flux=True, seed=0, bf16=False):
+    """A random-init VAE decoder file: norm scales ~1, biases small, conv
+    weights 1/sqrt(fan_in) (conv_out half that), batch-norm variances ~1."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shape in vae_tensor_list(z, flux):
+        n = int(np.prod(shape))
+        fan = n // shape[0] if len(shape) > 1 else 1
+        if name.endswith("running_var"):
+            a = 1.0 + 0.1 * rng.standard_normal(n)
+        elif name.endswith("running_mean"):
+            a = 0.1 * rng.standard_normal(n)
+        elif name.endswith(".bias"):
+            a = 0.05 * rng.standard_normal(n)
+        elif "norm" in name:
+            a = 1.0 + 0.1 * rng.standard_normal(n)
+        else:
+            a = (0.5 if name == "decoder.conv_out.weight" else 1.0) / np.sqrt(fan) * rng.standard_normal(n)
+        a = a.astype(np.float32).reshape(shape)
+        out.append((name, to_bf16(a) if bf16 else a))
+    write_safetensors(path, out)

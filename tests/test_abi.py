@@ -47,7 +47,8 @@ DECLS = declared_functions()
 
 def test_headers_parsed():
     assert "iris_hip.h" in DECLS and "iris_transformer.h" in DECLS and "iris_sample.h" in DECLS
-    assert "iris_hip_gemm" in DECLS["iris_hip.h"]
+    assert "iris_hip_gemm" in DECLS["iris_hip.h"] and "iris_hip_conv3x3" in DECLS["iris_hip.h"]
+    assert "iris_vae_gpu_decode" in DECLS["iris_vae.h"] and "iris_image_free" in DECLS["iris_vae.h"]
     assert "iris_transformer_forward" in DECLS["iris_transformer.h"]
     assert "zi_transformer_forward" in DECLS["iris_transformer.h"]
     assert "iris_conv2d" in DECLS["iris_kernels.h"] and "iris_substep_callback" in DECLS["iris_kernels.h"]

@@ -1,0 +1,206 @@
+"""The VAE decoder's kernels through the C ABI against float64 numpy
+statements of the same operations on the same bf16-rounded inputs:
+the implicit-GEMM 3x3 convolution (padding, fused nearest upsample, ragged
+pixel counts, cout below the tile width, split-K, each epilogue), GroupNorm
++ swish, the bf16 softmax, the transpose, the latent front end and
+conv_out with the uint8 conversion."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import iris_testlib as tl
+
+pytestmark = pytest.mark.gpu
+EPI_F32, EPI_BF16, EPI_ADD = 0, 1, 5
+vp = ctypes.c_void_p
+
+
+class Conv(ctypes.Structure):
+    _fields_ = [("inp", vp), ("wt", vp), ("out", vp), ("bias", vp), ("H", ctypes.c_int), ("W", ctypes.c_int),
+                ("cin", ctypes.c_int), ("cout", ctypes.c_int), ("up", ctypes.c_int), ("ldo", ctypes.c_int),
+                ("epi", ctypes.c_int), ("splits", ctypes.c_int), ("ws", vp), ("ws_bytes", ctypes.c_size_t)]
+
+
+@pytest.fixture(scope="module")
+def lib():
+    lib = tl.hip()
+    lib.iris_hip_gn_stats.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int]
+    lib.iris_hip_gn_finalize.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp,
+                                         ctypes.c_float, vp]
+    lib.iris_hip_gn_apply.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+    lib.iris_hip_vae_front.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp, ctypes.c_int, vp,
+                                       vp]
+    lib.iris_hip_softmax_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int]
+    lib.iris_hip_transpose_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int]
+    lib.iris_hip_vae_conv_out.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+    lib.iris_hip_conv3x3.argtypes = [ctypes.POINTER(Conv)]
+    return lib
+
+
+def bf(a):
+    return tl.bf16_to_f32(tl.to_bf16(a)).astype(np.float64)
+
+
+def np_conv3(x, w, b, up):
+    """x [h][w][cin] (NHWC), w [cout][9][cin]; output [H][W][cout], H = h << up"""
+    if up:
+        x = x.repeat(2, 0).repeat(2, 1)
+    H, W, _ = x.shape
+    xp = np.pad(x, ((1, 1), (1, 1), (0, 0)))
+    out = np.zeros((H, W, w.shape[0])) + (b if b is not None else 0.0)
+    for tap in range(9):
+        dy, dx = tap // 3, tap % 3
+        out += xp[dy:dy + H, dx:dx + W, :] @ w[:, tap, :].T
+    return out
+
+
+@pytest.mark.parametrize("H,W,cin,cout,up,splits", [
+    (20, 20, 64, 128, 0, 1),      # cout below the 256-wide tile, ragged last tile
+    (16, 24, 128, 256, 1, 1),     # fused nearest upsample
+    (37, 29, 256, 64, 0, 3),      # odd sizes, split-K over 36 K steps
+    (8, 64, 512, 512, 1, 4),      # 512 channels (8 K steps per tap), upsampled, split
+])
+def test_conv3x3(lib, H, W, cin, cout, up, splits):
+    rng = np.random.default_rng(H * W + cin)
+    h, w = H >> up, W >> up
+    x = rng.standard_normal((h, w, cin)).astype(np.float32)
+    wt = (rng.standard_normal((cout, 9, cin)) / np.sqrt(9 * cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    ref = np_conv3(bf(x), bf(wt), b.astype(np.float64), up).reshape(H * W, cout)
+    dx, dw, db = tl.Dev.of(tl.to_bf16(x)), tl.Dev.of(tl.to_bf16(wt)), tl.Dev.of(b)
+    ws_bytes = max(splits, 1) * H * W * cout * 4
+    ws = tl.Dev(ws_bytes)
+
+    def run(out, epi, bias=db.ptr):
+        c = Conv(dx.ptr, dw.ptr, out.ptr, bias, H, W, cin, cout, up, cout, epi, splits, ws.ptr, ws_bytes)
+        assert lib.iris_hip_conv3x3(ctypes.byref(c)) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+
+    o = tl.Dev(H * W * cout * 4)
+    run(o, EPI_F32)
+    got = o.get(np.float32, (H * W, cout))
+    assert tl.rel_l2(got, ref) < 1e-5
+    run(o, EPI_F32)
+    assert np.array_equal(got, o.get(np.float32, (H * W, cout)))
+    o16 = tl.Dev(H * W * cout * 2)
+    run(o16, EPI_BF16)
+    assert tl.rel_l2(tl.bf16_to_f32(o16.get(np.uint16, (H * W, cout))), ref) < 4e-3
+    x0 = rng.standard_normal((H * W, cout)).astype(np.float32)
+    ox = tl.Dev.of(x0)
+    run(ox, EPI_ADD)
+    assert tl.rel_l2(ox.get(np.float32, (H * W, cout)), x0 + ref) < 1e-5
+
+
+def test_conv3x3_rejects(lib):
+    d = tl.Dev(1 << 20)
+    bad = [Conv(d.ptr, d.ptr, d.ptr, None, 8, 8, 96, 64, 0, 64, EPI_F32, 1, None, 0),     # cin not 2^k
+           Conv(d.ptr, d.ptr, d.ptr, None, 7, 8, 64, 64, 1, 64, EPI_F32, 1, None, 0),     # odd H with upsample
+           Conv(d.ptr, d.ptr, d.ptr, None, 8, 8, 64, 64, 0, 64, 3, 1, None, 0),           # SwiGLU epilogue
+           Conv(d.ptr, d.ptr, d.ptr, None, 64, 64, 64, 64, 0, 64, EPI_F32, 4, d.ptr, 16)]  # workspace too small
+    for c in bad:
+        assert lib.iris_hip_conv3x3(ctypes.byref(c)) != 0
+
+
+@pytest.mark.parametrize("pixels,C,is_bf16,swish", [(1000, 128, 0, 1), (4096, 512, 1, 1), (777, 256, 0, 0)])
+def test_group_norm(lib, pixels, C, is_bf16, swish):
+    rng = np.random.default_rng(pixels + C)
+    x = (rng.standard_normal((pixels, C)) * 3 + 1.5).astype(np.float32)
+    xin = bf(x) if is_bf16 else x.astype(np.float64)
+    g = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    cpg = C // 32
+    xr = xin.reshape(pixels, 32, cpg)
+    mean = xr.mean((0, 2), keepdims=True)
+    var = ((xr - mean) ** 2).mean((0, 2), keepdims=True)
+    y = ((xr - mean) / np.sqrt(var + 1e-4)).reshape(pixels, C) * g + b
+    if swish:
+        y = y / (1 + np.exp(-y))
+    dx = tl.Dev.of(tl.to_bf16(x) if is_bf16 else x)
+    dg, db = tl.Dev.of(g), tl.Dev.of(b)
+    part, ab = tl.Dev(64 * C * 16), tl.Dev(2 * C * 4)
+    dy, raw = tl.Dev(pixels * C * 2), tl.Dev(pixels * C * 2)
+    nblk = lib.iris_hip_gn_stats(dx.ptr, is_bf16, pixels, C, part.ptr, 64)
+    assert 0 < nblk <= 64, lib.iris_hip_last_error()
+    assert lib.iris_hip_gn_finalize(part.ptr, nblk, pixels, C, 32, dg.ptr, db.ptr, 1e-4, ab.ptr) == 0
+    assert lib.iris_hip_gn_apply(dx.ptr, is_bf16, ab.ptr, pixels, C, swish, dy.ptr, raw.ptr) == 0
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(dy.get(np.uint16, (pixels, C)))
+    assert tl.rel_l2(got, y) < 4e-3
+    assert np.array_equal(raw.get(np.uint16, (pixels, C)), tl.to_bf16(xin.astype(np.float32)))
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(3, 1024, 1024), (70, 60, 64), (5, 16384, 16384)])
+def test_softmax_bf16(lib, rows, cols, pad):
+    rng = np.random.default_rng(cols)
+    s = (rng.standard_normal((rows, pad)) * 4).astype(np.float32)
+    ds, dp = tl.Dev.of(s), tl.Dev(rows * pad * 2)
+    assert lib.iris_hip_softmax_bf16(dp.ptr, pad, pad, ds.ptr, pad, rows, cols) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(dp.get(np.uint16, (rows, pad)))
+    e = np.exp(s[:, :cols].astype(np.float64) - s[:, :cols].max(1, keepdims=True))
+    ref = e / e.sum(1, keepdims=True)
+    assert tl.rel_l2(got[:, :cols], ref) < 4e-3
+    assert not got[:, cols:].any()
+
+
+def test_transpose_bf16(lib):
+    rng = np.random.default_rng(0)
+    rows, cols, ld, pad = 100, 512, 1536, 128
+    src = rng.integers(0, 65535, (rows, ld), dtype=np.uint16)
+    ds, dd = tl.Dev.of(src), tl.Dev(cols * pad * 2)
+    assert lib.iris_hip_transpose_bf16(dd.ptr, pad, pad, ds.ptr + 1024 * 2, ld, rows, cols) == 0
+    assert lib.iris_hip_sync() == 0
+    got = dd.get(np.uint16, (cols, pad))
+    assert np.array_equal(got[:, :rows], src[:, 1024:1024 + cols].T)
+    assert not got[:, rows:].any()
+
+
+@pytest.mark.parametrize("z,divide,pq", [(32, 0, 1), (16, 1, 0)])
+def test_vae_front(lib, z, divide, pq):
+    rng = np.random.default_rng(z)
+    h, w = 5, 7
+    lat = rng.standard_normal((4 * z, h, w)).astype(np.float32)
+    sc = (1 + 0.2 * rng.random(4 * z)).astype(np.float32)
+    sh = (0.1 * rng.standard_normal(4 * z)).astype(np.float32)
+    pqw = (rng.standard_normal((z, z)) / np.sqrt(z)).astype(np.float32)
+    pqb = (0.1 * rng.standard_normal(z)).astype(np.float32)
+    x = lat / sc[:, None, None] + sh[:, None, None] if divide else lat * sc[:, None, None] + sh[:, None, None]
+    u = np.zeros((2 * h, 2 * w, z))
+    for c in range(z):
+        for pi in range(2):
+            for pj in range(2):
+                u[pi::2, pj::2, c] = x[c * 4 + pi * 2 + pj]
+    if pq:
+        u = u @ pqw.T.astype(np.float64) + pqb
+    d = [tl.Dev.of(a) for a in (lat, sc, sh, pqw, pqb)]
+    out = tl.Dev(4 * h * w * 64 * 2)
+    assert lib.iris_hip_vae_front(out.ptr, d[0].ptr, z, h, w, d[1].ptr, d[2].ptr, divide,
+                                  d[3].ptr if pq else None, d[4].ptr if pq else None) == 0
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(out.get(np.uint16, (2 * h, 2 * w, 64)))
+    assert tl.rel_l2(got[..., :z], u) < 4e-3
+    assert not got[..., z:].any()
+
+
+def test_conv_out(lib):
+    rng = np.random.default_rng(1)
+    H, W, cin = 33, 47, 128
+    g = rng.standard_normal((H, W, cin)).astype(np.float32)
+    w = (0.5 * rng.standard_normal((3, cin, 3, 3)) / np.sqrt(9 * cin)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(3)).astype(np.float32)
+    wt = np.zeros((9, cin, 4), np.float32)
+    for o in range(3):
+        wt[:, :, o] = w[o].reshape(cin, 9).T
+    ref = np_conv3(bf(g), w.reshape(3, cin, 9).transpose(0, 2, 1).astype(np.float64), b, 0)   # [H][W][3]
+    dg, dw, db = tl.Dev.of(tl.to_bf16(g)), tl.Dev.of(wt), tl.Dev.of(np.r_[b, 0].astype(np.float32))
+    rgb, f = tl.Dev(H * W * 3), tl.Dev(3 * H * W * 4)
+    assert lib.iris_hip_vae_conv_out(rgb.ptr, f.ptr, dg.ptr, H, W, cin, dw.ptr, db.ptr) == 0
+    assert lib.iris_hip_sync() == 0
+    got = f.get(np.float32, (3, H, W))
+    assert tl.rel_l2(got, ref.transpose(2, 0, 1)) < 1e-5
+    u8 = rgb.get(np.uint8, (H, W, 3))
+    v = np.clip((got.transpose(1, 2, 0) + 1.0) * 0.5 * 255.0, 0, 255)
+    assert np.array_equal(u8, (v + 0.5).astype(np.uint8))
