@@ -50,6 +50,11 @@ CONFIGS = {
                   unit="encodes/s", data="synthetic (seeded random-init bf16 weights, random token ids)",
                   workload="Qwen3-4B-shaped text encoder, Flux mode (hidden states after layers 8, 17, 26), "
                            "512 tokens"),
+    "vae": dict(kind="vae", z=32, lh=64, lw=64, steps=1,
+                metric="ms per VAE decode + decodes/s @Flux.2 VAE 1024x1024; % of bf16 MFMA peak",
+                unit="images/s", data="synthetic (seeded random-init decoder weights, N(0,1) latent)",
+                workload="Flux.2 VAE decoder, 128x64x64 latent -> 1024x1024 RGB (z_channels 32, batch-norm "
+                         "denormalization, post_quant_conv, 16384-token bottleneck attention)"),
     "c5": dict(kind="zimage", d=3840, H=30, layers=30, refiners=2, cap_dim=2560, ffn=10240, t_mid=1024, lh=128,
                lw=128, cap=512, steps=8,
                workload="Z-Image-Turbo-6B-shaped S3-DiT, 1024x1024 (4096 img + 512 caption tokens), 8 NFE"),
@@ -351,6 +356,86 @@ def cpu_baseline_qwen3(c):
                       f"1 layer {t1:.2f} s at 512 tokens, hidden {c['h']}, extrapolated x27"}
 
 
+def vae_flops(c):
+    """Algorithmic FLOPs of one decode: 2 P cin cout 9 per 3x3 conv (conv_in
+    at its real z input channels), 2 P cin cout per 1x1, and 2 S (3C) C + 4 S^2 C
+    + 2 S C C for the bottleneck attention (S pixels at 1/8 resolution)."""
+    z, h, w = c["z"], 2 * c["lh"], 2 * c["lw"]
+    S = h * w
+    f = 2 * S * z * z + 2 * S * z * 512 * 9
+
+    def res(P, ci, co):
+        return 2 * P * 9 * (ci * co + co * co) + (2 * P * ci * co if ci != co else 0)
+
+    f += 2 * res(S, 512, 512) + 2 * S * 512 * 1536 + 4 * S * S * 512 + 2 * S * 512 * 512
+    P, prev = S, 512
+    for level in (3, 2, 1, 0):
+        ch = 128 * [1, 2, 4, 4][level]
+        f += res(P, prev, ch) + 2 * res(P, ch, ch)
+        prev = ch
+        if level:
+            P *= 4
+            f += 2 * P * ch * ch * 9
+    return f + 2 * P * 128 * 3 * 9
+
+
+def run_vae(lib, c, args):
+    t0 = time.time()
+    v = ctypes.c_void_p(lib.iris_vae_gpu_create_synthetic(c["z"], 0.0, 0.0, 20250101))
+    assert v.value, lib.iris_hip_last_error().decode()
+    t_load = time.time() - t0
+    lh, lw = c["lh"], c["lw"]
+    lat = tl.Dev.of(np.random.default_rng(1).standard_normal((4 * c["z"], lh, lw)).astype(np.float32))
+    P = 256 * lh * lw
+    rgb = tl.Dev(P * 3)
+
+    def step(i):
+        assert lib.iris_vae_gpu_decode_device(v, lat.ptr, lh, lw, rgb.ptr, None) == 0, lib.iris_hip_last_error()
+
+    ms_step, wall = timed_steps(lib, step, args)
+    lib.iris_vae_gpu_free(v)
+    # the dominant launch shape: 3x3 conv 256 -> 256 at 512x512 (5 per decode)
+    H = W = 8 * lh
+    cin = cout = 256
+    x = tl.Dev(H * W * cin * 2)
+    x.put(tl.to_bf16(tl.synth_f32((H * W * cin,), 3)))
+    wt = tl.Dev(cout * 9 * cin * 2)
+    wt.put(tl.to_bf16(tl.synth_f32((cout * 9 * cin,), 9, 0, 1.0 / 48)))
+    o = tl.Dev(H * W * cout * 4)
+    conv = tl.Conv3x3(x.ptr, wt.ptr, o.ptr, None, H, W, cin, cout, 0, cout, 0, 1, None, 0)
+    c_ms = time_launches(lib, lambda: lib.iris_hip_conv3x3(ctypes.byref(conv)))
+    for d in (x, wt, o, lat, rgb):
+        d.close()
+    kernels = [kernel_entry("gemm_bf16_kernel<conv>: 3x3 conv 256->256, 512x512 pixels", c_ms,
+                            2.0 * H * W * cin * cout * 9, 5, "conv_256_512")]
+    cfg = {"workload": c["workload"], "latent": [4 * c["z"], lh, lw], "image": [16 * lh, 16 * lw],
+           "z_channels": c["z"], "bottleneck_tokens": 4 * lh * lw}
+    return ms_step, wall, vae_flops(c), kernels, cfg, t_load
+
+
+def cpu_baseline_vae(c):
+    """Oracle decode of a 256x256 image (16x16 latent) on the host cores,
+    scaled to 1024x1024 by the ratio of algorithmic FLOPs."""
+    orc = tl.oracle()
+    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+    tl.bind_blas(orc, threads)
+    os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+    v = ctypes.c_void_p(orc.orc_vae_create_synth(c["z"], 0.0, 0.0, 20250101))
+    lh = lw = 16
+    lat = np.random.default_rng(1).standard_normal((4 * c["z"], lh, lw)).astype(np.float32)
+    rgb = np.zeros(256 * lh * lw * 3, np.uint8)
+    t0 = time.perf_counter()
+    assert orc.orc_vae_decode(v, tl.fptr(lat), lh, lw, rgb.ctypes.data, None, -1) == 0
+    t1 = time.perf_counter() - t0
+    orc.orc_vae_free(v)
+    scale = vae_flops(c) / vae_flops(dict(c, lh=lh, lw=lw))
+    ms = t1 * scale * 1000
+    return {"value": round(1000.0 / ms, 6), "unit": "images/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(ms, 1),
+            "sample": f"oracle (C restatement of the reference iris_vae_decode, OpenMP): 256x256 decode "
+                      f"{t1:.2f} s, scaled x{scale:.2f} by algorithmic FLOPs to 1024x1024"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -371,7 +456,7 @@ def main():
         return
     c = CONFIGS[args.config]
     lib = tl.hip()
-    run = {"flux": run_flux, "zimage": run_zimage, "qwen3": run_qwen3}[c["kind"]]
+    run = {"flux": run_flux, "zimage": run_zimage, "qwen3": run_qwen3, "vae": run_vae}[c["kind"]]
     ms_step, wall_ms, flops, kernels, cfg, t_load = run(lib, c, args)
     images_per_s = 1000.0 / (ms_step * c["steps"])   # one image per pass (CFG: both branches in one)
     dom = max(kernels, key=lambda k: k["ms_per_step"])
@@ -404,7 +489,7 @@ def main():
         "device": lib.iris_hip_device_name().decode(),
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_qwen3(c) if c["kind"] == "qwen3" else cpu_baseline(c)
+        result["cpu_baseline"] = {"qwen3": cpu_baseline_qwen3, "vae": cpu_baseline_vae}.get(c["kind"], cpu_baseline)(c)
     print(json.dumps(result))
 
 

@@ -103,6 +103,14 @@ class AttnArgs(ctypes.Structure):
                 ("kv_group", ctypes.c_int)]
 
 
+class Conv3x3(ctypes.Structure):
+    """iris_conv3x3_t (include/iris_hip.h)"""
+    _fields_ = [("inp", ctypes.c_void_p), ("wt", ctypes.c_void_p), ("out", ctypes.c_void_p),
+                ("bias", ctypes.c_void_p), ("H", ctypes.c_int), ("W", ctypes.c_int), ("cin", ctypes.c_int),
+                ("cout", ctypes.c_int), ("up", ctypes.c_int), ("ldo", ctypes.c_int), ("epi", ctypes.c_int),
+                ("splits", ctypes.c_int), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
+
+
 class IrisImage(ctypes.Structure):
     """iris_image (reference iris.h:73-78, include/iris_vae.h)"""
     _fields_ = [("width", ctypes.c_int), ("height", ctypes.c_int), ("channels", ctypes.c_int),
@@ -203,6 +211,7 @@ def hip():
         lib.iris_vae_gpu_decode.argtypes = [vp, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_image_free.argtypes = [ctypes.POINTER(IrisImage)]
         lib.iris_vae_gpu_z_channels.argtypes = [vp]
+        lib.iris_hip_conv3x3.argtypes = [ctypes.POINTER(Conv3x3)]
         if lib.iris_hip_init(0) != 0:
             raise RuntimeError("iris_hip_init failed: " + lib.iris_hip_last_error().decode())
         _libs["hip"] = lib

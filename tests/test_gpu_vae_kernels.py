@@ -16,10 +16,7 @@ EPI_F32, EPI_BF16, EPI_ADD = 0, 1, 5
 vp = ctypes.c_void_p
 
 
-class Conv(ctypes.Structure):
-    _fields_ = [("inp", vp), ("wt", vp), ("out", vp), ("bias", vp), ("H", ctypes.c_int), ("W", ctypes.c_int),
-                ("cin", ctypes.c_int), ("cout", ctypes.c_int), ("up", ctypes.c_int), ("ldo", ctypes.c_int),
-                ("epi", ctypes.c_int), ("splits", ctypes.c_int), ("ws", vp), ("ws_bytes", ctypes.c_size_t)]
+Conv = tl.Conv3x3
 
 
 @pytest.fixture(scope="module")
@@ -36,7 +33,6 @@ def lib():
     lib.iris_hip_transpose_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
     lib.iris_hip_vae_conv_out.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
-    lib.iris_hip_conv3x3.argtypes = [ctypes.POINTER(Conv)]
     return lib
 
 
