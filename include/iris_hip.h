@@ -87,10 +87,14 @@ int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *
  * image by the loads themselves, no im2col buffer.
  *   out[y*W + x][n] = sum_{tap, c} in[(y+dy) >> up][(x+dx) >> up][c] * wt[n][tap][c]
  * with tap = 3 (dy + 1) + (dx + 1), then the epilogue (F32 / BF16 with bias,
- * or ADD: out f32 += conv + bias). in bf16 NHWC [(H >> up)][(W >> up)][cin],
+ * or ADD: out f32 += conv + bias). in bf16 NHWC [H'][W'][cin] (H' = H/2 for
+ * up 1, 2H for up 2, else H),
  * cin a power of two >= 64; wt bf16 [cout][9][cin]; out [H*W][ldo].
  * up = 1 reads the input through a nearest-neighbour 2x upsample
- * (iris_upsample_nearest followed by the conv, iris_vae.c:957-965).
+ * (iris_upsample_nearest followed by the conv, iris_vae.c:957-965); up = 2
+ * is the encoder's downsample: stride 2 over a (2H) x (2W) input zero-padded
+ * on the right and bottom only, out[y][x] = sum in[2y + ky][2x + kx]
+ * (vae_pad_right_bottom + the stride-2 conv, iris_vae.c:172-193, :407-418).
  * splits > 1 splits K over blocks into the f32 workspace ws (splits * H*W *
  * cout floats) and reduces in order (deterministic). */
 typedef struct {
@@ -107,13 +111,13 @@ int iris_hip_conv3x3(const iris_conv3x3_t *c);
 
 /* ---- VAE decoder kernels (vae.hip), channels-last (NHWC) activations ---- */
 /* GroupNorm (iris_group_norm, iris_kernels.c:542) in three launches:
- * per-block float64 channel sums of x (f32, or bf16 if is_bf16) over
- * `pixels` rows of C channels into part (>= nblk * C * 2 doubles; returns the
- * number of blocks used, < 0 on error), per-group finalize into
+ * per-block float64 group sums of x (f32, or bf16 if is_bf16) over
+ * `pixels` rows of C channels into part (>= nblk * groups * 2 doubles;
+ * returns the number of blocks used, < 0 on error), per-group finalize into
  * ab[2][C] = (gamma / std, beta - mean * gamma / std), and the apply pass
  * y = act(x * ab[0][c] + ab[1][c]) in bf16 with act = swish
  * (iris_vae.c:195) or identity; raw, if not NULL, receives x in bf16. */
-int iris_hip_gn_stats(const void *d_x, int is_bf16, int pixels, int C, double *d_part, int nblk);
+int iris_hip_gn_stats(const void *d_x, int is_bf16, int pixels, int C, int groups, double *d_part, int nblk);
 int iris_hip_gn_finalize(const double *d_part, int nblk, int pixels, int C, int groups, const float *d_gamma,
                          const float *d_beta, float eps, float *d_ab);
 int iris_hip_gn_apply(const void *d_x, int is_bf16, const float *d_ab, int pixels, int C, int swish, uint16_t *d_y,
@@ -123,6 +127,13 @@ int iris_hip_gn_apply(const void *d_x, int is_bf16, const float *d_ab, int pixel
  * NULL to skip), channels z..63 zero (iris_vae.c:860-897). z <= 32. */
 int iris_hip_vae_front(uint16_t *d_out, const float *d_latent, int z, int h, int w, const float *d_sc,
                        const float *d_sh, int divide, const float *d_pqw, const float *d_pqb);
+/* Encoder input: image [3][H][W] f32 -> bf16 [H][W][64] (channels 3..63 zero). */
+int iris_hip_vae_img_in(uint16_t *d_out, const float *d_img, int H, int W);
+/* Encoder output (iris_vae.c:440-482): moments [h][w][2z] f32 -> 1x1
+ * quant_conv (qw [2z][2z], NULL to skip) -> mean (first z) -> patchify 2x2
+ * -> (x - sh[c]) * sc[c] per latent channel -> latent [4z][h/2][w/2] f32. */
+int iris_hip_vae_enc_out(float *d_latent, const float *d_moments, int z, int h, int w, const float *d_qw,
+                         const float *d_qb, const float *d_sc, const float *d_sh);
 /* Row softmax, f32 scores [rows][ld_s] -> bf16 [rows][ld_p], columns
  * cols..cols_pad-1 zeroed (iris_softmax in attnblock_forward, iris_vae.c:335). */
 int iris_hip_softmax_bf16(uint16_t *d_p, int ld_p, int cols_pad, const float *d_s, int ld_s, int rows, int cols);

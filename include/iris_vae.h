@@ -1,8 +1,9 @@
 /*
- * iris_vae.h - the VAE decoder on the GPU: latent -> RGB image.
+ * iris_vae.h - the VAE on the GPU: latent -> RGB image, image -> latent.
  *
- * Replaces the reference's decoder path, iris_vae.c:835-998 (iris_vae_decode)
- * with the weights of iris_vae_load_safetensors_ex (iris_vae.c:1227-1386).
+ * Replaces the reference's decoder path, iris_vae.c:835-998 (iris_vae_decode),
+ * and encoder path, iris_vae.c:363-482 (iris_vae_encode), with the weights of
+ * iris_vae_load_safetensors_ex (iris_vae.c:1227-1386).
  * Architecture fixed as in the reference: base 128 channels, ch_mult
  * {1, 2, 4, 4}, 2 + 1 resblocks per up level, 32 groups, a single-head
  * attention block at the bottleneck, nearest 2x upsampling; z_channels 32
@@ -67,6 +68,16 @@ int iris_vae_gpu_decode_to(iris_vae_gpu_t *vae, const float *latent, int latent_
 int iris_vae_gpu_decode_device(iris_vae_gpu_t *vae, const float *d_latent, int latent_h, int latent_w,
                                uint8_t *d_rgb, float *d_f32);
 int iris_vae_gpu_z_channels(const iris_vae_gpu_t *vae);
+
+/* cf. iris_vae_encode (iris_vae.c:363-482): images [batch][3][H][W] f32 in
+ * [-1, 1] (host), H and W multiples of 16 up to IRIS_VAE_MAX_DIM; returns
+ * malloc'd latents [batch][4z][H/16][W/16] (mean of the posterior, patchified
+ * and normalized) and their size in out_h, out_w; NULL on error or when the
+ * file had no encoder tensors. */
+float *iris_vae_gpu_encode(iris_vae_gpu_t *vae, const float *img, int batch, int H, int W, int *out_h, int *out_w);
+/* Device-resident encode of one image: d_img [3][H][W] -> d_latent. */
+int iris_vae_gpu_encode_device(iris_vae_gpu_t *vae, const float *d_img, int H, int W, float *d_latent);
+int iris_vae_gpu_has_encoder(const iris_vae_gpu_t *vae);
 
 #ifdef __cplusplus
 }

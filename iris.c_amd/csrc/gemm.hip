@@ -77,8 +77,13 @@ constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <bool CONV>
+/* MODE 0: GEMM; 1: 3x3 convolution, stride 1, input optionally read through
+ * a nearest 2x upsample; 2: 3x3 convolution, stride 2, right/bottom padding.
+ * The modes are separate kernels: the load-issue phase has no cycles to
+ * spare for the address arithmetic of the modes it does not run. */
+template <int MODE>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
+    constexpr bool CONV = MODE != 0;
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
      * the other */
@@ -169,12 +174,17 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             const int soff = (kg & ((1 << P.conv_cpt_shift) - 1)) * (BK * 2);
             const int ty = tap / 3;
             const int dy = ty - 1, dx = tap - 3 * ty - 1;
-            const int up = P.conv_up, win = P.conv_w >> up;
+            /* MODE 1: input pixel ((y + dy) >> up, (x + dx) >> up); MODE 2 (stride 2,
+             * zero padding on the right and bottom only): input pixel
+             * (2y + dy + 1, 2x + dx + 1) of a (2 conv_h) x (2 conv_w) image */
+            const int up = MODE == 1 ? P.conv_up : 0;
+            const int hin = MODE == 2 ? 2 * P.conv_h : P.conv_h, win = MODE == 2 ? 2 * P.conv_w : P.conv_w;
+            constexpr int mul = MODE == 2 ? 2 : 1, off = MODE == 2 ? 1 : 0;
 #pragma unroll
             for (int i = 0; i < DMA_PER_WAVE; i++) {
-                const int yy = (int)(pix[i] >> 16) + dy, xx = (int)(pix[i] & 0xffffu) + dx;
-                const bool ok = (unsigned)yy < (unsigned)P.conv_h && (unsigned)xx < (unsigned)P.conv_w;
-                const int src = ((((yy >> up) * win) + (xx >> up)) << P.conv_cin_bshift) + a_chunk[i & 1];
+                const int yy = (int)(pix[i] >> 16) * mul + dy + off, xx = (int)(pix[i] & 0xffffu) * mul + dx + off;
+                const bool ok = (unsigned)yy < (unsigned)hin && (unsigned)xx < (unsigned)win;
+                const int src = ((((yy >> up) * (win >> up)) + (xx >> up)) << P.conv_cin_bshift) + a_chunk[i & 1];
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
                                                          ok ? src : (int)0x80000000u, soff, 0, 0);
             }
@@ -493,7 +503,7 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
 }
 
@@ -521,7 +531,7 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     P.kchunk = kchunk;
     P.ws = ws;
     P.ws_stride = stride;
-    hipLaunchKernelGGL(gemm_bf16_kernel<false>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel")) return -1;
     const size_t n_out = (size_t)p->M * (p->epi == IRIS_EPI_SWIGLU ? p->N / 2 : p->N);
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
@@ -533,12 +543,14 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     if (!c || !c->in || !c->wt || !c->out) return iris_set_error("conv3x3: null operand");
     if (c->cin < 64 || c->cin > 8192 || (c->cin & (c->cin - 1)))
         return iris_set_error("conv3x3: cin=%d must be a power of two in 64..8192", c->cin);
-    if (c->up != 0 && c->up != 1) return iris_set_error("conv3x3: up=%d (0 or 1)", c->up);
-    if (c->H <= 0 || c->W <= 0 || c->H > 16000 || c->W > 16000 || (c->up && ((c->H | c->W) & 1)))
+    if (c->up < 0 || c->up > 2) return iris_set_error("conv3x3: up=%d (0, 1 or 2)", c->up);
+    if (c->H <= 0 || c->W <= 0 || c->H > 8000 || c->W > 8000 || (c->up == 1 && ((c->H | c->W) & 1)))
         return iris_set_error("conv3x3: output %dx%d", c->H, c->W);
     if (c->epi != IRIS_EPI_F32 && c->epi != IRIS_EPI_BF16 && c->epi != IRIS_EPI_ADD)
         return iris_set_error("conv3x3: epilogue %d (F32, BF16 or ADD)", c->epi);
-    const size_t in_bytes = (size_t)(c->H >> c->up) * (size_t)(c->W >> c->up) * (size_t)c->cin * 2;
+    const size_t in_pix = c->up == 1 ? (size_t)(c->H / 2) * (c->W / 2)
+                          : c->up == 2 ? (size_t)(2 * c->H) * (2 * c->W) : (size_t)c->H * c->W;
+    const size_t in_bytes = in_pix * (size_t)c->cin * 2;
     if (in_bytes >= (1ull << 31)) return iris_set_error("conv3x3: input of %zu bytes (< 2 GiB)", in_bytes);
     if ((long long)c->H * c->W >= (1LL << 31)) return iris_set_error("conv3x3: too many pixels");
     iris_gemm_problem_t p;
@@ -585,7 +597,10 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
         P.ws = c->ws;
         P.ws_stride = stride;
     }
-    hipLaunchKernelGGL(gemm_bf16_kernel<true>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    if (c->up == 2)
+        hipLaunchKernelGGL(gemm_bf16_kernel<2>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    else
+        hipLaunchKernelGGL(gemm_bf16_kernel<1>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel<conv>")) return -1;
     if (chunks == 1) return 0;
     const size_t n_out = (size_t)p.M * p.N;

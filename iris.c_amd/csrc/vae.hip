@@ -46,18 +46,21 @@ __device__ __forceinline__ uint4 pack8(const float v[8]) {
     return o;
 }
 
-/* Per-block channel sums of x and x^2 over pixels [b*ppb, (b+1)*ppb):
- * part[(b * C + c) * 2 + {0, 1}], float64. Thread t reads channel chunk
+/* Per-block group sums of x and x^2 over pixels [b*ppb, (b+1)*ppb):
+ * part[(b * G + g) * 2 + {0, 1}], float64. Thread t reads channel chunk
  * t % (C/8) of every (256 / (C/8))-th pixel; the block then sums the threads
- * of each chunk in a fixed order, so the result does not depend on timing. */
+ * of each chunk, then the channels of each group, in a fixed order, so the
+ * result does not depend on timing. */
 template <typename T>
-__global__ __launch_bounds__(NT) void gn_stats_kernel(const T *x, int pixels, int C, int ppb, double *part) {
+__global__ __launch_bounds__(NT) void gn_stats_kernel(const T *x, int pixels, int C, int G, int ppb, double *part) {
     __shared__ double ls[NT][8], lq[NT][8];
+    __shared__ double cs[512], cq[512];
     const int cpr = C >> 3, tid = threadIdx.x, ci = tid % cpr, rows = NT / cpr;
     const int p0 = blockIdx.x * ppb, p1 = min(pixels, p0 + ppb);
     double s[8], q[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) s[j] = q[j] = 0.0;
+#pragma unroll 4
     for (int p = p0 + tid / cpr; p < p1; p += rows) {
         float v[8];
         load8(x + (size_t)p * C + ci * 8, v);
@@ -79,13 +82,24 @@ __global__ __launch_bounds__(NT) void gn_stats_kernel(const T *x, int pixels, in
             a += ls[r * cpr + (c >> 3)][c & 7];
             b += lq[r * cpr + (c >> 3)][c & 7];
         }
-        part[((size_t)blockIdx.x * C + c) * 2] = a;
-        part[((size_t)blockIdx.x * C + c) * 2 + 1] = b;
+        cs[c] = a;
+        cq[c] = b;
+    }
+    __syncthreads();
+    const int cpg = C / G;
+    for (int g = tid; g < G; g += NT) {
+        double a = 0.0, b = 0.0;
+        for (int c = g * cpg; c < (g + 1) * cpg; c++) {
+            a += cs[c];
+            b += cq[c];
+        }
+        part[((size_t)blockIdx.x * G + g) * 2] = a;
+        part[((size_t)blockIdx.x * G + g) * 2 + 1] = b;
     }
 }
 
-/* One block per group: mean and variance of the group from the partial sums
- * (float64, fixed order), then per channel y = x * a + b with
+/* One block per group: mean and variance of the group from the per-block
+ * partial sums (float64, fixed order), then per channel y = x * a + b with
  * a = gamma / sqrt(var + eps), b = beta - mean * a; ab[c] = a, ab[C + c] = b. */
 __global__ __launch_bounds__(NT) void gn_finalize_kernel(const double *part, int nblk, int C, int G,
                                                          const float *gamma, const float *beta, float eps,
@@ -93,10 +107,9 @@ __global__ __launch_bounds__(NT) void gn_finalize_kernel(const double *part, int
     __shared__ double rs[NT], rq[NT];
     const int g = blockIdx.x, cpg = C / G, tid = threadIdx.x;
     double s = 0.0, q = 0.0;
-    for (int e = tid; e < nblk * cpg; e += NT) {
-        const size_t o = ((size_t)(e / cpg) * C + g * cpg + e % cpg) * 2;
-        s += part[o];
-        q += part[o + 1];
+    for (int e = tid; e < nblk; e += NT) {
+        s += part[((size_t)e * G + g) * 2];
+        q += part[((size_t)e * G + g) * 2 + 1];
     }
     rs[tid] = s;
     rq[tid] = q;
@@ -180,6 +193,49 @@ __global__ __launch_bounds__(NT) void vae_front_kernel(const float *lat, int z, 
     uint4 *dst = (uint4 *)(out + (size_t)p * 64);
 #pragma unroll
     for (int k = 0; k < 8; k++) dst[k] = pack8(o + 8 * k);
+}
+
+/* Encoder input: image [3][H][W] f32 (NCHW) -> bf16 [H][W][64], channels
+ * 3..63 zero (conv_in's weights are padded to match). */
+__global__ __launch_bounds__(NT) void vae_img_in_kernel(const float *img, int npix, uint16_t *out) {
+    const int p = blockIdx.x * NT + threadIdx.x;
+    if (p >= npix) return;
+    float o[64];
+#pragma unroll
+    for (int j = 0; j < 64; j++) o[j] = 0.0f;
+    o[0] = img[p];
+    o[1] = img[(size_t)npix + p];
+    o[2] = img[2 * (size_t)npix + p];
+    uint4 *dst = (uint4 *)(out + (size_t)p * 64);
+#pragma unroll
+    for (int k = 0; k < 8; k++) dst[k] = pack8(o + 8 * k);
+}
+
+/* Encoder output (iris_vae.c:440-482): moments [h][w][2z] f32 (NHWC) ->
+ * optional 1x1 quant_conv (qw [2z][2z]) -> the mean (first z channels) ->
+ * patchify 2x2 (channel c at (y, x) becomes channel c * 4 + 2 (y & 1) + (x & 1)
+ * at (y / 2, x / 2)) -> per latent channel (x - sh) * sc (Z-Image: scaling,
+ * shift; Flux: 1 / sqrt(var + eps), mean) -> latent [4z][h/2][w/2] f32. */
+__global__ __launch_bounds__(NT) void vae_enc_out_kernel(const float *mom, int z, int h, int w, const float *qw,
+                                                         const float *qb, const float *sc, const float *sh,
+                                                         float *lat) {
+    const int p = blockIdx.x * NT + threadIdx.x;
+    if (p >= h * w) return;
+    const int y = p / w, x = p % w, z2 = 2 * z;
+    const float *m = mom + (size_t)p * z2;
+    const int lh = h / 2, lw = w / 2;
+    if ((y >> 1) >= lh || (x >> 1) >= lw) return;
+    for (int c = 0; c < z; c++) {
+        float v;
+        if (qw) {
+            v = qb ? qb[c] : 0.0f;
+            for (int k = 0; k < z2; k++) v += qw[c * z2 + k] * m[k];
+        } else {
+            v = m[c];
+        }
+        const int lc = c * 4 + (y & 1) * 2 + (x & 1);
+        lat[((size_t)lc * lh + (y >> 1)) * lw + (x >> 1)] = (v - sh[lc]) * sc[lc];
+    }
 }
 
 /* Row softmax from f32 scores to bf16 probabilities, one block per row:
@@ -294,18 +350,19 @@ unsigned blocks_for(size_t n) {
 
 }  // namespace
 
-extern "C" int iris_hip_gn_stats(const void *x, int is_bf16, int pixels, int C, double *part, int nblk) {
+extern "C" int iris_hip_gn_stats(const void *x, int is_bf16, int pixels, int C, int groups, double *part, int nblk) {
     if (!x || !part || pixels <= 0 || nblk <= 0) return iris_set_error("gn_stats: bad arguments");
-    if (C < 64 || C > 2048 || (C & (C - 1))) return iris_set_error("gn_stats: C=%d (a power of two in 64..2048)", C);
+    if (C < 64 || C > 512 || (C & (C - 1))) return iris_set_error("gn_stats: C=%d (a power of two in 64..512)", C);
+    if (groups <= 0 || C % groups) return iris_set_error("gn_stats: %d groups of %d channels", groups, C);
     if ((uintptr_t)x & 15) return iris_set_error("gn_stats: x must be 16-byte aligned");
     const int ppb = (pixels + nblk - 1) / nblk;
     const int used = (pixels + ppb - 1) / ppb;
     if (is_bf16)
         hipLaunchKernelGGL(gn_stats_kernel<uint16_t>, dim3(used), dim3(NT), 0, iris_stream(), (const uint16_t *)x,
-                           pixels, C, ppb, part);
+                           pixels, C, groups, ppb, part);
     else
         hipLaunchKernelGGL(gn_stats_kernel<float>, dim3(used), dim3(NT), 0, iris_stream(), (const float *)x, pixels,
-                           C, ppb, part);
+                           C, groups, ppb, part);
     if (iris_launch_check("gn_stats_kernel")) return -1;
     return used;
 }
@@ -374,4 +431,19 @@ extern "C" int iris_hip_vae_conv_out(uint8_t *rgb, float *f32, const uint16_t *g
     hipLaunchKernelGGL(conv_out_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 9 * cin * sizeof(float4), iris_stream(),
                        g, H, W, cin, wt, bias, rgb, f32);
     return iris_launch_check("conv_out_kernel");
+}
+
+extern "C" int iris_hip_vae_img_in(uint16_t *out, const float *img, int H, int W) {
+    if (!out || !img || H <= 0 || W <= 0 || ((uintptr_t)out & 15)) return iris_set_error("vae_img_in: bad arguments");
+    const int npix = H * W;
+    hipLaunchKernelGGL(vae_img_in_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 0, iris_stream(), img, npix, out);
+    return iris_launch_check("vae_img_in_kernel");
+}
+
+extern "C" int iris_hip_vae_enc_out(float *lat, const float *mom, int z, int h, int w, const float *qw,
+                                    const float *qb, const float *sc, const float *sh) {
+    if (!lat || !mom || !sc || !sh || z <= 0 || h < 2 || w < 2) return iris_set_error("vae_enc_out: bad arguments");
+    hipLaunchKernelGGL(vae_enc_out_kernel, dim3((h * w + NT - 1) / NT), dim3(NT), 0, iris_stream(), mom, z, h, w, qw,
+                       qb, sc, sh, lat);
+    return iris_launch_check("vae_enc_out_kernel");
 }

@@ -40,25 +40,37 @@ typedef struct {
     int cin, cout;
 } vres_t;
 
+typedef struct {
+    float *g, *b;              /* group_norm */
+    uint16_t *qkv_w, *o_w;     /* [1536][512] (q rows scaled by 1/sqrt(512)), [512][512] */
+    float *qkv_b, *o_b;
+} vattn_t;
+
 struct iris_vae_gpu {
-    int z, lat_ch, divide;
+    int z, lat_ch, divide, has_enc;
     float eps;
     float *lsc, *lsh;          /* per latent channel: x * lsc + lsh (or x / lsc + lsh) */
     float *pqw, *pqb;          /* post_quant_conv [z][z], or NULL */
     uint16_t *cin_w;           /* [512][9][64] */
     float *cin_b;
     vres_t mid1, mid2, up[12];
-    float *an_g, *an_b;
-    uint16_t *qkv_w, *o_w;     /* [1536][512] (q rows scaled by 1/sqrt(512)), [512][512] */
-    float *qkv_b, *o_b;
+    vattn_t attn;
     uint16_t *ups_w[3];
     float *ups_b[3];
     float *no_g, *no_b, *co_w, *co_b;   /* conv_out f32 [9][128][4], bias [4] */
+    /* encoder (iris_vae_encode, iris_vae.c:363-482) */
+    uint16_t *e_cin_w, *e_ds_w[3], *e_co_w;   /* [128][9][64], [C][9][C], [2z][9][512] */
+    float *e_cin_b, *e_ds_b[3], *e_co_b;
+    vres_t e_down[8], e_mid1, e_mid2;
+    vattn_t e_attn;
+    float *e_no_g, *e_no_b, *qw, *qb;         /* quant_conv [2z][2z] (Flux) */
+    float *esc, *esh;                          /* latent normalization: (x - esh) * esc */
     /* work buffers, sized for cap_pix output pixels */
     size_t cap_pix;
     float *x, *y, *sc, *ws, *ab, *dlat, *df32;
     uint16_t *t, *h, *raw, *qkv, *vt, *att, *pm, *front;
     uint8_t *drgb;
+    float *dimg;
     double *part;
     size_t ws_bytes;
 };
@@ -173,13 +185,86 @@ static void free_res(vres_t *r) {
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
 }
 
+/* load_attnblock_sf (iris_vae.c:1184-1225): q, k, v stacked; q (weights and
+ * bias) scaled by 1/sqrt(C) as the reference scales q before Q K^T
+ * (iris_vae.c:318) */
+static int load_attn(vsrc_t *s, vattn_t *a, const char *pre) {
+    char n[256];
+    const float qs = 1.0f / sqrtf((float)VAE_MID);
+    snprintf(n, sizeof(n), "%s.group_norm.weight", pre);
+    if (!(a->g = up_vec(s, n, VAE_MID))) return -1;
+    snprintf(n, sizeof(n), "%s.group_norm.bias", pre);
+    if (!(a->b = up_vec(s, n, VAE_MID))) return -1;
+    a->qkv_w = (uint16_t *)iris_hip_malloc((size_t)3 * VAE_MID * VAE_MID * 2);
+    a->o_w = (uint16_t *)iris_hip_malloc((size_t)VAE_MID * VAE_MID * 2);
+    if (!a->qkv_w || !a->o_w) return -1;
+    const char *proj[3] = {"to_q", "to_k", "to_v"};
+    float bias[3 * VAE_MID];
+    for (int i = 0; i < 3; i++) {
+        snprintf(n, sizeof(n), "%s.%s.weight", pre, proj[i]);
+        if (up_mat_into(s, n, VAE_MID, VAE_MID, i == 0 ? qs : 1.0f, a->qkv_w + (size_t)i * VAE_MID * VAE_MID))
+            return -1;
+        snprintf(n, sizeof(n), "%s.%s.bias", pre, proj[i]);
+        float *b = vsrc_read(s, n, VAE_MID, 0);
+        if (!b) return -1;
+        for (int j = 0; j < VAE_MID; j++) bias[i * VAE_MID + j] = b[j] * (i == 0 ? qs : 1.0f);
+        free(b);
+    }
+    if (!(a->qkv_b = (float *)upload(bias, sizeof(bias)))) return -1;
+    snprintf(n, sizeof(n), "%s.to_out.0.weight", pre);
+    if (up_mat_into(s, n, VAE_MID, VAE_MID, 1.0f, a->o_w)) return -1;
+    snprintf(n, sizeof(n), "%s.to_out.0.bias", pre);
+    return (a->o_b = up_vec(s, n, VAE_MID)) ? 0 : -1;
+}
+
+static void free_attn(vattn_t *a) {
+    void *p[] = {a->g, a->b, a->qkv_w, a->o_w, a->qkv_b, a->o_b};
+    for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
+}
+
+/* encoder half of iris_vae_load_safetensors_ex (iris_vae.c:1260-1310) */
+static int load_encoder(vsrc_t *s, iris_vae_gpu_t *v) {
+    char n[256];
+    const int z2 = 2 * v->z;
+    if (!(v->e_cin_w = up_conv3(s, "encoder.conv_in.weight", VAE_BASE, 3, VAE_CIN_PAD)) ||
+        !(v->e_cin_b = up_vec(s, "encoder.conv_in.bias", VAE_BASE)))
+        return -1;
+    for (int level = 0, bi = 0; level < 4; level++) {
+        const int ch = VAE_BASE * ch_mult[level], prev = level ? VAE_BASE * ch_mult[level - 1] : VAE_BASE;
+        for (int r = 0; r < 2; r++, bi++) {
+            snprintf(n, sizeof(n), "encoder.down_blocks.%d.resnets.%d", level, r);
+            if (load_res(s, &v->e_down[bi], n, r == 0 && level > 0 ? prev : ch, ch)) return -1;
+        }
+        if (level < 3) {
+            snprintf(n, sizeof(n), "encoder.down_blocks.%d.downsamplers.0.conv.weight", level);
+            if (!(v->e_ds_w[level] = up_conv3(s, n, ch, ch, ch))) return -1;
+            snprintf(n, sizeof(n), "encoder.down_blocks.%d.downsamplers.0.conv.bias", level);
+            if (!(v->e_ds_b[level] = up_vec(s, n, ch))) return -1;
+        }
+    }
+    if (load_res(s, &v->e_mid1, "encoder.mid_block.resnets.0", VAE_MID, VAE_MID) ||
+        load_attn(s, &v->e_attn, "encoder.mid_block.attentions.0") ||
+        load_res(s, &v->e_mid2, "encoder.mid_block.resnets.1", VAE_MID, VAE_MID) ||
+        !(v->e_no_g = up_vec(s, "encoder.conv_norm_out.weight", VAE_MID)) ||
+        !(v->e_no_b = up_vec(s, "encoder.conv_norm_out.bias", VAE_MID)) ||
+        !(v->e_co_w = up_conv3(s, "encoder.conv_out.weight", z2, VAE_MID, VAE_MID)) ||
+        !(v->e_co_b = up_vec(s, "encoder.conv_out.bias", z2)))
+        return -1;
+    if (vsrc_has(s, "quant_conv.weight") &&
+        (!(v->qw = up_vec(s, "quant_conv.weight", (size_t)z2 * z2)) || !(v->qb = up_vec(s, "quant_conv.bias", z2))))
+        return -1;
+    v->has_enc = 1;
+    return 0;
+}
+
 static void free_work(iris_vae_gpu_t *v) {
     void *p[] = {v->x, v->y, v->sc, v->ws, v->ab, v->dlat, v->df32, v->t, v->h, v->raw, v->qkv, v->vt,
-                 v->att, v->pm, v->front, v->drgb, v->part};
+                 v->att, v->pm, v->front, v->drgb, v->part, v->dimg};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     v->x = v->y = v->sc = v->ws = v->ab = v->dlat = v->df32 = NULL;
     v->t = v->h = v->raw = v->qkv = v->vt = v->att = v->pm = v->front = NULL;
     v->drgb = NULL;
+    v->dimg = NULL;
     v->part = NULL;
     v->cap_pix = 0;
 }
@@ -190,9 +275,15 @@ void iris_vae_gpu_free(iris_vae_gpu_t *v) {
     free_res(&v->mid1);
     free_res(&v->mid2);
     for (int i = 0; i < 12; i++) free_res(&v->up[i]);
-    void *p[] = {v->lsc, v->lsh, v->pqw, v->pqb, v->cin_w, v->cin_b, v->an_g, v->an_b, v->qkv_w, v->o_w,
-                 v->qkv_b, v->o_b, v->no_g, v->no_b, v->co_w, v->co_b, v->ups_w[0], v->ups_w[1], v->ups_w[2],
-                 v->ups_b[0], v->ups_b[1], v->ups_b[2]};
+    for (int i = 0; i < 8; i++) free_res(&v->e_down[i]);
+    free_res(&v->e_mid1);
+    free_res(&v->e_mid2);
+    free_attn(&v->attn);
+    free_attn(&v->e_attn);
+    void *p[] = {v->lsc, v->lsh, v->pqw, v->pqb, v->cin_w, v->cin_b, v->no_g, v->no_b, v->co_w, v->co_b,
+                 v->ups_w[0], v->ups_w[1], v->ups_w[2], v->ups_b[0], v->ups_b[1], v->ups_b[2], v->e_cin_w,
+                 v->e_cin_b, v->e_ds_w[0], v->e_ds_w[1], v->e_ds_w[2], v->e_ds_b[0], v->e_ds_b[1], v->e_ds_b[2],
+                 v->e_co_w, v->e_co_b, v->e_no_g, v->e_no_b, v->qw, v->qb, v->esc, v->esh};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     free(v);
 }
@@ -242,6 +333,17 @@ static iris_vae_gpu_t *load(vsrc_t *s, int z, float scaling, float shift) {
     }
     if (!(v->lsc = (float *)upload(sc, lc * sizeof(float))) || !(v->lsh = (float *)upload(sh, lc * sizeof(float))))
         goto bad;
+    /* the encoder's inverse: (x - shift) * scaling, or (x - mean) / sqrt(var + eps)
+     * (iris_batch_norm, iris_kernels.c:584-604) */
+    {
+        float esc[128], esh[128];
+        for (int c = 0; c < lc; c++) {
+            esc[c] = v->divide ? scaling : 1.0f / sc[c];
+            esh[c] = sh[c];
+        }
+        if (!(v->esc = (float *)upload(esc, lc * sizeof(float))) || !(v->esh = (float *)upload(esh, lc * sizeof(float))))
+            goto bad;
+    }
     if (vsrc_has(s, "post_quant_conv.weight")) {
         if (!(v->pqw = up_vec(s, "post_quant_conv.weight", (size_t)z * z)) ||
             !(v->pqb = up_vec(s, "post_quant_conv.bias", z)))
@@ -253,36 +355,7 @@ static iris_vae_gpu_t *load(vsrc_t *s, int z, float scaling, float shift) {
     if (load_res(s, &v->mid1, "decoder.mid_block.resnets.0", VAE_MID, VAE_MID) ||
         load_res(s, &v->mid2, "decoder.mid_block.resnets.1", VAE_MID, VAE_MID))
         goto bad;
-    /* attention: q, k, v stacked; q (weights and bias) scaled by 1/sqrt(C) as
-     * the reference scales q before Q K^T (iris_vae.c:318) */
-    {
-        const char *pre = "decoder.mid_block.attentions.0";
-        const float qs = 1.0f / sqrtf((float)VAE_MID);
-        snprintf(n, sizeof(n), "%s.group_norm.weight", pre);
-        if (!(v->an_g = up_vec(s, n, VAE_MID))) goto bad;
-        snprintf(n, sizeof(n), "%s.group_norm.bias", pre);
-        if (!(v->an_b = up_vec(s, n, VAE_MID))) goto bad;
-        v->qkv_w = (uint16_t *)iris_hip_malloc((size_t)3 * VAE_MID * VAE_MID * 2);
-        v->o_w = (uint16_t *)iris_hip_malloc((size_t)VAE_MID * VAE_MID * 2);
-        if (!v->qkv_w || !v->o_w) goto bad;
-        const char *proj[3] = {"to_q", "to_k", "to_v"};
-        float bias[3 * VAE_MID];
-        for (int i = 0; i < 3; i++) {
-            snprintf(n, sizeof(n), "%s.%s.weight", pre, proj[i]);
-            if (up_mat_into(s, n, VAE_MID, VAE_MID, i == 0 ? qs : 1.0f, v->qkv_w + (size_t)i * VAE_MID * VAE_MID))
-                goto bad;
-            snprintf(n, sizeof(n), "%s.%s.bias", pre, proj[i]);
-            float *b = vsrc_read(s, n, VAE_MID, 0);
-            if (!b) goto bad;
-            for (int j = 0; j < VAE_MID; j++) bias[i * VAE_MID + j] = b[j] * (i == 0 ? qs : 1.0f);
-            free(b);
-        }
-        if (!(v->qkv_b = (float *)upload(bias, sizeof(bias)))) goto bad;
-        snprintf(n, sizeof(n), "%s.to_out.0.weight", pre);
-        if (up_mat_into(s, n, VAE_MID, VAE_MID, 1.0f, v->o_w)) goto bad;
-        snprintf(n, sizeof(n), "%s.to_out.0.bias", pre);
-        if (!(v->o_b = up_vec(s, n, VAE_MID))) goto bad;
-    }
+    if (load_attn(s, &v->attn, "decoder.mid_block.attentions.0")) goto bad;
     /* up blocks: up_blocks.i is level 3 - i */
     for (int i = 0, bi = 0; i < 4; i++) {
         const int level = 3 - i, ch = VAE_BASE * ch_mult[level];
@@ -321,6 +394,7 @@ static iris_vae_gpu_t *load(vsrc_t *s, int z, float scaling, float shift) {
         free(wt);
         if (!ok || !v->co_w || !v->co_b) goto bad;
     }
+    if (vsrc_has(s, "encoder.conv_in.weight") && load_encoder(s, v)) goto bad;
     return v;
 bad:
     fail("load");
@@ -402,7 +476,7 @@ static int ensure_work(iris_vae_gpu_t *v, int lh, int lw) {
     ALLOC(v->t, P * 256 * 2);
     ALLOC(v->h, P * 256 * 2);
     ALLOC(v->raw, P * 256 * 2);
-    ALLOC(v->part, (size_t)GN_BLOCKS * 512 * 2 * sizeof(double));
+    ALLOC(v->part, (size_t)GN_BLOCKS * VAE_GROUPS * 2 * sizeof(double));
     ALLOC(v->ab, 2 * 512 * sizeof(float));
     ALLOC(v->qkv, S * 3 * VAE_MID * 2);
     ALLOC(v->att, S * VAE_MID * 2);
@@ -415,6 +489,7 @@ static int ensure_work(iris_vae_gpu_t *v, int lh, int lw) {
     ALLOC(v->dlat, (size_t)v->lat_ch * lh * lw * sizeof(float));
     ALLOC(v->drgb, P * 3);
     ALLOC(v->df32, P * 3 * sizeof(float));
+    ALLOC(v->dimg, P * 3 * sizeof(float));
     v->cap_pix = P;
     return 0;
 oom:
@@ -424,7 +499,7 @@ oom:
 
 static int gn(iris_vae_gpu_t *v, const void *x, int is_bf16, int pix, int C, const float *g, const float *b,
               int swish, uint16_t *y, uint16_t *raw) {
-    const int nblk = iris_hip_gn_stats(x, is_bf16, pix, C, v->part, GN_BLOCKS);
+    const int nblk = iris_hip_gn_stats(x, is_bf16, pix, C, VAE_GROUPS, v->part, GN_BLOCKS);
     if (nblk < 0 || iris_hip_gn_finalize(v->part, nblk, pix, C, VAE_GROUPS, g, b, v->eps, v->ab)) return -1;
     return iris_hip_gn_apply(x, is_bf16, v->ab, pix, C, swish, y, raw);
 }
@@ -488,10 +563,10 @@ static int resblock(iris_vae_gpu_t *v, const vres_t *r, int H, int W) {
 
 /* attnblock_forward (iris_vae.c:260-357): single head over the S pixels,
  * x += out_proj(softmax(q k^T / sqrt(C)) v); scores in f32, in row chunks */
-static int attention(iris_vae_gpu_t *v, int H, int W) {
+static int attention(iris_vae_gpu_t *v, const vattn_t *a, int H, int W) {
     const int S = H * W, C = VAE_MID, Kp = (S + 63) / 64 * 64, R = score_rows(S, Kp);
-    if (gn(v, v->x, 0, S, C, v->an_g, v->an_b, 0, v->t, NULL) ||
-        gemm(v->t, C, v->qkv_w, C, v->qkv, 3 * C, v->qkv_b, S, 3 * C, C, IRIS_EPI_BF16) ||
+    if (gn(v, v->x, 0, S, C, a->g, a->b, 0, v->t, NULL) ||
+        gemm(v->t, C, a->qkv_w, C, v->qkv, 3 * C, a->qkv_b, S, 3 * C, C, IRIS_EPI_BF16) ||
         iris_hip_transpose_bf16(v->vt, Kp, Kp, v->qkv + 2 * C, 3 * C, S, C))
         return -1;
     for (int q0 = 0; q0 < S; q0 += R) {
@@ -501,7 +576,7 @@ static int attention(iris_vae_gpu_t *v, int H, int W) {
             gemm(v->pm, Kp, v->vt, Kp, v->att + (size_t)q0 * C, C, NULL, r, C, Kp, IRIS_EPI_BF16))
             return -1;
     }
-    return gemm(v->att, C, v->o_w, C, v->x, C, v->o_b, S, C, C, IRIS_EPI_ADD);
+    return gemm(v->att, C, a->o_w, C, v->x, C, a->o_b, S, C, C, IRIS_EPI_ADD);
 }
 
 int iris_vae_gpu_decode_device(iris_vae_gpu_t *v, const float *d_lat, int lh, int lw, uint8_t *d_rgb, float *d_f32) {
@@ -513,7 +588,7 @@ int iris_vae_gpu_decode_device(iris_vae_gpu_t *v, const float *d_lat, int lh, in
     int H = 2 * lh, W = 2 * lw;
     if (iris_hip_vae_front(v->front, d_lat, v->z, lh, lw, v->lsc, v->lsh, v->divide, v->pqw, v->pqb) ||
         conv(v, v->front, v->cin_w, v->cin_b, v->x, H, W, VAE_CIN_PAD, VAE_MID, 0, IRIS_EPI_F32) ||
-        resblock(v, &v->mid1, H, W) || attention(v, H, W) || resblock(v, &v->mid2, H, W))
+        resblock(v, &v->mid1, H, W) || attention(v, &v->attn, H, W) || resblock(v, &v->mid2, H, W))
         return fail("decode (mid block)");
     for (int level = 3, bi = 0; level >= 0; level--) {
         const int ch = VAE_BASE * ch_mult[level];
@@ -571,3 +646,65 @@ void iris_image_free(iris_image *img) {
     free(img->data);
     free(img);
 }
+
+/* ------------------------------------------------------------------ encode */
+
+/* iris_vae_encode (iris_vae.c:363-482) for one image [3][H][W] (device),
+ * H and W multiples of 16: latent [4z][H/16][W/16] (device) */
+int iris_vae_gpu_encode_device(iris_vae_gpu_t *v, const float *d_img, int H, int W, float *d_lat) {
+    if (!v || !d_img || !d_lat || !v->has_enc) {
+        fprintf(stderr, "vae: encode needs the encoder weights\n");
+        return -1;
+    }
+    if (H < 16 || W < 16 || H % 16 || W % 16 || H > IRIS_VAE_MAX_DIM || W > IRIS_VAE_MAX_DIM) {
+        fprintf(stderr, "vae: image %dx%d (multiples of 16 up to %d)\n", H, W, IRIS_VAE_MAX_DIM);
+        return -1;
+    }
+    if (ensure_work(v, H / 16, W / 16)) return -1;
+    if (iris_hip_vae_img_in(v->raw, d_img, H, W) ||
+        conv(v, v->raw, v->e_cin_w, v->e_cin_b, v->x, H, W, VAE_CIN_PAD, VAE_BASE, 0, IRIS_EPI_F32))
+        return fail("encode (conv_in)");
+    int h = H, w = W;
+    for (int level = 0, bi = 0; level < 4; level++) {
+        const int ch = VAE_BASE * ch_mult[level];
+        for (int r = 0; r < 2; r++)
+            if (resblock(v, &v->e_down[bi++], h, w)) return fail("encode (resblock)");
+        if (level < 3) {
+            /* pad right/bottom + 3x3 stride 2, in the conv's loads */
+            if (iris_hip_f32_to_bf16(v->raw, v->x, (size_t)h * w * ch) ||
+                conv(v, v->raw, v->e_ds_w[level], v->e_ds_b[level], v->y, h / 2, w / 2, ch, ch, 2, IRIS_EPI_F32))
+                return fail("encode (downsample)");
+            swap(&v->x, &v->y);
+            h /= 2;
+            w /= 2;
+        }
+    }
+    if (resblock(v, &v->e_mid1, h, w) || attention(v, &v->e_attn, h, w) || resblock(v, &v->e_mid2, h, w) ||
+        gn(v, v->x, 0, h * w, VAE_MID, v->e_no_g, v->e_no_b, 1, v->t, NULL) ||
+        conv(v, v->t, v->e_co_w, v->e_co_b, v->y, h, w, VAE_MID, 2 * v->z, 0, IRIS_EPI_F32) ||
+        iris_hip_vae_enc_out(d_lat, v->y, v->z, h, w, v->qw, v->qb, v->esc, v->esh))
+        return fail("encode (output)");
+    return 0;
+}
+
+float *iris_vae_gpu_encode(iris_vae_gpu_t *v, const float *img, int batch, int H, int W, int *out_h, int *out_w) {
+    if (!v || !img || batch < 1 || H < 16 || W < 16 || H % 16 || W % 16 || H > IRIS_VAE_MAX_DIM ||
+        W > IRIS_VAE_MAX_DIM || ensure_work(v, H / 16, W / 16))
+        return NULL;
+    const size_t per_img = (size_t)3 * H * W, per_lat = (size_t)v->lat_ch * (H / 16) * (W / 16);
+    float *lat = (float *)malloc(batch * per_lat * sizeof(float));
+    if (!lat) return NULL;
+    for (int b = 0; b < batch; b++) {
+        if (iris_hip_memcpy_h2d(v->dimg, img + b * per_img, per_img * sizeof(float)) ||
+            iris_vae_gpu_encode_device(v, v->dimg, H, W, v->dlat) ||
+            iris_hip_memcpy_d2h(lat + b * per_lat, v->dlat, per_lat * sizeof(float))) {
+            free(lat);
+            return NULL;
+        }
+    }
+    if (out_h) *out_h = H / 16;
+    if (out_w) *out_w = W / 16;
+    return lat;
+}
+
+int iris_vae_gpu_has_encoder(const iris_vae_gpu_t *v) { return v ? v->has_enc : 0; }

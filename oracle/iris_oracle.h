@@ -136,5 +136,7 @@ orc_vae_t *orc_vae_load(const char *path, int z, float scaling, float shift);
 orc_vae_t *orc_vae_create_synth(int z, float scaling, float shift, uint64_t seed);
 void orc_vae_free(orc_vae_t *v);
 int orc_vae_decode(orc_vae_t *v, const float *latent, int lh, int lw, uint8_t *rgb, float *f32, int stop_after);
+/* iris_vae_encode for one image [3][H][W] -> latent [4z][H/16][W/16]; -1 without encoder weights */
+int orc_vae_encode(orc_vae_t *v, const float *img, int H, int W, float *latent);
 
 #endif

@@ -62,6 +62,7 @@ def oracle():
         lib.orc_vae_create_synth.restype = ctypes.c_void_p
         lib.orc_vae_create_synth.argtypes = [ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_uint64]
         lib.orc_vae_free.argtypes = [ctypes.c_void_p]
+        lib.orc_vae_encode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, FP]
         lib.orc_vae_decode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, FP,
                                        ctypes.c_int]
         _libs["oracle"] = lib
@@ -211,6 +212,10 @@ def hip():
         lib.iris_vae_gpu_decode.argtypes = [vp, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_image_free.argtypes = [ctypes.POINTER(IrisImage)]
         lib.iris_vae_gpu_z_channels.argtypes = [vp]
+        lib.iris_vae_gpu_encode.restype = ctypes.POINTER(ctypes.c_float)
+        lib.iris_vae_gpu_encode.argtypes = [vp, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int, IP, IP]
+        lib.iris_vae_gpu_encode_device.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        lib.iris_vae_gpu_has_encoder.argtypes = [vp]
         lib.iris_hip_conv3x3.argtypes = [ctypes.POINTER(Conv3x3)]
         if lib.iris_hip_init(0) != 0:
             raise RuntimeError("iris_hip_init failed: " + lib.iris_hip_last_error().decode())
@@ -316,6 +321,8 @@ def ref():
         lib.iris_vae_decode.restype = ctypes.POINTER(IrisImage)
         lib.iris_vae_decode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_vae_free.argtypes = [ctypes.c_void_p]
+        lib.iris_vae_encode.restype = ctypes.POINTER(ctypes.c_float)
+        lib.iris_vae_encode.argtypes = [ctypes.c_void_p, FP, ctypes.c_int, ctypes.c_int, ctypes.c_int, IP, IP]
         lib.iris_image_free.argtypes = [ctypes.POINTER(IrisImage)]
         _libs["ref"] = lib
     return _libs["ref"]
@@ -546,9 +553,10 @@ class Qwen3Encoder(ctypes.Structure):
     _fields_ = [("tokenizer", ctypes.c_void_p), ("model", ctypes.c_void_p)]
 
 
-def vae_tensor_list(z, flux=True):
-    """(name, shape) of the VAE decoder tensors in the diffusers layout the
-    reference loads (iris_vae.c:1227-1386); Flux adds bn and post_quant_conv."""
+def vae_tensor_list(z, flux=True, encoder=False):
+    """(name, shape) of the VAE decoder (and encoder) tensors in the diffusers
+    layout the reference loads (iris_vae.c:1227-1386); Flux adds bn,
+    post_quant_conv and quant_conv."""
     t = [("decoder.conv_in.weight", (512, z, 3, 3)), ("decoder.conv_in.bias", (512,))]
 
     def res(p, cin, cout):
@@ -579,15 +587,33 @@ def vae_tensor_list(z, flux=True):
     if flux:
         t += [("bn.running_mean", (4 * z,)), ("bn.running_var", (4 * z,)),
               ("post_quant_conv.weight", (z, z, 1, 1)), ("post_quant_conv.bias", (z,))]
+    if encoder:
+        t += [("encoder.conv_in.weight", (128, 3, 3, 3)), ("encoder.conv_in.bias", (128,))]
+        for level in range(4):
+            ch, prev = 128 * mult[level], 128 * mult[level - 1] if level else 128
+            for r in range(2):
+                t += res(f"encoder.down_blocks.{level}.resnets.{r}", prev if r == 0 and level else ch, ch)
+            if level < 3:
+                t += [(f"encoder.down_blocks.{level}.downsamplers.0.conv.weight", (ch, ch, 3, 3)),
+                      (f"encoder.down_blocks.{level}.downsamplers.0.conv.bias", (ch,))]
+        t += res("encoder.mid_block.resnets.0", 512, 512) + res("encoder.mid_block.resnets.1", 512, 512)
+        a = "encoder.mid_block.attentions.0."
+        t += [(a + "group_norm.weight", (512,)), (a + "group_norm.bias", (512,))]
+        for n in ("to_q", "to_k", "to_v", "to_out.0"):
+            t += [(a + n + ".weight", (512, 512)), (a + n + ".bias", (512,))]
+        t += [("encoder.conv_norm_out.weight", (512,)), ("encoder.conv_norm_out.bias", (512,)),
+              ("encoder.conv_out.weight", (2 * z, 512, 3, 3)), ("encoder.conv_out.bias", (2 * z,))]
+        if flux:
+            t += [("quant_conv.weight", (2 * z, 2 * z, 1, 1)), ("quant_conv.bias", (2 * z,))]
     return t
 
 
-def write_vae_file(path, z=32, flux=True, seed=0, bf16=False):
+def write_vae_file(path, z=32, flux=True, seed=0, bf16=False, encoder=False):
     """A random-init VAE decoder file: norm scales ~1, biases small, conv
     weights 1/sqrt(fan_in) (conv_out half that), batch-norm variances ~1."""
     rng = np.random.default_rng(seed)
     out = []
-    for name, shape in vae_tensor_list(z, flux):
+    for name, shape in vae_tensor_list(z, flux, encoder):
         n = int(np.prod(shape))
         fan = n // shape[0] if len(shape) > 1 else 1
         if name.endswith("running_var"):

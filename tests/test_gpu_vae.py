@@ -153,3 +153,86 @@ def test_1024_synthetic(lib):
     lib.iris_vae_gpu_free(g)
     assert np.array_equal(a, b) and np.array_equal(fa, fb)
     assert np.all(np.isfinite(fa)) and a.std() > 5 and 0.05 < np.mean((a > 0) & (a < 255))
+
+
+# ----------------------------------------------------------------- encoder
+
+@pytest.fixture(scope="module")
+def enc_models(lib, orc, tmp_path_factory):
+    d = tmp_path_factory.mktemp("vae_enc_gpu")
+    out = {}
+    for kind, z, flux, sc, sh, bf16 in (("flux", 32, True, 0.0, 0.0, False), ("zimage", 16, False, ZI_SCALE, ZI_SHIFT, True)):
+        path = str(d / f"{kind}.safetensors")
+        tl.write_vae_file(path, z=z, flux=flux, seed=5 + z, bf16=bf16, encoder=True)
+        g = ctypes.c_void_p(lib.iris_vae_gpu_load(path.encode(), z, sc, sh))
+        o = ctypes.c_void_p(orc.orc_vae_load(path.encode(), z, sc, sh))
+        assert g.value and o.value and lib.iris_vae_gpu_has_encoder(g)
+        out[kind] = (g, o, z)
+    yield out
+    for g, o, _ in out.values():
+        lib.iris_vae_gpu_free(g)
+        orc.orc_vae_free(o)
+
+
+def gpu_encode(lib, g, img, z, batch=1):
+    H, W = img.shape[-2:]
+    oh, ow = ctypes.c_int(), ctypes.c_int()
+    p = lib.iris_vae_gpu_encode(g, tl.fptr(np.ascontiguousarray(img)), batch, H, W, ctypes.byref(oh), ctypes.byref(ow))
+    assert p, lib.iris_hip_last_error()
+    assert (oh.value, ow.value) == (H // 16, W // 16)
+    out = np.ctypeslib.as_array(p, shape=(batch * 4 * z * oh.value * ow.value,)).copy()
+    ctypes.CDLL(None).free(ctypes.cast(p, ctypes.c_void_p))
+    return out.reshape(batch, 4 * z, oh.value, ow.value)
+
+
+def oracle_encode(orc, o, img, z):
+    H, W = img.shape[1:]
+    lat = np.zeros((4 * z, H // 16, W // 16), np.float32)
+    assert orc.orc_vae_encode(o, tl.fptr(np.ascontiguousarray(img)), H, W, tl.fptr(lat)) == 0
+    return lat
+
+
+@pytest.mark.parametrize("kind,H,W", [("flux", 32, 32), ("flux", 48, 80), ("zimage", 64, 48), ("flux", 256, 256)])
+def test_encode_vs_oracle(lib, orc, enc_models, kind, H, W):
+    """Same bar as the decoder: the latent over 8 resblocks, 3 stride-2
+    downsamples, attention and 25 convolutions with bf16 conv inputs."""
+    g, o, z = enc_models[kind]
+    img = np.random.default_rng(H * W).uniform(-1, 1, (3, H, W)).astype(np.float32)
+    print(f"vae encode {kind} {H}x{W}", flush=True)
+    got = gpu_encode(lib, g, img, z)[0]
+    want = oracle_encode(orc, o, img, z)
+    print(f"rel_l2 {tl.rel_l2(got, want):.3e} cosine {tl.cosine(got, want):.6f}")
+    assert tl.rel_l2(got, want) < 2e-2 and tl.cosine(got, want) > 0.999
+
+
+def test_encode_lcg_golden_model(lib, orc, tmp_path):
+    """The reference test's LCG-seeded VAE and 32x32 input (the oracle meets
+    its golden checksum on these): GPU against the oracle."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import vae_lcg
+    path = str(tmp_path / "lcg_vae.safetensors")
+    tl.write_safetensors(path, vae_lcg.build_vae(seed=1, z=32, with_quant=True))
+    g = ctypes.c_void_p(lib.iris_vae_gpu_load(path.encode(), 32, 0.0, 0.0))
+    o = ctypes.c_void_p(orc.orc_vae_load(path.encode(), 32, 0.0, 0.0))
+    img = vae_lcg.make_input(7, 32, 32)
+    got = gpu_encode(lib, g, img, 32)[0]
+    want = oracle_encode(orc, o, img, 32)
+    lib.iris_vae_gpu_free(g)
+    orc.orc_vae_free(o)
+    print(f"checksum gpu {vae_lcg.checksum(got):.5f} oracle {vae_lcg.checksum(want):.5f}")
+    assert tl.rel_l2(got, want) < 2e-2 and tl.cosine(got, want) > 0.999
+
+
+def test_encode_batch_and_errors(lib, enc_models, models):
+    g, _, z = enc_models["flux"]
+    rng = np.random.default_rng(3)
+    imgs = rng.uniform(-1, 1, (2, 3, 32, 48)).astype(np.float32)
+    both = gpu_encode(lib, g, imgs, z, batch=2)
+    assert np.array_equal(both[0], gpu_encode(lib, g, imgs[0], z)[0])
+    assert np.array_equal(both[1], gpu_encode(lib, g, imgs[1], z)[0])
+    oh, ow = ctypes.c_int(), ctypes.c_int()
+    assert not lib.iris_vae_gpu_encode(g, tl.fptr(imgs), 1, 40, 48, ctypes.byref(oh), ctypes.byref(ow))  # 40 % 16
+    dec_only = models["flux"][0]
+    assert not lib.iris_vae_gpu_has_encoder(dec_only)
+    assert not lib.iris_vae_gpu_encode(dec_only, tl.fptr(imgs), 1, 32, 48, ctypes.byref(oh), ctypes.byref(ow))

@@ -22,7 +22,7 @@ Conv = tl.Conv3x3
 @pytest.fixture(scope="module")
 def lib():
     lib = tl.hip()
-    lib.iris_hip_gn_stats.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int]
+    lib.iris_hip_gn_stats.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int]
     lib.iris_hip_gn_finalize.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp,
                                          ctypes.c_float, vp]
     lib.iris_hip_gn_apply.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
@@ -58,6 +58,9 @@ def np_conv3(x, w, b, up):
     (16, 24, 128, 256, 1, 1),     # fused nearest upsample
     (37, 29, 256, 64, 0, 3),      # odd sizes, split-K over 36 K steps
     (8, 64, 512, 512, 1, 4),      # 512 channels (8 K steps per tap), upsampled, split
+    (16, 96, 128, 128, 0, 1),     # cout <= 128 and rows >= 80 pixels: 512x128 tiles
+    (9, 200, 256, 64, 0, 2),      # 512x128 tiles, half-empty N, ragged M, split-K
+    (8, 160, 128, 128, 1, 1),     # 512x128 tiles through the upsample
 ])
 def test_conv3x3(lib, H, W, cin, cout, up, splits):
     rng = np.random.default_rng(H * W + cin)
@@ -90,6 +93,29 @@ def test_conv3x3(lib, H, W, cin, cout, up, splits):
     assert tl.rel_l2(ox.get(np.float32, (H * W, cout)), x0 + ref) < 1e-5
 
 
+@pytest.mark.parametrize("H,W,cin,cout,splits", [(16, 24, 128, 128, 1), (5, 7, 256, 256, 1), (4, 4, 512, 512, 4)])
+def test_conv3x3_stride2(lib, H, W, cin, cout, splits):
+    """up = 2: the encoder's downsample, a (2H) x (2W) input padded by one
+    zero row and column on the right and bottom, 3x3 stride 2."""
+    rng = np.random.default_rng(H * W * cin)
+    x = rng.standard_normal((2 * H, 2 * W, cin)).astype(np.float32)
+    wt = (rng.standard_normal((cout, 9, cin)) / np.sqrt(9 * cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    xp = np.pad(bf(x), ((0, 1), (0, 1), (0, 0)))
+    ref = np.zeros((H, W, cout)) + b
+    for tap in range(9):
+        ky, kx = tap // 3, tap % 3
+        ref += xp[ky:ky + 2 * H:2, kx:kx + 2 * W:2, :] @ bf(wt)[:, tap, :].T
+    dx, dw, db = tl.Dev.of(tl.to_bf16(x)), tl.Dev.of(tl.to_bf16(wt)), tl.Dev.of(b)
+    ws_bytes = splits * H * W * cout * 4
+    ws = tl.Dev(ws_bytes)
+    o = tl.Dev(H * W * cout * 4)
+    c = Conv(dx.ptr, dw.ptr, o.ptr, db.ptr, H, W, cin, cout, 2, cout, EPI_F32, splits, ws.ptr, ws_bytes)
+    assert lib.iris_hip_conv3x3(ctypes.byref(c)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    assert tl.rel_l2(o.get(np.float32, (H, W, cout)), ref) < 1e-5
+
+
 def test_conv3x3_rejects(lib):
     d = tl.Dev(1 << 20)
     bad = [Conv(d.ptr, d.ptr, d.ptr, None, 8, 8, 96, 64, 0, 64, EPI_F32, 1, None, 0),     # cin not 2^k
@@ -118,7 +144,7 @@ def test_group_norm(lib, pixels, C, is_bf16, swish):
     dg, db = tl.Dev.of(g), tl.Dev.of(b)
     part, ab = tl.Dev(64 * C * 16), tl.Dev(2 * C * 4)
     dy, raw = tl.Dev(pixels * C * 2), tl.Dev(pixels * C * 2)
-    nblk = lib.iris_hip_gn_stats(dx.ptr, is_bf16, pixels, C, part.ptr, 64)
+    nblk = lib.iris_hip_gn_stats(dx.ptr, is_bf16, pixels, C, 32, part.ptr, 64)
     assert 0 < nblk <= 64, lib.iris_hip_last_error()
     assert lib.iris_hip_gn_finalize(part.ptr, nblk, pixels, C, 32, dg.ptr, db.ptr, 1e-4, ab.ptr) == 0
     assert lib.iris_hip_gn_apply(dx.ptr, is_bf16, ab.ptr, pixels, C, swish, dy.ptr, raw.ptr) == 0
@@ -183,7 +209,7 @@ def test_vae_front(lib, z, divide, pq):
 
 def test_conv_out(lib):
     rng = np.random.default_rng(1)
-    H, W, cin = 33, 47, 128
+    H, W, cin = 33, 47, 128       # W % 4 != 0: a partial quad per row
     g = rng.standard_normal((H, W, cin)).astype(np.float32)
     w = (0.5 * rng.standard_normal((3, cin, 3, 3)) / np.sqrt(9 * cin)).astype(np.float32)
     b = (0.1 * rng.standard_normal(3)).astype(np.float32)

@@ -141,3 +141,61 @@ def test_deterministic_and_synthetic(orc):
     orc.orc_vae_free(v)
     assert np.array_equal(a, b) and np.array_equal(fa, fb)
     assert np.all(np.isfinite(fa)) and a.std() > 5
+
+
+# ----------------------------------------------------------------- encoder
+
+@pytest.fixture(scope="module")
+def enc_files(tmp_path_factory):
+    d = tmp_path_factory.mktemp("vae_enc")
+    flux, zi = str(d / "flux_vae.safetensors"), str(d / "zimage_vae.safetensors")
+    tl.write_vae_file(flux, z=32, flux=True, seed=3, encoder=True)
+    tl.write_vae_file(zi, z=16, flux=False, seed=4, bf16=True, encoder=True)
+    return {"flux": (flux, 32, 0.0, 0.0), "zimage": (zi, 16, ZI_SCALE, ZI_SHIFT)}
+
+
+def oracle_encode(orc, v, img, z):
+    H, W = img.shape[1:]
+    lat = np.zeros((4 * z, H // 16, W // 16), np.float32)
+    assert orc.orc_vae_encode(v, tl.fptr(np.ascontiguousarray(img)), H, W, tl.fptr(lat)) == 0
+    return lat
+
+
+def test_encode_golden_checksum(orc, tmp_path):
+    """The reference test's own golden value (debug/test_vae.c:292-309): the
+    LCG-seeded VAE of its build_vae, a 32x32 input from seed 7, checksum
+    sum(latent[i] * (i % 13 + 1)) = 29.091131 +- 0.2."""
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import vae_lcg
+    path = str(tmp_path / "lcg_vae.safetensors")
+    tl.write_safetensors(path, vae_lcg.build_vae(seed=1, z=32, with_quant=True))
+    v = ctypes.c_void_p(orc.orc_vae_load(path.encode(), 32, 0.0, 0.0))
+    assert v.value
+    lat = oracle_encode(orc, v, vae_lcg.make_input(7, 32, 32), 32)
+    orc.orc_vae_free(v)
+    assert lat.shape == (128, 2, 2)
+    assert abs(vae_lcg.checksum(lat) - vae_lcg.GOLDEN_ENCODE_CHECKSUM) < vae_lcg.GOLDEN_TOL, vae_lcg.checksum(lat)
+
+
+@pytest.mark.skipif(not os.path.exists(tl.REF_SO), reason="reference build (oracle/_ref) not present")
+@pytest.mark.parametrize("kind,H,W", [("flux", 32, 48), ("zimage", 48, 32)])
+def test_encode_vs_reference(orc, enc_files, kind, H, W):
+    path, z, sc, sh = enc_files[kind]
+    ref = tl.ref()
+    sf = ctypes.c_void_p(ref.safetensors_open(path.encode()))
+    rv = ctypes.c_void_p(ref.iris_vae_load_safetensors_ex(sf, z, sc, sh))
+    ref.safetensors_close(sf)
+    assert rv.value
+    img = np.random.default_rng(H + W).uniform(-1, 1, (3, H, W)).astype(np.float32)
+    oh, ow = ctypes.c_int(), ctypes.c_int()
+    p = ref.iris_vae_encode(rv, tl.fptr(img), 1, H, W, ctypes.byref(oh), ctypes.byref(ow))
+    assert p and (oh.value, ow.value) == (H // 16, W // 16)
+    want = np.ctypeslib.as_array(p, shape=(4 * z, oh.value, ow.value)).copy()
+    ctypes.CDLL(None).free(ctypes.cast(p, ctypes.c_void_p))
+    ref.iris_vae_free(rv)
+    v = ctypes.c_void_p(orc.orc_vae_load(path.encode(), z, sc, sh))
+    got = oracle_encode(orc, v, img, z)
+    orc.orc_vae_free(v)
+    assert np.all(np.isfinite(want)) and want.std() > 0.1
+    assert tl.rel_l2(got, want) < 1e-4
