@@ -406,7 +406,7 @@ def run_vae(lib, c, args):
     c_ms = time_launches(lib, lambda: lib.iris_hip_conv3x3(ctypes.byref(conv)))
     for d in (x, wt, o, lat, rgb):
         d.close()
-    kernels = [kernel_entry("gemm_bf16_kernel<conv>: 3x3 conv 256->256, 512x512 pixels", c_ms,
+    kernels = [kernel_entry("gemm_bf16_kernel<1> (implicit-GEMM 3x3 conv): 256->256, 512x512 pixels", c_ms,
                             2.0 * H * W * cin * cout * 9, 5, "conv_256_512")]
     cfg = {"workload": c["workload"], "latent": [4 * c["z"], lh, lw], "image": [16 * lh, 16 * lw],
            "z_channels": c["z"], "bottleneck_tokens": 4 * lh * lw}
