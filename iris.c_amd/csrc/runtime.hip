@@ -7,6 +7,8 @@
 #include "iris_internal.h"
 
 #include <atomic>
+#include <mutex>
+#include <thread>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -91,9 +93,65 @@ void iris_hip_free(void *p) {
 
 size_t iris_hip_mem_in_use(void) { return g_in_use; }
 
+/* Weight upload (the reference maps safetensors and copies tensor by tensor,
+ * iris_safetensors.c, iris_transformer_flux.c:473-570): copies of 8 MiB and
+ * more go through a ring of 4 pinned 16 MiB staging buffers. Host threads
+ * copy chunk i from the (possibly mmap'd, page-faulting) source into a free
+ * staging buffer while the DMA engine moves chunk i - 1 to the device, so the
+ * file read, the host copy and PCIe overlap. A buffer is refilled only after
+ * the event recorded behind its previous DMA has completed. The call returns
+ * once the whole source has been copied out, so the caller may reuse it, as
+ * with a pageable hipMemcpyAsync; during stream capture the plain copy is
+ * used. */
+namespace {
+constexpr size_t UP_CHUNK = 16u << 20, UP_MIN = 8u << 20;
+constexpr int UP_BUFS = 4, UP_THREADS = 8;
+void *g_up_buf[UP_BUFS];
+hipEvent_t g_up_ev[UP_BUFS];
+int g_up_state;   /* 0 untried, 1 ready, -1 unavailable */
+std::mutex g_up_mutex;   /* one upload at a time through the staging ring */
+
+int up_init() {
+    if (g_up_state) return g_up_state > 0 ? 0 : -1;
+    g_up_state = -1;
+    for (int i = 0; i < UP_BUFS; i++) {
+        if (hipHostMalloc(&g_up_buf[i], UP_CHUNK, hipHostMallocDefault) != hipSuccess) return -1;
+        if (hipEventCreateWithFlags(&g_up_ev[i], hipEventDisableTiming) != hipSuccess) return -1;
+    }
+    g_up_state = 1;
+    return 0;
+}
+
+void par_memcpy(void *dst, const void *src, size_t n) {
+    const size_t per = ((n + UP_THREADS - 1) / UP_THREADS + 4095) & ~(size_t)4095;
+    std::thread th[UP_THREADS];
+    int used = 0;
+    for (size_t off = per; off < n; off += per, used++)
+        th[used] = std::thread(memcpy, (char *)dst + off, (const char *)src + off, n - off < per ? n - off : per);
+    memcpy(dst, src, n < per ? n : per);
+    for (int i = 0; i < used; i++) th[i].join();
+}
+}  // namespace
+
 int iris_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
     if (!bytes) return 0;
-    return iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream), "memcpy h2d");
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (bytes < UP_MIN || hipStreamIsCapturing(g_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone ||
+        up_init())
+        return iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream), "memcpy h2d");
+    std::lock_guard<std::mutex> lock(g_up_mutex);
+    size_t i = 0;
+    for (size_t off = 0; off < bytes; off += UP_CHUNK, i++) {
+        const int b = (int)(i % UP_BUFS);
+        const size_t n = bytes - off < UP_CHUNK ? bytes - off : UP_CHUNK;
+        if (iris_check(hipEventSynchronize(g_up_ev[b]), "upload staging wait")) return -1;
+        par_memcpy(g_up_buf[b], (const char *)src + off, n);
+        if (iris_check(hipMemcpyAsync((char *)dst + off, g_up_buf[b], n, hipMemcpyHostToDevice, g_stream),
+                       "upload chunk") ||
+            iris_check(hipEventRecord(g_up_ev[b], g_stream), "upload event"))
+            return -1;
+    }
+    return 0;
 }
 
 int iris_hip_memcpy_d2h(void *dst, const void *src, size_t bytes) {
