@@ -190,6 +190,9 @@ typedef struct {
     int period;                       /* 0: none; else split and table row use row % period */
     float eps;
     int kv_heads;                     /* K / V heads; 0: same as heads */
+    const float *kcos_t, *ksin_t;     /* K-side tables [rows][128]; NULL: the Q tables (SREF RoPE
+                                         band control scales the reference rows' K bands,
+                                         iris_transformer_flux.c:1272-1321) */
 } iris_qkprep_args_t;
 int iris_hip_qk_prepare(const iris_qkprep_args_t *a);
 
@@ -209,6 +212,9 @@ typedef struct {
     int kv_lo0, kv_hi0, kv_lo1, kv_hi1;
     int causal;                       /* 1: key j is masked for query i < j */
     int kv_group;                     /* query heads per K / V head; 0: 1 */
+    int bias_from;                    /* keys >= bias_from get key_bias added to their logits */
+    float key_bias;                   /* (SREF strength: log gamma on the reference keys,
+                                         iris_transformer_flux.c:1328-1338); 0: none */
 } iris_attn_args_t;
 int iris_hip_attention(const iris_attn_args_t *a);
 

@@ -161,6 +161,17 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
                     s[ks][r] = ok ? s[ks][r] : -INFINITY;
                 }
         }
+        if (a.key_bias != 0.0f && k0 + KB > a.bias_from) {
+            /* logit bias on keys >= bias_from, in units of the raw scores */
+            const float bs = a.key_bias / a.scale;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = k0 + ks * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
+                    s[ks][r] += key >= a.bias_from ? bs : 0.0f;
+                }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)

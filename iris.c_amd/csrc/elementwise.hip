@@ -154,6 +154,14 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
     }
 #pragma unroll
     for (int which = 0; which < 2; which++) {
+        if (which && a.kcos_t) {   /* K-side tables (reference-key band control) */
+            const float4 c0 = *(const float4 *)(a.kcos_t + (size_t)prow * 128 + d0);
+            const float4 c1 = *(const float4 *)(a.kcos_t + (size_t)prow * 128 + d0 + 4);
+            const float4 s0 = *(const float4 *)(a.ksin_t + (size_t)prow * 128 + d0);
+            const float4 s1 = *(const float4 *)(a.ksin_t + (size_t)prow * 128 + d0 + 4);
+            c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+            sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+        }
         const float *wsel = which ? (use_b ? a.wkB : a.wkA) : (use_b ? a.wqB : a.wqA);
         const float4 w0 = *(const float4 *)(wsel + d0), w1 = *(const float4 *)(wsel + d0 + 4);
         const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};

@@ -60,6 +60,9 @@ typedef struct {
     float *lat;              /* [C][I] target then refs, NCHW per image */
     float *vel;              /* [B][C][I0] */
     float *rope_cos, *rope_sin;   /* [S][128] */
+    float *krope_cos, *krope_sin; /* [S][128] K side: the reference rows' H/W bands scaled (SREF) */
+    float kshf, kslf;             /* band scales the K tables hold */
+    float kgamma;                 /* SREF strength the captured graph applies */
     float *tsin;             /* [256] */
     float *tmp, *temb;       /* [h] */
     float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
@@ -384,7 +387,7 @@ int iris_transformer_text_dim(iris_transformer_t *tf) { return tf->text_dim; }
 static void work_free(work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
-                    w->rope_cos, w->rope_sin, w->tsin, w->tmp, w->temb, w->mod};
+                    w->rope_cos, w->rope_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp, w->temb, w->mod};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -398,6 +401,60 @@ static int same_geometry(const work_t *w, int ih, int iw, const iris_ref_t *refs
 }
 
 static int enqueue_forward(iris_transformer_t *tf);
+
+/* K-side RoPE tables: the Q tables with the H and W bands of the reference
+ * rows [T + I0, S) scaled by s(d) = shf + (slf - shf) (d / 15)^2 per rotation
+ * pair d (band_scale_ref_krope, iris_transformer_flux.c:1255-1280; a scalar
+ * per pair commutes with the rotation, so it scales that band's share of
+ * q . k). Text and target rows are unchanged. */
+static int fill_ktables(iris_transformer_t *tf, const float *c, const float *s) {
+    work_t *w = &tf->w;
+    const size_t n = (size_t)w->S * 128;
+    float *kc = (float *)malloc(n * sizeof(float)), *ks = (float *)malloc(n * sizeof(float));
+    if (!kc || !ks) { free(kc); free(ks); return -1; }
+    memcpy(kc, c, n * sizeof(float));
+    memcpy(ks, s, n * sizeof(float));
+    const float shf = tf->sref_shf, slf = tf->sref_slf;
+    const int ad = tf->axis_dim, half = ad / 2;
+    if (w->n_refs > 0 && (shf != 1.0f || slf != 1.0f)) {
+        float sd[64];
+        for (int d = 0; d < half && d < 64; d++) {
+            const float dn = half > 1 ? (float)d / (float)(half - 1) : 0.0f;
+            sd[d] = shf + (slf - shf) * dn * dn;
+        }
+        for (int pos = w->T + w->I0; pos < w->S; pos++) {
+            float *cr = kc + (size_t)pos * 128, *sr = ks + (size_t)pos * 128;
+            for (int d = 0; d < half; d++) {
+                const int hh = ad + d * 2, ww = ad * 2 + d * 2;
+                cr[hh] *= sd[d]; cr[hh + 1] *= sd[d]; sr[hh] *= sd[d]; sr[hh + 1] *= sd[d];
+                cr[ww] *= sd[d]; cr[ww + 1] *= sd[d]; sr[ww] *= sd[d]; sr[ww + 1] *= sd[d];
+            }
+        }
+    }
+    const int rc = iris_hip_memcpy_h2d(w->krope_cos, kc, n * 4) || iris_hip_memcpy_h2d(w->krope_sin, ks, n * 4) ||
+                   iris_hip_sync();
+    free(kc);
+    free(ks);
+    if (rc) return -1;
+    w->kshf = shf;
+    w->kslf = slf;
+    return 0;
+}
+
+/* (re)capture one forward into the step graph */
+static int capture(iris_transformer_t *tf) {
+    work_t *w = &tf->w;
+    if (w->graph) { iris_hip_graph_destroy(w->graph); w->graph = NULL; }
+    w->kgamma = tf->sref_strength;
+    if (iris_hip_graph_begin()) return -1;
+    if (enqueue_forward(tf)) {
+        void *g = iris_hip_graph_end();
+        iris_hip_graph_destroy(g);
+        return -1;
+    }
+    w->graph = iris_hip_graph_end();
+    return w->graph ? 0 : -1;
+}
 
 int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *refs, int n_refs, int T, int B) {
     work_t *w = &tf->w;
@@ -431,6 +488,8 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
     DA(w->lat, (size_t)w->I * C * 4);
     DA(w->vel, (size_t)B * C * w->I0 * 4);
     DA(w->rope_cos, S * 128 * 4);
+    DA(w->krope_cos, S * 128 * 4);
+    DA(w->krope_sin, S * 128 * 4);
     DA(w->rope_sin, S * 128 * 4);
     DA(w->tsin, 256 * 4);
     DA(w->tmp, (size_t)h * 4);
@@ -452,20 +511,12 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
             off += (size_t)refs[r].h * refs[r].w * 128;
         }
         int rc = iris_hip_memcpy_h2d(w->rope_cos, c, S * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, S * 128 * 4) ||
-                 iris_hip_sync();
+                 iris_hip_sync() || fill_ktables(tf, c, s);
         free(c); free(s);
         if (rc) goto fail;
     }
     w->valid = 1;
-    /* capture one forward */
-    if (iris_hip_graph_begin()) goto fail;
-    if (enqueue_forward(tf)) {
-        void *g = iris_hip_graph_end();
-        iris_hip_graph_destroy(g);
-        goto fail;
-    }
-    w->graph = iris_hip_graph_end();
-    if (!w->graph) goto fail;
+    if (capture(tf)) goto fail;
     return 0;
 fail:
     fprintf(stderr, "iris_flux_prepare: %s\n", iris_hip_last_error());
@@ -504,6 +555,7 @@ static int qk_prepare(iris_transformer_t *tf, const float *wqA, const float *wkA
         a.rows = w->S; a.heads = tf->heads;
         a.wqA = wqA; a.wkA = wkA; a.wqB = wqB; a.wkB = wkB; a.split = split;
         a.cos_t = w->rope_cos; a.sin_t = w->rope_sin;
+        a.kcos_t = w->krope_cos; a.ksin_t = w->krope_sin;
         a.eps = 1e-6f;
         CK(iris_hip_qk_prepare(&a));
     }
@@ -522,6 +574,12 @@ static int attention(iris_transformer_t *tf, uint16_t *o, int ld_o) {
     a.vt_bstride = (long long)tf->heads * 128 * w->S_pad; a.o_bstride = (long long)w->S * ld_o;
     a.scale = 1.0f / sqrtf(128.0f);
     a.kv_lo0 = 0; a.kv_hi0 = w->S;
+    /* SREF strength (sref_set_strength_bias, iris_transformer_flux.c:1328-1338):
+     * log gamma on the logits of the reference keys, the trailing I - I0 tokens */
+    if (w->n_refs > 0 && tf->sref_strength != 1.0f) {
+        a.bias_from = w->S - (w->I - w->I0);
+        a.key_bias = logf(tf->sref_strength);
+    }
     return iris_hip_attention(&a);
 }
 
@@ -698,6 +756,17 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
     work_t *w = &tf->w;
     if (!w->valid) return -1;
     if (adapter_active(tf)) return -1;
+    /* SREF settings changed since the graph was captured */
+    if (w->kshf != tf->sref_shf || w->kslf != tf->sref_slf) {
+        const size_t n = (size_t)w->S * 128;
+        float *c = (float *)malloc(n * 4), *s = (float *)malloc(n * 4);
+        const int rc = !c || !s || iris_hip_memcpy_d2h(c, w->rope_cos, n * 4) ||
+                       iris_hip_memcpy_d2h(s, w->rope_sin, n * 4) || fill_ktables(tf, c, s);
+        free(c);
+        free(s);
+        if (rc) return -1;
+    }
+    if (w->kgamma != tf->sref_strength && capture(tf)) return -1;
     /* get_timestep_embedding(t * 1000), :3967 */
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
@@ -737,6 +806,8 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
     if (!strcmp(name, "velocity")) return w->vel;
     if (!strcmp(name, "tokens")) return w->tok;
     if (!strcmp(name, "rope_cos")) return w->rope_cos;
+    if (!strcmp(name, "krope_cos")) return w->krope_cos;
+    if (!strcmp(name, "krope_sin")) return w->krope_sin;
     if (!strcmp(name, "rope_sin")) return w->rope_sin;
     if (!strcmp(name, "t_emb")) return w->temb;
     if (!strcmp(name, "mod")) return w->mod;
@@ -754,8 +825,8 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
 
 /* The reference's adapter setters (iris_transformer_flux.c:5131-5201), kept
  * so a caller links unchanged. The HIP forward implements none of the
- * adapters: while one is attached (LoRA, CSD style delta, SREF bands or
- * strength other than off, IP-Adapter) every forward fails with a message
+ * adapters other than SREF: while one is attached (LoRA, CSD style delta,
+ * IP-Adapter) every forward fails with a message
  * instead of silently ignoring it. Ownership follows the reference: the
  * transformer takes what it is given and releases it on replacement or free
  * through the reference's own release functions when those are linked in. */
@@ -775,9 +846,7 @@ static void release_adapters(iris_transformer_t *tf) {
 
 static int adapter_active(const iris_transformer_t *tf) {
     const char *what = tf->lora ? "LoRA" : tf->ip ? "IP-Adapter"
-                     : (tf->csd_delta && !tf->csd_skip) ? "CSD style delta"
-                     : (tf->sref_shf != 1.0f || tf->sref_slf != 1.0f) ? "SREF RoPE bands"
-                     : tf->sref_strength != 1.0f ? "SREF strength" : NULL;
+                     : (tf->csd_delta && !tf->csd_skip) ? "CSD style delta" : NULL;
     if (what) fprintf(stderr, "iris_hip: %s is attached; the HIP denoiser does not apply adapters\n", what);
     return what != NULL;
 }

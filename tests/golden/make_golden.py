@@ -96,6 +96,12 @@ def flux_goldens(r, d, res):
     refs = (Ref * 2)(Ref(tl.fptr(r1), 8, 8, 1), Ref(tl.fptr(r2), 4, 6, 2))
     p = r.iris_transformer_forward_with_multi_refs(tf, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(temb_txt), T, f(0.6))
     res["flux_fwd_refs"] = tl.take_f32(r, p, 128 * 64)
+    # SREF RoPE band control on the reference keys (iris_transformer_set_sref_bands)
+    r.iris_transformer_set_sref_bands.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_float]
+    r.iris_transformer_set_sref_bands(tf, 0.0, 8.0)
+    p = r.iris_transformer_forward_with_multi_refs(tf, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(temb_txt), T, f(0.6))
+    res["flux_fwd_refs_sref_bands"] = tl.take_f32(r, p, 128 * 64)
+    r.iris_transformer_set_sref_bands(tf, 1.0, 1.0)
     # 2-step Euler sample from the reference's own noise and schedule
     sched = r.iris_official_schedule(2, 64)
     sched_arr = np.ctypeslib.as_array(ctypes.cast(sched, tl.FP), shape=(3,)).copy()

@@ -90,7 +90,8 @@ class QkPrepArgs(ctypes.Structure):
                 ("ld_vt", ctypes.c_int), ("rows", ctypes.c_int), ("heads", ctypes.c_int),
                 ("wqA", ctypes.c_void_p), ("wkA", ctypes.c_void_p), ("wqB", ctypes.c_void_p), ("wkB", ctypes.c_void_p),
                 ("split", ctypes.c_int), ("cos_t", ctypes.c_void_p), ("sin_t", ctypes.c_void_p),
-                ("period", ctypes.c_int), ("eps", ctypes.c_float), ("kv_heads", ctypes.c_int)]
+                ("period", ctypes.c_int), ("eps", ctypes.c_float), ("kv_heads", ctypes.c_int),
+                ("kcos_t", ctypes.c_void_p), ("ksin_t", ctypes.c_void_p)]
 
 
 class AttnArgs(ctypes.Structure):
@@ -101,7 +102,7 @@ class AttnArgs(ctypes.Structure):
                 ("vt_bstride", ctypes.c_longlong), ("o_bstride", ctypes.c_longlong),
                 ("scale", ctypes.c_float), ("kv_lo0", ctypes.c_int), ("kv_hi0", ctypes.c_int),
                 ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int), ("causal", ctypes.c_int),
-                ("kv_group", ctypes.c_int)]
+                ("kv_group", ctypes.c_int), ("bias_from", ctypes.c_int), ("key_bias", ctypes.c_float)]
 
 
 class Conv3x3(ctypes.Structure):

@@ -282,7 +282,10 @@ def test_rms_gated_add(lib, gate_mode):
     assert tl.rel_l2(dx.get(np.float32, (rows, cols)), want) < 1e-6
 
 
-def test_qk_prepare(lib):
+@pytest.mark.parametrize("ktables", [False, True])
+def test_qk_prepare(lib, ktables):
+    """Q/K RMSNorm + rotary; with ktables, K rotates with its own tables
+    (SREF band control: the reference rows' K bands are scaled)."""
     rng = np.random.default_rng(4)
     S, H, split = 200, 3, 60
     h = H * 128
@@ -296,12 +299,17 @@ def test_qk_prepare(lib):
              vt=tl.Dev(H * 128 * S_pad * 2), c=tl.Dev.of(cos), s=tl.Dev.of(sin))
     ws = [tl.Dev.of(w) for w in (wqA, wkA, wqB, wkB)]
     d["vt"].put(np.full(H * 128 * S_pad, 0x7FC0, np.uint16))     # poison: padding must be rewritten
+    kscale = np.repeat(rng.uniform(0, 3, (S, 64)).astype(np.float32), 2, 1) if ktables else np.ones((S, 128), np.float32)
+    kcos, ksin = (cos * kscale).astype(np.float32), (sin * kscale).astype(np.float32)
+    d["kc"], d["ks"] = tl.Dev.of(kcos), tl.Dev.of(ksin)
     a = tl.QkPrepArgs(d["qkv"].ptr, 3 * h, h, 2 * h, d["q"].ptr, d["k"].ptr, d["vt"].ptr, S_pad, S, H,
-                      ws[0].ptr, ws[1].ptr, ws[2].ptr, ws[3].ptr, split, d["c"].ptr, d["s"].ptr, 0, 1e-6)
+                      ws[0].ptr, ws[1].ptr, ws[2].ptr, ws[3].ptr, split, d["c"].ptr, d["s"].ptr, 0, 1e-6, 0,
+                      d["kc"].ptr if ktables else None, d["ks"].ptr if ktables else None)
     assert lib.iris_hip_qk_prepare(ctypes.byref(a)) == 0
     assert lib.iris_hip_sync() == 0
     x = bf(qkv).astype(np.float64)
     for which, col, wa, wb, dev in [(0, 0, wqA, wqB, "q"), (1, h, wkA, wkB, "k")]:
+        cos, sin = (kcos, ksin) if which else (cos, sin)
         got = tl.bf16_to_f32(d[dev].get(np.uint16, (S, h)))
         for hh in range(H):
             v = x[:, col + hh * 128: col + (hh + 1) * 128]
@@ -360,3 +368,32 @@ def test_euler_and_cfg(lib):
     assert lib.iris_hip_euler(dz.ptr, dv.ptr, dv2.ptr, 4.0, -0.1, 1.0, n) == 0
     np.testing.assert_allclose(dz.get(np.float32, (n,)), z + np.float32(-0.1) * (v + 4 * (v2 - v)), rtol=1e-5,
                                atol=1e-6)
+
+
+@pytest.mark.parametrize("S,bias_from,gamma", [(200, 130, 0.3), (513, 64, 4.0), (96, 96, 0.5)])
+def test_flash_attention_key_bias(lib, S, bias_from, gamma):
+    """SREF strength: log(gamma) added to the logits of keys >= bias_from
+    (iris_transformer_flux.c:1328-1338), against float64 numpy."""
+    rng = np.random.default_rng(S + bias_from)
+    H = 2
+    S_pad = (S + 63) // 64 * 64
+    q = rng.standard_normal((S, H * 128), np.float32) * np.float32(2.0)
+    k = rng.standard_normal((S, H * 128), np.float32)
+    v = rng.standard_normal((S, H * 128), np.float32)
+    vt = np.zeros((H, 128, S_pad), np.float32)
+    for h in range(H):
+        vt[h, :, :S] = v[:, h * 128:(h + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(q)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    do = tl.Dev(S * H * 128 * 2)
+    a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, do.ptr, H * 128, H * 128, S_pad, H * 128, S, S, H, 1, 0, 0, 0, 0,
+                    1 / math.sqrt(128), 0, S, 0, 0, 0, 0, bias_from, math.log(gamma))
+    assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(do.get(np.uint16, (S, H * 128)))
+    bias = np.where(np.arange(S) >= bias_from, math.log(gamma), 0.0)[None, :]
+    for h in range(H):
+        sl = slice(h * 128, (h + 1) * 128)
+        sc = bf(q[:, sl]).astype(np.float64) @ bf(k[:, sl]).astype(np.float64).T / math.sqrt(128) + bias
+        p = np.exp(sc - sc.max(1, keepdims=True))
+        ref = (p / p.sum(1, keepdims=True)) @ bf(v[:, sl]).astype(np.float64)
+        assert tl.rel_l2(got[:, sl], ref) < 1e-2, h
