@@ -109,6 +109,11 @@ typedef struct {
 } iris_conv3x3_t;
 int iris_hip_conv3x3(const iris_conv3x3_t *c);
 
+/* LoRA merge (lora_apply's out += scale * B (A x), iris_lora.c:43-90, folded
+ * into the weights): W[rowmap[o]][i] = bf16(W + scale * dW[o][i]), W bf16
+ * [.][cols], dW f32 [rows][cols], rowmap device int [rows]. */
+int iris_hip_merge_rows(uint16_t *d_W, int cols, const int *d_rowmap, const float *d_dW, int rows, float scale);
+
 /* ---- VAE decoder kernels (vae.hip), channels-last (NHWC) activations ---- */
 /* GroupNorm (iris_group_norm, iris_kernels.c:542) in three launches:
  * per-block float64 group sums of x (f32, or bf16 if is_bf16) over

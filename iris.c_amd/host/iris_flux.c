@@ -29,6 +29,30 @@
 
 #define MAX_REFS 8
 
+/* The reference's LoRA state (iris_lora.h:22-51), same layout: a caller loads
+ * it with the reference's lora_load and hands it to iris_transformer_set_lora. */
+typedef struct {
+    float *lora_A;   /* [rank][in_dim] */
+    float *lora_B;   /* [out_dim][rank] */
+    int rank, in_dim, out_dim;
+} lora_adapter_t;
+
+typedef struct {
+    float scale;
+    int num_double_blocks;
+    lora_adapter_t *double_img_q, *double_img_k, *double_img_v, *double_img_proj;
+    lora_adapter_t *double_txt_q, *double_txt_k, *double_txt_v, *double_txt_proj;
+    int num_single_blocks;
+    lora_adapter_t *single_linear1, *single_linear2;
+    float *scratch;
+    int scratch_len, max_rank;
+} lora_state_t;
+
+typedef struct {
+    uint16_t *w, *orig;   /* device weight and its copy before the merge */
+    size_t bytes;
+} lora_backup_t;
+
 typedef struct {
     uint16_t *img_qkv, *img_o, *img_ffin, *img_down;    /* ffin rows gate/up interleaved by 32 */
     uint16_t *txt_qkv, *txt_o, *txt_ffin, *txt_down;
@@ -79,6 +103,10 @@ struct iris_transformer {
     work_t w;
     /* adapters set through the reference's setters (owned, not applied) */
     void *lora, *ip, *ip_embeds;
+    void *lora_merged;                /* the LoRA state merged into the weights, or NULL */
+    int lora_dirty;                   /* set_lora was called since the last merge */
+    lora_backup_t *lora_bk;
+    int n_lora_bk, cap_lora_bk;
     float *csd_delta;
     int csd_skip;
     float sref_shf, sref_slf, sref_strength;
@@ -295,10 +323,13 @@ static int load_weights(iris_transformer_t *tf, source_t *s) {
 static void work_free(work_t *w);
 static void release_adapters(iris_transformer_t *tf);
 static int adapter_active(const iris_transformer_t *tf);
+static int lora_sync(iris_transformer_t *tf);
 
 void iris_transformer_free(iris_transformer_t *tf) {
     if (!tf) return;
     work_free(&tf->w);
+    for (int i = 0; i < tf->n_lora_bk; i++) iris_hip_free(tf->lora_bk[i].orig);
+    free(tf->lora_bk);
     iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
     iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
     iris_hip_free(tf->final_mod); iris_hip_free(tf->proj_out);
@@ -756,6 +787,7 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
     work_t *w = &tf->w;
     if (!w->valid) return -1;
     if (adapter_active(tf)) return -1;
+    if (lora_sync(tf)) return -1;
     /* SREF settings changed since the graph was captured */
     if (w->kshf != tf->sref_shf || w->kslf != tf->sref_slf) {
         const size_t n = (size_t)w->S * 128;
@@ -823,6 +855,144 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
 
 /* ------------------------------------------------------------- adapters */
 
+/* ------------------------------------------------------------------ LoRA */
+
+/* The reference adds scale * B (A x) to the output of each adapted linear
+ * (lora_apply, iris_lora.c:43-90; call sites iris_transformer_flux.c:2430-2532,
+ * :3819, :3910). The linears have no bias, so this equals the linear with
+ * W + scale * B A: the product is formed once with the MFMA GEMM (A and B in
+ * bf16, rank padded to 64) and merged into the resident bf16 weights through
+ * a row map into the fused / SwiGLU-interleaved layouts. The weights before
+ * the merge are kept and restored when the LoRA is replaced or removed. */
+static int lora_backup(iris_transformer_t *tf, uint16_t *w, size_t bytes) {
+    for (int i = 0; i < tf->n_lora_bk; i++)
+        if (tf->lora_bk[i].w == w) return 0;
+    if (tf->n_lora_bk == tf->cap_lora_bk) {
+        const int cap = tf->cap_lora_bk ? 2 * tf->cap_lora_bk : 64;
+        lora_backup_t *n = (lora_backup_t *)realloc(tf->lora_bk, cap * sizeof(*n));
+        if (!n) return -1;
+        tf->lora_bk = n;
+        tf->cap_lora_bk = cap;
+    }
+    uint16_t *o = (uint16_t *)iris_hip_malloc(bytes);
+    if (!o || iris_hip_memcpy_d2d(o, w, bytes)) { iris_hip_free(o); return -1; }
+    tf->lora_bk[tf->n_lora_bk++] = (lora_backup_t){w, o, bytes};
+    return 0;
+}
+
+static int lora_restore(iris_transformer_t *tf) {
+    int rc = 0;
+    for (int i = 0; i < tf->n_lora_bk; i++) {
+        rc |= iris_hip_memcpy_d2d(tf->lora_bk[i].w, tf->lora_bk[i].orig, tf->lora_bk[i].bytes);
+        rc |= iris_hip_sync();
+        iris_hip_free(tf->lora_bk[i].orig);
+    }
+    tf->n_lora_bk = 0;
+    tf->lora_merged = NULL;
+    return rc ? -1 : 0;
+}
+
+/* W (total_rows x cols, bf16) += scale * B A for output rows o -> row map(o):
+ * row0 + o, except rows >= il_from, which are the SwiGLU gate / up halves
+ * (il_len rows each) interleaved in groups of SWIGLU_GROUP */
+static int lora_merge(iris_transformer_t *tf, uint16_t *W, size_t total_rows, int cols, const lora_adapter_t *ad,
+                      float scale, int row0, int il_from, int il_len) {
+    if (!ad || !ad->lora_A || !ad->lora_B || ad->rank <= 0) return 0;
+    if (ad->in_dim != cols) {
+        fprintf(stderr, "iris_hip: LoRA adapter in_dim %d, the linear has %d\n", ad->in_dim, cols);
+        return -1;
+    }
+    const int r = ad->rank, rp = (r + 63) / 64 * 64, out = ad->out_dim;
+    uint16_t *hb = (uint16_t *)calloc((size_t)out * rp, 2), *ha = (uint16_t *)calloc((size_t)cols * rp, 2);
+    int *map = (int *)malloc((size_t)out * sizeof(int));
+    uint16_t *db = NULL, *da = NULL;
+    float *dw = NULL;
+    int *dmap = NULL, rc = -1;
+    if (!hb || !ha || !map) goto out;
+    for (int o = 0; o < out; o++)
+        for (int k = 0; k < r; k++) hb[(size_t)o * rp + k] = iris_f32_to_bf16(ad->lora_B[(size_t)o * r + k]);
+    for (int i = 0; i < cols; i++)
+        for (int k = 0; k < r; k++) ha[(size_t)i * rp + k] = iris_f32_to_bf16(ad->lora_A[(size_t)k * cols + i]);
+    for (int o = 0; o < out; o++) {
+        int m = row0 + o;
+        if (il_len > 0 && o >= il_from) {
+            const int q = o - il_from, up = q >= il_len, g = (up ? q - il_len : q);
+            m = row0 + il_from + (g / SWIGLU_GROUP) * 2 * SWIGLU_GROUP + up * SWIGLU_GROUP + g % SWIGLU_GROUP;
+        }
+        if (m < 0 || (size_t)m >= total_rows) { fprintf(stderr, "iris_hip: LoRA adapter rows out of range\n"); goto out; }
+        map[o] = m;
+    }
+    db = (uint16_t *)iris_hip_malloc((size_t)out * rp * 2);
+    da = (uint16_t *)iris_hip_malloc((size_t)cols * rp * 2);
+    dw = (float *)iris_hip_malloc((size_t)out * cols * 4);
+    dmap = (int *)iris_hip_malloc((size_t)out * sizeof(int));
+    if (!db || !da || !dw || !dmap || lora_backup(tf, W, total_rows * (size_t)cols * 2) ||
+        iris_hip_memcpy_h2d(db, hb, (size_t)out * rp * 2) || iris_hip_memcpy_h2d(da, ha, (size_t)cols * rp * 2) ||
+        iris_hip_memcpy_h2d(dmap, map, (size_t)out * sizeof(int)))
+        goto out;
+    {
+        iris_gemm_problem_t p = {db, da, dw, NULL, out, cols, rp, rp, rp, cols, IRIS_EPI_F32};
+        if (iris_hip_gemm(&p, 1) || iris_hip_merge_rows(W, cols, dmap, dw, out, scale) || iris_hip_sync()) goto out;
+    }
+    rc = 0;
+out:
+    iris_hip_free(db);
+    iris_hip_free(da);
+    iris_hip_free(dw);
+    iris_hip_free(dmap);
+    free(hb);
+    free(ha);
+    free(map);
+    return rc;
+}
+
+/* make the resident weights match tf->lora (restore, then merge the new one) */
+static int lora_sync(iris_transformer_t *tf) {
+    if (!tf->lora_dirty && tf->lora == tf->lora_merged) return 0;
+    tf->lora_dirty = 0;
+    if (lora_restore(tf)) return -1;
+    const lora_state_t *L = (const lora_state_t *)tf->lora;
+    if (!L || L->scale == 0.0f) {
+        tf->lora_merged = tf->lora;
+        return 0;
+    }
+    const int h = tf->hidden, mlp = tf->mlp;
+    const float sc = L->scale;
+    for (int i = 0; i < tf->n_double && i < L->num_double_blocks; i++) {
+        dev_double_t *b = &tf->dbl[i];
+        const lora_adapter_t *iq = L->double_img_q ? &L->double_img_q[i] : NULL;
+        const lora_adapter_t *ik = L->double_img_k ? &L->double_img_k[i] : NULL;
+        const lora_adapter_t *iv = L->double_img_v ? &L->double_img_v[i] : NULL;
+        const lora_adapter_t *ip = L->double_img_proj ? &L->double_img_proj[i] : NULL;
+        const lora_adapter_t *tq = L->double_txt_q ? &L->double_txt_q[i] : NULL;
+        const lora_adapter_t *tk = L->double_txt_k ? &L->double_txt_k[i] : NULL;
+        const lora_adapter_t *tv = L->double_txt_v ? &L->double_txt_v[i] : NULL;
+        const lora_adapter_t *tp = L->double_txt_proj ? &L->double_txt_proj[i] : NULL;
+        if (lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, iq, sc, 0, 0, 0) ||
+            lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, ik, sc, h, 0, 0) ||
+            lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, iv, sc, 2 * h, 0, 0) ||
+            lora_merge(tf, b->img_o, h, h, ip, sc, 0, 0, 0) ||
+            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tq, sc, 0, 0, 0) ||
+            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tk, sc, h, 0, 0) ||
+            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tv, sc, 2 * h, 0, 0) ||
+            lora_merge(tf, b->txt_o, h, h, tp, sc, 0, 0, 0))
+            goto fail;
+    }
+    for (int i = 0; i < tf->n_single && i < L->num_single_blocks; i++) {
+        dev_single_t *b = &tf->sgl[i];
+        const lora_adapter_t *l1 = L->single_linear1 ? &L->single_linear1[i] : NULL;
+        const lora_adapter_t *l2 = L->single_linear2 ? &L->single_linear2[i] : NULL;
+        if (lora_merge(tf, b->qkv_mlp, 3 * (size_t)h + 2 * (size_t)mlp, h, l1, sc, 0, 3 * h, mlp) ||
+            lora_merge(tf, b->out, h, h + mlp, l2, sc, 0, 0, 0))
+            goto fail;
+    }
+    tf->lora_merged = tf->lora;
+    return 0;
+fail:
+    lora_restore(tf);
+    return -1;
+}
+
 /* The reference's adapter setters (iris_transformer_flux.c:5131-5201), kept
  * so a caller links unchanged. The HIP forward implements none of the
  * adapters other than SREF: while one is attached (LoRA, CSD style delta,
@@ -845,7 +1015,7 @@ static void release_adapters(iris_transformer_t *tf) {
 }
 
 static int adapter_active(const iris_transformer_t *tf) {
-    const char *what = tf->lora ? "LoRA" : tf->ip ? "IP-Adapter"
+    const char *what = tf->ip ? "IP-Adapter"
                      : (tf->csd_delta && !tf->csd_skip) ? "CSD style delta" : NULL;
     if (what) fprintf(stderr, "iris_hip: %s is attached; the HIP denoiser does not apply adapters\n", what);
     return what != NULL;
@@ -855,6 +1025,7 @@ void iris_transformer_set_lora(iris_transformer_t *tf, void *lora) {
     if (!tf) return;
     if (tf->lora && tf->lora != lora && lora_free) lora_free(tf->lora);
     tf->lora = lora;
+    tf->lora_dirty = 1;   /* merged at the next forward (a freed state's address may come back) */
 }
 
 void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta) {

@@ -102,6 +102,12 @@ def flux_goldens(r, d, res):
     p = r.iris_transformer_forward_with_multi_refs(tf, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(temb_txt), T, f(0.6))
     res["flux_fwd_refs_sref_bands"] = tl.take_f32(r, p, 128 * 64)
     r.iris_transformer_set_sref_bands(tf, 1.0, 1.0)
+    # LoRA on every adapted linear (lora_apply at the reference's call sites)
+    r.iris_transformer_set_lora.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    r.iris_transformer_set_lora(tf, tl.make_lora(cfg, seed=5, std=0.2))
+    p = r.iris_transformer_forward(tf, tl.fptr(lat), 8, 8, tl.fptr(temb_txt), T, f(0.8))
+    res["flux_fwd_lora"] = tl.take_f32(r, p, 128 * 64)
+    r.iris_transformer_set_lora(tf, None)
     # 2-step Euler sample from the reference's own noise and schedule
     sched = r.iris_official_schedule(2, 64)
     sched_arr = np.ctypeslib.as_array(ctypes.cast(sched, tl.FP), shape=(3,)).copy()

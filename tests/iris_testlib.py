@@ -630,3 +630,58 @@ def write_vae_file(path, z=32, flux=True, seed=0, bf16=False, encoder=False):
         a = a.astype(np.float32).reshape(shape)
         out.append((name, to_bf16(a) if bf16 else a))
     write_safetensors(path, out)
+
+
+class LoraAdapter(ctypes.Structure):
+    """lora_adapter_t (reference iris_lora.h:22-28)"""
+    _fields_ = [("lora_A", FP), ("lora_B", FP), ("rank", ctypes.c_int), ("in_dim", ctypes.c_int),
+                ("out_dim", ctypes.c_int)]
+
+
+class LoraState(ctypes.Structure):
+    """lora_state_t (reference iris_lora.h:30-51)"""
+    _fields_ = ([("scale", ctypes.c_float), ("num_double_blocks", ctypes.c_int)] +
+                [(n, ctypes.POINTER(LoraAdapter)) for n in ("double_img_q", "double_img_k", "double_img_v",
+                                                            "double_img_proj", "double_txt_q", "double_txt_k",
+                                                            "double_txt_v", "double_txt_proj")] +
+                [("num_single_blocks", ctypes.c_int), ("single_linear1", ctypes.POINTER(LoraAdapter)),
+                 ("single_linear2", ctypes.POINTER(LoraAdapter)), ("scratch", FP), ("scratch_len", ctypes.c_int),
+                 ("max_rank", ctypes.c_int)])
+
+
+def make_lora(cfg, seed, rank=8, scale=1.0, std=0.05, max_seq=4096):
+    """A LoRA state for a Flux-shaped model with every adapter filled from the
+    seeded generator, all memory from the C allocator (the reference's
+    lora_free releases it)."""
+    libc = ctypes.CDLL(None)
+    libc.malloc.restype = ctypes.c_void_p
+    libc.malloc.argtypes = [ctypes.c_size_t]
+    h = cfg["heads"] * 128
+    mlp = int(h * cfg.get("mlp_ratio", 3.0))
+
+    def carr(a):
+        a = np.ascontiguousarray(a, np.float32)
+        p = libc.malloc(a.nbytes)
+        ctypes.memmove(p, a.ctypes.data, a.nbytes)
+        return ctypes.cast(p, FP)
+
+    def adapters(n, in_dim, out_dim, tag):
+        p = ctypes.cast(libc.malloc(n * ctypes.sizeof(LoraAdapter)), ctypes.POINTER(LoraAdapter))
+        for i in range(n):
+            s = seed * 1000 + tag * 50 + i
+            p[i] = LoraAdapter(carr(synth_f32((rank, in_dim), 2 * s, 0.0, std)),
+                               carr(synth_f32((out_dim, rank), 2 * s + 1, 0.0, std)), rank, in_dim, out_dim)
+        return p
+
+    st = ctypes.cast(libc.malloc(ctypes.sizeof(LoraState)), ctypes.POINTER(LoraState))
+    nd, ns = cfg["n_double"], cfg["n_single"]
+    f = st.contents
+    f.scale, f.num_double_blocks, f.num_single_blocks = scale, nd, ns
+    for k, name in enumerate(("double_img_q", "double_img_k", "double_img_v", "double_img_proj",
+                              "double_txt_q", "double_txt_k", "double_txt_v", "double_txt_proj")):
+        setattr(f, name, adapters(nd, h, h, k))
+    f.single_linear1 = adapters(ns, h, 3 * h + 2 * mlp, 8)
+    f.single_linear2 = adapters(ns, h + mlp, h, 9)
+    f.scratch = ctypes.cast(libc.malloc(rank * max_seq * 4), FP)
+    f.scratch_len, f.max_rank = max_seq, rank
+    return st

@@ -433,8 +433,33 @@ def test_sref_strength(lib, tiny):
     assert tl.rel_l2(weak, plain) < 0.2 * tl.rel_l2(base, plain)
 
 
+def test_lora_vs_reference(lib, tiny):
+    """LoRA on every adapted linear of the reference (double-block img/txt
+    q, k, v, proj; single-block linear1 incl. the SwiGLU rows, linear2),
+    merged into the resident weights, against the reference's forward that
+    applies scale * B (A x) at run time (golden flux_fwd_lora from
+    oracle/_ref; the LoRA moves the velocity by 28 %); removing the LoRA
+    restores the weights bit for bit."""
+    lib.iris_transformer_set_lora.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+
+    def fwd():
+        return take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+
+    base = fwd()
+    lib.iris_transformer_set_lora(tiny, tl.make_lora(TINY, seed=5, std=0.2))
+    got = fwd()
+    lib.iris_transformer_set_lora(tiny, None)
+    again = fwd()
+    ref = G["flux_fwd_lora"]
+    print(f"lora: rel_l2 {tl.rel_l2(got, ref):.3e} cosine {tl.cosine(got, ref):.6f}")
+    assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+    assert np.array_equal(again, base)
+
+
 def test_adapters_fail_loudly(lib, tiny):
-    """Adapter setters link and take ownership; an attached adapter makes the
+    """Adapter setters link and take ownership; an attached adapter the HIP
+    forward does not apply (CSD delta, IP-Adapter) makes the
     forward fail (the HIP denoiser applies none) instead of being ignored."""
     vp = ctypes.c_void_p
     libc = ctypes.CDLL(None)
