@@ -66,6 +66,10 @@ int iris_transformer_text_dim(iris_transformer_t *tf);
 void iris_transformer_set_lora(iris_transformer_t *tf, void *lora);
 void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta);
 void iris_transformer_set_csd_skip(iris_transformer_t *tf, int skip);
+/* No counterpart in the reference: whether a CSD style delta is attached (the
+ * CFG sampler then runs the two branches as separate forwards so the delta
+ * reaches the conditional one only, as the reference's style-CFG). */
+int iris_transformer_csd_active(iris_transformer_t *tf);
 void iris_transformer_set_sref_bands(iris_transformer_t *tf, float shf, float slf);
 void iris_transformer_set_sref_strength(iris_transformer_t *tf, float gamma);
 int iris_transformer_set_ip_adapter(iris_transformer_t *tf, void *ip, float *ip_embeds);

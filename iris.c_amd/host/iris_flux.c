@@ -87,6 +87,7 @@ typedef struct {
     float *krope_cos, *krope_sin; /* [S][128] K side: the reference rows' H/W bands scaled (SREF) */
     float kshf, kslf;             /* band scales the K tables hold */
     float kgamma;                 /* SREF strength the captured graph applies */
+    int csd_on;                   /* the captured graph adds the CSD style delta to temb */
     float *tsin;             /* [256] */
     float *tmp, *temb;       /* [h] */
     float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
@@ -105,6 +106,7 @@ struct iris_transformer {
     void *lora, *ip, *ip_embeds;
     void *lora_merged;                /* the LoRA state merged into the weights, or NULL */
     int lora_dirty;                   /* set_lora was called since the last merge */
+    float *d_csd;                     /* device copy of the CSD style delta [hidden] */
     lora_backup_t *lora_bk;
     int n_lora_bk, cap_lora_bk;
     float *csd_delta;
@@ -330,6 +332,7 @@ void iris_transformer_free(iris_transformer_t *tf) {
     work_free(&tf->w);
     for (int i = 0; i < tf->n_lora_bk; i++) iris_hip_free(tf->lora_bk[i].orig);
     free(tf->lora_bk);
+    iris_hip_free(tf->d_csd);
     iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
     iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
     iris_hip_free(tf->final_mod); iris_hip_free(tf->proj_out);
@@ -477,6 +480,8 @@ static int capture(iris_transformer_t *tf) {
     work_t *w = &tf->w;
     if (w->graph) { iris_hip_graph_destroy(w->graph); w->graph = NULL; }
     w->kgamma = tf->sref_strength;
+    w->csd_on = tf->csd_delta && !tf->csd_skip;
+    if (w->csd_on && !tf->d_csd && !(tf->d_csd = (float *)iris_hip_malloc((size_t)tf->hidden * 4))) return -1;
     if (iris_hip_graph_begin()) return -1;
     if (enqueue_forward(tf)) {
         void *g = iris_hip_graph_end();
@@ -706,7 +711,9 @@ static int enqueue_forward(iris_transformer_t *tf) {
      * :3787-3797, :4270-4277); the single-block modulation is the same for all
      * 20 blocks and is computed once */
     CK(iris_hip_gemv(w->tmp, tf->t_fc1, w->tsin, NULL, h, 256, 0));
-    CK(iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, NULL, h, h, 1));
+    /* the CSD style delta is added to temb before its SiLU (iris_transformer_flux.c:3969-3972):
+     * the bias of the second time-MLP linear */
+    CK(iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, w->csd_on ? tf->d_csd : NULL, h, h, 1));
     CK(iris_hip_gemv(w->mod, tf->mod_dimg, w->temb, NULL, 6 * h, h, 1));
     CK(iris_hip_gemv(w->mod + 6 * h, tf->mod_dtxt, w->temb, NULL, 6 * h, h, 1));
     CK(iris_hip_gemv(w->mod + 12 * h, tf->mod_single, w->temb, NULL, 3 * h, h, 1));
@@ -798,7 +805,10 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
         free(s);
         if (rc) return -1;
     }
-    if (w->kgamma != tf->sref_strength && capture(tf)) return -1;
+    const int csd_on = tf->csd_delta && !tf->csd_skip;
+    if ((w->kgamma != tf->sref_strength || w->csd_on != csd_on) && capture(tf)) return -1;
+    if (csd_on && (iris_hip_memcpy_h2d(tf->d_csd, tf->csd_delta, (size_t)tf->hidden * 4) || iris_hip_sync()))
+        return -1;
     /* get_timestep_embedding(t * 1000), :3967 */
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
@@ -1015,8 +1025,7 @@ static void release_adapters(iris_transformer_t *tf) {
 }
 
 static int adapter_active(const iris_transformer_t *tf) {
-    const char *what = tf->ip ? "IP-Adapter"
-                     : (tf->csd_delta && !tf->csd_skip) ? "CSD style delta" : NULL;
+    const char *what = tf->ip ? "IP-Adapter" : NULL;
     if (what) fprintf(stderr, "iris_hip: %s is attached; the HIP denoiser does not apply adapters\n", what);
     return what != NULL;
 }
@@ -1037,6 +1046,8 @@ void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta) {
 void iris_transformer_set_csd_skip(iris_transformer_t *tf, int skip) {
     if (tf) tf->csd_skip = skip;
 }
+
+int iris_transformer_csd_active(iris_transformer_t *tf) { return tf && tf->csd_delta != NULL; }
 
 void iris_transformer_set_sref_bands(iris_transformer_t *tf, float shf, float slf) {
     if (!tf) return;

@@ -161,7 +161,7 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
                              void (*progress_callback)(int, int)) {
     (void)text_encoder; (void)batch;
     iris_transformer_t *tf = (iris_transformer_t *)transformer;
-    if (text_seq_cond == text_seq_uncond) {
+    if (text_seq_cond == text_seq_uncond && !iris_transformer_csd_active(tf)) {
         /* one batch-2 pass per step: slot 0 = uncond, slot 1 = cond */
         size_t tsz = (size_t)text_seq_cond * iris_transformer_text_dim(tf);
         float *both = (float *)malloc(2 * tsz * sizeof(float));
@@ -173,8 +173,10 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
         free(both);
         return r;
     }
-    /* different text lengths: two sequential forwards per step, as the
-     * reference; the guided Euler update runs on the device */
+    /* different text lengths, or a CSD style delta (applied to the
+     * conditional forward only, iris_sample.c:750-760): two sequential
+     * forwards per step, as the reference; the guided Euler update runs on
+     * the device */
     size_t n = (size_t)channels * h * w;
     float *zc = (float *)malloc(n * sizeof(float));
     float *dz = (float *)iris_hip_malloc(3 * n * sizeof(float));
@@ -188,7 +190,9 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
     for (int i = 0; ok && i < num_steps; i++) {
         if (iris_step_callback) iris_step_callback(i + 1, num_steps);
         if (iris_cancel_requested || iris_hip_memcpy_d2h(zc, dz, n * sizeof(float))) { ok = 0; break; }
+        iris_transformer_set_csd_skip(tf, 1);
         float *vu = iris_transformer_forward(tf, zc, h, w, text_emb_uncond, text_seq_uncond, schedule[i]);
+        iris_transformer_set_csd_skip(tf, 0);
         float *vc = vu ? iris_transformer_forward(tf, zc, h, w, text_emb_cond, text_seq_cond, schedule[i]) : NULL;
         ok = vu && vc && !iris_hip_memcpy_h2d(dvu, vu, n * sizeof(float)) &&
              !iris_hip_memcpy_h2d(dvc, vc, n * sizeof(float)) &&

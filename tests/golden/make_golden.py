@@ -108,6 +108,12 @@ def flux_goldens(r, d, res):
     p = r.iris_transformer_forward(tf, tl.fptr(lat), 8, 8, tl.fptr(temb_txt), T, f(0.8))
     res["flux_fwd_lora"] = tl.take_f32(r, p, 128 * 64)
     r.iris_transformer_set_lora(tf, None)
+    # CSD style delta on the time embedding (iris_transformer_set_csd_delta)
+    r.iris_transformer_set_csd_delta.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    r.iris_transformer_set_csd_delta(tf, tl.c_floats(tl.synth_f32((256,), 61, 0.0, 0.5)))
+    p = r.iris_transformer_forward(tf, tl.fptr(lat), 8, 8, tl.fptr(temb_txt), T, f(0.8))
+    res["flux_fwd_csd"] = tl.take_f32(r, p, 128 * 64)
+    r.iris_transformer_set_csd_delta(tf, None)
     # 2-step Euler sample from the reference's own noise and schedule
     sched = r.iris_official_schedule(2, 64)
     sched_arr = np.ctypeslib.as_array(ctypes.cast(sched, tl.FP), shape=(3,)).copy()

@@ -685,3 +685,15 @@ def make_lora(cfg, seed, rank=8, scale=1.0, std=0.05, max_seq=4096):
     f.scratch = ctypes.cast(libc.malloc(rank * max_seq * 4), FP)
     f.scratch_len, f.max_rank = max_seq, rank
     return st
+
+
+def c_floats(a):
+    """A copy of a float32 array in memory from the C allocator (for setters
+    that take ownership and release it with free())."""
+    libc = ctypes.CDLL(None)
+    libc.malloc.restype = ctypes.c_void_p
+    libc.malloc.argtypes = [ctypes.c_size_t]
+    a = np.ascontiguousarray(a, np.float32)
+    p = libc.malloc(a.nbytes)
+    ctypes.memmove(p, a.ctypes.data, a.nbytes)
+    return p

@@ -457,22 +457,42 @@ def test_lora_vs_reference(lib, tiny):
     assert np.array_equal(again, base)
 
 
-def test_adapters_fail_loudly(lib, tiny):
-    """Adapter setters link and take ownership; an attached adapter the HIP
-    forward does not apply (CSD delta, IP-Adapter) makes the
-    forward fail (the HIP denoiser applies none) instead of being ignored."""
-    vp = ctypes.c_void_p
-    libc = ctypes.CDLL(None)
-    libc.malloc.restype = vp
-    lib.iris_transformer_set_csd_delta.argtypes = [vp, vp]
-    lib.iris_transformer_set_sref_strength.argtypes = [vp, ctypes.c_float]
-    lib.iris_transformer_set_sref_bands.argtypes = [vp, ctypes.c_float, ctypes.c_float]
+def test_csd_delta_vs_reference(lib, tiny):
+    """CSD style delta added to the time embedding before its SiLU
+    (iris_transformer_flux.c:3969-3972), against the reference's forward
+    (golden flux_fwd_csd from oracle/_ref; the delta moves the velocity by
+    14 %); csd_skip and removal restore the plain forward bit for bit."""
+    lib.iris_transformer_set_csd_delta.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.iris_transformer_set_csd_skip.argtypes = [ctypes.c_void_p, ctypes.c_int]
     lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
-    lib.iris_transformer_set_sref_strength(tiny, 1.0)          # off
-    lib.iris_transformer_set_sref_bands(tiny, 1.0, 1.0)        # off
-    base = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
-    lib.iris_transformer_set_csd_delta(tiny, libc.malloc(256 * 4))
-    assert not lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8))
+
+    def fwd():
+        return take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+
+    base = fwd()
+    lib.iris_transformer_set_csd_delta(tiny, tl.c_floats(tl.synth_f32((256,), 61, 0.0, 0.5)))
+    got = fwd()
+    lib.iris_transformer_set_csd_skip(tiny, 1)
+    skipped = fwd()
+    lib.iris_transformer_set_csd_skip(tiny, 0)
     lib.iris_transformer_set_csd_delta(tiny, None)
+    again = fwd()
+    ref = G["flux_fwd_csd"]
+    print(f"csd: rel_l2 {tl.rel_l2(got, ref):.3e} cosine {tl.cosine(got, ref):.6f}")
+    assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+    assert np.array_equal(skipped, base) and np.array_equal(again, base)
+
+
+def test_ip_adapter_fails_loudly(lib, tiny):
+    """The IP-Adapter is the one adapter the HIP forward does not apply: while
+    one is attached the forward fails with a message instead of ignoring it."""
+    vp = ctypes.c_void_p
+    lib.iris_transformer_set_ip_adapter.argtypes = [vp, vp, vp]
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    base = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
+    dummy = ctypes.c_char_p(b"ip-adapter state")
+    lib.iris_transformer_set_ip_adapter(tiny, ctypes.cast(dummy, vp), None)
+    assert not lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8))
+    lib.iris_transformer_set_ip_adapter(tiny, None, None)
     again = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(lat), 8, 8, tl.fptr(txt), 32, F(0.8)), 8192)
     np.testing.assert_array_equal(base, again)
