@@ -21,9 +21,15 @@ extern "C" {
 
 extern volatile int iris_cancel_requested;
 
-float *iris_linear_schedule(int num_steps);
-float *iris_official_schedule(int num_steps, int image_seq_len);
-float *iris_zimage_schedule(int num_steps, int image_seq_len);   /* shift 3 or IRIS_ZIMAGE_SHIFT */
+/* Schedules of num_steps + 1 values from 1 to 0 (iris_sample.c:61-244), with
+ * the bits of the reference's -O3 -march=native -ffast-math build on the same
+ * host (its vectorized lanes use the CPU's reciprocal estimate). */
+float *iris_linear_schedule(int num_steps);                       /* :61-68 */
+float *iris_power_schedule(int num_steps, float alpha);           /* :75-84 */
+float *iris_sigmoid_schedule(int num_steps, float shift);         /* :90-107 */
+float *iris_resolution_schedule(int num_steps, int height, int width);   /* :113-136 */
+float *iris_official_schedule(int num_steps, int image_seq_len);  /* :160-182 */
+float *iris_zimage_schedule(int num_steps, int image_seq_len);    /* :216-244; shift 3 or IRIS_ZIMAGE_SHIFT */
 float *iris_init_noise(int batch, int channels, int h, int w, int64_t seed);
 void iris_rng_seed(uint64_t seed);
 float iris_random_uniform(void);

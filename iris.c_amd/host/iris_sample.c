@@ -1,8 +1,9 @@
 /*
- * iris_sample.c - schedules, seeded noise and Euler samplers (host C).
+ * iris_sample.c - seeded noise and Euler samplers (host C).
  *
- * Schedules and noise follow iris_sample.c:61-244, :1146-1188 and the
- * xoshiro256** RNG of iris_kernels.c:50-107 (same seeds give the same noise).
+ * Noise follows iris_sample.c:1146-1188 and the xoshiro256** RNG of
+ * iris_kernels.c:50-107 (same seeds give the same noise); the schedules are
+ * in iris_schedule.c.
  * The Euler loops (iris_sample.c:313-405, :412-536, :630-702, :717-802) keep
  * the latent resident on the device: one upload, one graph replay and one
  * update kernel per step, one download at the end.
@@ -17,52 +18,6 @@
 #include <string.h>
 
 volatile int iris_cancel_requested = 0;
-
-float *iris_linear_schedule(int n) {
-    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
-    if (!s) return NULL;
-    for (int i = 0; i <= n; i++) s[i] = 1.0f - (float)i / (float)n;
-    return s;
-}
-
-/* compute_empirical_mu, iris_sample.c:144-158 */
-static float empirical_mu(int seq, int n) {
-    const float a1 = 8.73809524e-05f, b1 = 1.89833333f, a2 = 0.00016927f, b2 = 0.45666666f;
-    if (seq > 4300) return a2 * seq + b2;
-    float m200 = a2 * seq + b2, m10 = a1 * seq + b1;
-    float a = (m200 - m10) / 190.0f;
-    return a * n + (m200 - 200.0f * a);
-}
-
-/* iris_official_schedule with generalized_time_snr_shift(sigma = 1), :160-182 */
-float *iris_official_schedule(int n, int seq) {
-    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
-    if (!s) return NULL;
-    float mu = empirical_mu(seq, n);
-    for (int i = 0; i <= n; i++) {
-        float t = 1.0f - (float)i / (float)n;
-        s[i] = t <= 0.0f ? 0.0f : t >= 1.0f ? 1.0f : expf(mu) / (expf(mu) + powf(1.0f / t - 1.0f, 1.0f));
-    }
-    return s;
-}
-
-/* iris_zimage_schedule, :216-244 */
-float *iris_zimage_schedule(int n, int seq) {
-    (void)seq;
-    float *s = (float *)malloc((size_t)(n + 1) * sizeof(float));
-    if (!s) return NULL;
-    float shift = 3.0f;
-    const char *e = getenv("IRIS_ZIMAGE_SHIFT");
-    if (e && atof(e) > 0.0) shift = (float)atof(e);
-    const float smin = shift * (1.0f / 1000.0f) / (1.0f + (shift - 1.0f) * (1.0f / 1000.0f));
-    for (int i = 0; i < n; i++) {
-        float u = n > 1 ? (float)i / (float)(n - 1) : 0.0f;
-        float raw = 1.0f + (smin - 1.0f) * u;
-        s[i] = shift * raw / (1.0f + (shift - 1.0f) * raw);
-    }
-    s[n] = 0.0f;
-    return s;
-}
 
 /* xoshiro256** seeded with SplitMix64; Box-Muller normals */
 static uint64_t rng[4] = {0x853c49e6748fea9bULL, 0xda3e39cb94b95bdbULL, 0x647c4677a2884327ULL,
