@@ -86,6 +86,27 @@ def zimage_flops(c):
             + 2 * I * 64 * d + 2 * T * c["cap_dim"] * d + 2 * I * d * 64)
 
 
+def host_cpu():
+    """(threads, description) of the host cores the CPU baseline runs on: the
+    `model name` of /proc/cpuinfo, the online CPU count (nproc) and the
+    threads used. One GPU of this machine is allotted 16 host cores, so the
+    baseline uses min(the cores this process may run on, 16), or
+    IRIS_ORACLE_THREADS when set."""
+    model = "unknown CPU"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    online = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else online
+    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(avail, 16)))
+    return threads, (f"{model}, nproc {online}, {avail} available to the process, {threads} threads "
+                     f"(the 16-core host share of one GPU)")
+
+
 def time_launches(lib, fn, n=30, warm=3):
     """Average duration of one launch over n back-to-back launches, HIP events on the library stream."""
     for _ in range(warm):
@@ -146,10 +167,15 @@ def run_flux(lib, c, args):
                     P(dbuf["a"], wdev.ptr + 3 * h * h * 2, dbuf["cat"] + h * 2, None, BS, 2 * mlp, h, h, h,
                       h + mlp, 3))
     g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(probs, 2))
-    at = tl.AttnArgs(dbuf["q"], dbuf["k"], dbuf["vt"], dbuf["cat"], h, h, S_pad, h + mlp, S, S, H, B, S * h, S * h,
-                     H * 128 * S_pad, S * (h + mlp), 1.0 / np.sqrt(128.0), 0, S, 0, 0)
+    # the joint attention as the step runs it: Q normalised and rotated in the prologue
+    wq = tl.Dev.of(np.ones(128, np.float32))
+    rc, rs = (lib.iris_flux_device_buffer(tf, n) for n in (b"rope_pair_cos", b"rope_pair_sin"))
+    at = tl.AttnArgs(dbuf["qkv"], dbuf["k"], dbuf["vt"], dbuf["cat"], 3 * h, h, S_pad, h + mlp, S, S, H, B,
+                     S * 3 * h, S * h, H * 128 * S_pad, S * (h + mlp), 1.0 / np.sqrt(128.0), 0, S, 0, 0, 0, 0, 0,
+                     0.0, wq.ptr, wq.ptr, S, 1e-6, rc, rs)
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
     wdev.close()
+    wq.close()
     kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_ms,
                             2.0 * BS * h * (3 * h + 2 * mlp), c["ns"], f"gemm_fused_{args.config}"),
                kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_ms, 4.0 * B * S * S * h,
@@ -258,11 +284,16 @@ def probe(kind, n):
         fn = lambda: lib.iris_hip_gemm(probs, 2)  # noqa: E731
         alg = 2 * S * h + 2 * (3 * h + 2 * mlp) * h + 2 * S * (3 * h + mlp)
     elif kind == "attn":
-        q, k = dev(S * h * 2, 11), dev(S * h * 2, 12)
+        q, k = dev(S * 3 * h * 2, 11), dev(S * h * 2, 12)
         vt, o = dev(H * 128 * S_pad * 2, 13), dev(S * (h + mlp) * 2)
-        at = tl.AttnArgs(q, k, vt, o, h, h, S_pad, h + mlp, S, S, H, 1, 0, 0, 0, 0, 1.0 / np.sqrt(128.0), 0, S, 0, 0)
+        wq = tl.Dev.of(np.ones(128, np.float32))
+        ang = np.random.default_rng(5).uniform(-3, 3, (S, 64))
+        rc, rs = (tl.Dev.of(f(ang).astype(np.float32)) for f in (np.cos, np.sin))
+        bufs.extend([wq, rc, rs])
+        at = tl.AttnArgs(q, k, vt, o, 3 * h, h, S_pad, h + mlp, S, S, H, 1, 0, 0, 0, 0, 1.0 / np.sqrt(128.0), 0, S,
+                         0, 0, 0, 0, 0, 0.0, wq.ptr, wq.ptr, S, 1e-6, rc.ptr, rs.ptr)
         fn = lambda: lib.iris_hip_attention(ctypes.byref(at))  # noqa: E731
-        alg = 2 * 4 * S * h
+        alg = 2 * 4 * S * h + 2 * 64 * 4 * S
     else:
         nb = 1 << 30
         src, dst = dev(nb), dev(nb)
@@ -339,7 +370,7 @@ def run_qwen3(lib, c, args):
 def cpu_baseline_qwen3(c):
     """Oracle on the host cores: one layer at 512 tokens, extrapolated to 27."""
     orc = tl.oracle()
-    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+    threads, host = host_cpu()
     tl.bind_blas(orc, threads)
     m = ctypes.c_void_p(orc.orc_qwen3_create_synth(c["h"], c["inter"], c["H"], c["KV"], 2, 4096, 20250101))
     S = c["seq"]
@@ -352,8 +383,8 @@ def cpu_baseline_qwen3(c):
     ms = t1 * 27 * 1000
     return {"value": round(1000.0 / ms, 6), "unit": "encodes/s", "cores": threads, "kind": "port",
             "ms_per_step": round(ms, 1),
-            "sample": f"oracle (C restatement of the reference qwen3_forward, {orc.orc_blas_info().decode()}): "
-                      f"1 layer {t1:.2f} s at 512 tokens, hidden {c['h']}, extrapolated x27"}
+            "sample": f"oracle (C restatement of the reference qwen3_forward, {orc.orc_blas_info().decode()}) on "
+                      f"{host}: 1 layer {t1:.2f} s at 512 tokens, hidden {c['h']}, extrapolated x27"}
 
 
 def vae_flops(c):
@@ -417,7 +448,7 @@ def cpu_baseline_vae(c):
     """Oracle decode of a 256x256 image (16x16 latent) on the host cores,
     scaled to 1024x1024 by the ratio of algorithmic FLOPs."""
     orc = tl.oracle()
-    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+    threads, host = host_cpu()
     tl.bind_blas(orc, threads)
     os.environ.setdefault("OMP_NUM_THREADS", str(threads))
     v = ctypes.c_void_p(orc.orc_vae_create_synth(c["z"], 0.0, 0.0, 20250101))
@@ -432,7 +463,7 @@ def cpu_baseline_vae(c):
     ms = t1 * scale * 1000
     return {"value": round(1000.0 / ms, 6), "unit": "images/s", "cores": threads, "kind": "port",
             "ms_per_step": round(ms, 1),
-            "sample": f"oracle (C restatement of the reference iris_vae_decode, OpenMP): 256x256 decode "
+            "sample": f"oracle (C restatement of the reference iris_vae_decode, OpenMP) on {host}: 256x256 decode "
                       f"{t1:.2f} s, scaled x{scale:.2f} by algorithmic FLOPs to 1024x1024"}
 
 
@@ -498,10 +529,10 @@ def cpu_baseline(c):
     one block of each kind at the benchmark's shape, timed once each,
     extrapolated to one step."""
     orc = tl.oracle()
-    threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(os.cpu_count() or 1, 16)))
+    threads, host = host_cpu()
     tl.bind_blas(orc, threads)
     if c["kind"] == "zimage":
-        return cpu_baseline_zimage(orc, c, threads)
+        return cpu_baseline_zimage(orc, c, threads, host)
     h, T, I0 = c["h"], c["T"], c["ih"] * c["iw"]
     I = I0 + sum(a * b for a, b, _ in c["refs"])
     m = ctypes.c_void_p(orc.orc_flux_create_synth(h, c["H"], 1, 1, c["td"], 128, 3.0, 2000.0, 20250101))
@@ -525,11 +556,11 @@ def cpu_baseline(c):
     return {"value": round(1000.0 / (ms_step * c["steps"]), 6), "unit": "images/s", "cores": threads,
             "kind": "port", "ms_per_step": round(ms_step, 1),
             "sample": f"oracle (C restatement of the reference make-blas path, "
-                      f"{orc.orc_blas_info().decode()}): 1 double block {t_d:.2f} s + 1 single block {t_s:.2f} s "
+                      f"{orc.orc_blas_info().decode()}) on {host}: 1 double block {t_d:.2f} s + 1 single block {t_s:.2f} s "
                       f"at S={T + I}, h={h}, extrapolated x{c['nd']} + x{c['ns']} per step"}
 
 
-def cpu_baseline_zimage(orc, c, threads):
+def cpu_baseline_zimage(orc, c, threads, host):
     d, T = c["d"], c["cap"]
     I = (c["lh"] // 2) * (c["lw"] // 2)
     S = I + T
@@ -556,7 +587,7 @@ def cpu_baseline_zimage(orc, c, threads):
     return {"value": round(1000.0 / (ms_step * c["steps"]), 6), "unit": "images/s", "cores": threads,
             "kind": "port", "ms_per_step": round(ms_step, 1),
             "sample": f"oracle (C restatement of the reference f32 path with sgemm attention, "
-                      f"{orc.orc_blas_info().decode()}): 1 main block {t_main:.2f} s at S={S}, d={d}, "
+                      f"{orc.orc_blas_info().decode()}) on {host}: 1 main block {t_main:.2f} s at S={S}, d={d}, "
                       f"extrapolated to {n_eq:.2f} block-equivalents per step"}
 
 

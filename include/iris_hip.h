@@ -200,6 +200,10 @@ typedef struct {
                                          iris_transformer_flux.c:1272-1321) */
 } iris_qkprep_args_t;
 int iris_hip_qk_prepare(const iris_qkprep_args_t *a);
+/* The K and V half of iris_hip_qk_prepare (q_out, wqA and wqB unused): K'
+ * and V^T in one pass, for attention calls that normalise and rotate Q in
+ * their own prologue (iris_attn_args_t.qn_wA). */
+int iris_hip_kv_prepare(const iris_qkprep_args_t *a);
 
 /* Flash attention over head_dim 128: O = softmax(Q K^T * scale) V per head.
  * Q [sq][ld_q], K [sk][ld_k] (head h at column h*128), Vt [h][128][ld_vt],
@@ -220,6 +224,17 @@ typedef struct {
     int bias_from;                    /* keys >= bias_from get key_bias added to their logits */
     float key_bias;                   /* (SREF strength: log gamma on the reference keys,
                                          iris_transformer_flux.c:1328-1338); 0: none */
+    /* Q prologue (apply_qk_norm + apply_rope_2d on Q, iris_transformer_flux.c:
+     * 1464-1518, :1026-1048): when qn_wA is set, q holds the raw projection and
+     * each (query, head) row is RMS-normalised (eps qn_eps) times qn_wA
+     * (queries < qn_split) or qn_wB, then its pairs (2i, 2i+1) are rotated by
+     * the per-pair tables rope_cos / rope_sin [sq][64] (entry i rotates dims
+     * 2i, 2i+1; NULL: no rotation), before the product. Causal masking and
+     * key_bias do not combine. */
+    const float *qn_wA, *qn_wB;
+    int qn_split;
+    float qn_eps;
+    const float *rope_cos, *rope_sin;
 } iris_attn_args_t;
 int iris_hip_attention(const iris_attn_args_t *a);
 

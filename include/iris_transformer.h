@@ -60,9 +60,9 @@ int iris_transformer_text_dim(iris_transformer_t *tf);
 
 /* Adapter setters of the reference (iris_transformer_flux.c:5131-5201; LoRA
  * state and IP-Adapter passed as opaque pointers, same ABI). Ownership passes
- * to the transformer as in the reference. The HIP forward applies no adapter:
- * while LoRA, IP-Adapter, an unskipped CSD delta, or SREF bands/strength other
- * than off are attached, every forward returns NULL with a message. */
+ * to the transformer as in the reference. The HIP forward applies LoRA, the
+ * CSD style delta and the SREF bands and strength; while an IP-Adapter is
+ * attached every forward returns NULL with a message. */
 void iris_transformer_set_lora(iris_transformer_t *tf, void *lora);
 void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta);
 void iris_transformer_set_csd_skip(iris_transformer_t *tf, int skip);
@@ -133,7 +133,17 @@ int zi_velocity(zi_transformer_t *tf, float timestep);
 /* Z-Image update: z += (sigma_next - sigma) * (-v), v at timestep 1 - sigma */
 int zi_step(zi_transformer_t *tf, float sigma, float sigma_next);
 int zi_download_latent(zi_transformer_t *tf, float *latent);
+/* Device buffers of the prepared geometry: "x" (unified [image (padded) |
+ * caption (padded)] residual stream, f32 [U][dim]), "t_emb" (adaLN input,
+ * [256]), "latent", "velocity", "rope_cos", "rope_sin", "patches", and the
+ * block scratch "a", "qkv", "cat" */
 void *zi_device_buffer(zi_transformer_t *tf, const char *name);
+/* One block on the resident stream, the reference's zi_block_forward
+ * (iris_transformer_zimage.c:790-870) as an entry point: kind 0 = noise
+ * refiner idx on the image rows, 1 = context refiner idx on the caption rows,
+ * 2 = main layer idx on the unified sequence, each with the forward's key
+ * masks; the modulated kinds take their modulation from the resident t_emb. */
+int zi_block_forward_resident(zi_transformer_t *tf, int kind, int idx);
 
 #ifdef __cplusplus
 }

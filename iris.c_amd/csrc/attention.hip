@@ -5,12 +5,12 @@
  * 1789-2022: per-head sgemm, iris_softmax_cpu, sgemm over a materialised
  * [heads, S, S] score buffer; the generic build's online-softmax variant
  * iris_kernels.c:737-1048; Z-Image's masked scalar loops
- * iris_transformer_zimage.c:689-761). Scores never leave registers.
+ * iris_transformer_zimage.c:689-761) and, in its prologue, the Q half of
+ * apply_qk_norm + apply_rope_2d (iris_transformer_flux.c:1464-1518,
+ * :1026-1048). Scores never leave registers.
  *
- * Block = 8 waves, 256 queries of one head (32 per wave), two waves per SIMD:
- * while one wave forms probabilities (VALU) the other's matrix products run.
- * A wave's Q fragments, scores, probabilities and output accumulators all fit
- * in its 256 registers. Keys stream through LDS in tiles of 64 (two stages):
+ * Block = 8 waves, 256 queries of one head (32 per wave). Per 64-key tile a
+ * wave runs
  *   S^T[key][q] = K Q^T          (K tile = MFMA A operand from LDS,
  *                                 Q = B operand held in registers)
  *   online softmax per query column in the log2 domain, f32: the scale and
@@ -19,17 +19,40 @@
  *                                 taken straight from the S^T accumulators)
  * Computing S transposed puts each query's probabilities in the B-operand
  * layout of the PV product, so P never goes through LDS. V arrives already
- * transposed ([head][d][key], written by iris_hip_qk_prepare).
+ * transposed ([head][d][key], written by iris_hip_kv_prepare).
  *
- * Grouped-query attention reads K / V head h / kv_group for query head h.
- * With causal set a block stops at the key tile of its last query and tiles
- * past a wave's first query are masked per element (key <= query).
+ * Wave groups in ping-pong: waves w and w + 4 share SIMD w, group 0 = waves
+ * 0..3, group 1 = waves 4..7. Phases are separated by block barriers; in
+ * every phase one group runs matrix products (M phase: PV of the previous
+ * tile, then QK of this tile: 32 MFMAs) while the other forms probabilities
+ * (V phase: masks, max, rescale, exp2, row sums: VALU), so each SIMD's
+ * matrix core and VALU work at the same time:
+ *   phase 2t:     group 0 M(t)      group 1 V(t-1)
+ *   phase 2t + 1: group 0 V(t)      group 1 M(t)
+ * Keys and values stream through two K and two V^T stages. In its M(t)
+ * phase each group stores its half of K(t+1) and V(t) from registers (loaded
+ * one phase pair earlier) and issues the loads of K(t+2) and V(t+1):
+ *   - K(t+1) goes to the K stage of K(t-1), read in phases 2t-2 and 2t-1,
+ *     and is read from phase 2t+2;
+ *   - V(t) goes to the V stage of V(t-2), read (PV of tile t-2) in phases
+ *     2t-2 and 2t-1, and is read from phase 2t+2.
+ * A barrier waits only for the wave's LDS operations, not for its global
+ * loads in flight.
+ *
+ * With a Q prologue (qn_wA set) each wave normalises its 32 raw query rows
+ * row by row (16 lanes per row: coalesced reads of the projection and of the
+ * per-pair RoPE tables), RMS-normalises each head row in f32, rotates the
+ * pairs (2i, 2i+1) and rounds to bf16 once: the arithmetic of the K pass,
+ * without writing and re-reading Q. The rows go through LDS into the MFMA
+ * operand layout.
  *
  * The running max is updated lazily: O and the row sums are rescaled only when
  * some query's tile max exceeds its running max by more than 8 (log2 units),
  * so probabilities stay <= 2^8 and most tiles skip the rescale. Key masks
  * (sequence end, padding ranges) cost one uniform branch per tile and are
- * applied only to tiles that are not fully valid.
+ * applied only to tiles that are not fully valid. Causal masking and the key
+ * logit bias are separate instantiations, so the joint attention of the
+ * denoiser carries none of their code.
  *
  * LDS rows are padded instead of swizzled, so every fragment address is one
  * base register plus an immediate offset: K rows hold 128 + 8 elements (272 B:
@@ -51,10 +74,20 @@ constexpr float RESCALE_LOG2 = 8.0f;
 constexpr int KSTR = HD + 8, VSTR = KB + 4;
 constexpr int KS_ELEMS = KB * KSTR, VS_ELEMS = HD * VSTR;
 constexpr size_t SMEM_BYTES = (size_t)(2 * KS_ELEMS + 2 * VS_ELEMS) * 2;
+/* with the Q prologue: each wave's 32 normalised, rotated rows after the stages */
+constexpr int QS_OFF = 2 * KS_ELEMS + 2 * VS_ELEMS;
+constexpr size_t SMEM_FUSEQ_BYTES = SMEM_BYTES + (size_t)NW * 32 * KSTR * 2;
 static_assert(QW == 32, "one 32-query MFMA column block per wave");
 
+enum { F_FUSEQ = 1, F_CAUSAL = 2, F_BIAS = 4 };
+
+/* s_waitcnt immediate: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8 */
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
+
+template <int FEAT>
 __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a, float scale_log2, int nqb,
                                                         int per_xcd, int total) {
+    constexpr bool FUSEQ = FEAT & F_FUSEQ, CAUSAL = FEAT & F_CAUSAL, BIAS = FEAT & F_BIAS;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 #define KBUF(b) (smem + (b) * KS_ELEMS)
 #define VBUF(b) (smem + 2 * KS_ELEMS + (b) * VS_ELEMS)
@@ -64,24 +97,129 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     const int qblk = L % nqb, hb = L / nqb;
     const int head = hb % a.heads, bz = hb / a.heads;
     const int kv_head = a.kv_group > 1 ? head / a.kv_group : head;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lr = lane & 31, lg = lane >> 5;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, lg = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, gt = tid & 255;
     const uint16_t *Q = a.q + (size_t)bz * a.q_bstride + head * HD;
     const uint16_t *K = a.k + (size_t)bz * a.k_bstride + kv_head * HD;
     const uint16_t *VT = a.vt + (size_t)bz * a.vt_bstride + (size_t)kv_head * HD * a.ld_vt;
     uint16_t *O = a.o + (size_t)bz * a.o_bstride + head * HD;
     const int sq = a.sq, sk = a.sk;
     /* causal: the block's last query needs keys up to its own index */
-    const int nkt = a.causal ? (min(sk, min(sq, (qblk + 1) * QB)) + KB - 1) / KB : (sk + KB - 1) / KB;
+    const int nkt = CAUSAL ? (min(sk, min(sq, (qblk + 1) * QB)) + KB - 1) / KB : (sk + KB - 1) / KB;
     const int wave_q0 = qblk * QB + wave * QW;
+    const int q_row = wave_q0 + lr;
+
+    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)K, (short)0, (int)(((size_t)(sk - 1) * a.ld_k + HD) * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)VT, (short)0, (int)((size_t)HD * a.ld_vt * 2), 0x00020000);
+
+    /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
+    {
+        const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
+        uint4 r0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, 0, 0));
+        uint4 r1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, 32 * a.ld_k * 2, 0));
+        uint16_t *kd = KBUF(0) + (tid >> 4) * KSTR + (tid & 15) * 8;
+        *(uint4 *)kd = r0;
+        *(uint4 *)(kd + 32 * KSTR) = r1;
+    }
+    /* this group's half of a tile: K rows 32 grp + gt/16 (+ 16), chunk gt % 16;
+     * V^T d rows 64 grp + gt/8 (+ 32), chunk gt % 8 */
+    const int kh_off = ((32 * grp + (gt >> 4)) * a.ld_k + (gt & 15) * 8) * 2;
+    const int vh_off = ((64 * grp + (gt >> 3)) * a.ld_vt + (gt & 7) * 8) * 2;
+    uint16_t *const kh_dst = smem + (32 * grp + (gt >> 4)) * KSTR + (gt & 15) * 8;
+    uint16_t *const vh_dst = smem + 2 * KS_ELEMS + (64 * grp + (gt >> 3)) * VSTR + (gt & 7) * 8;
+    uint4 rk[2], rv[2];
+    auto load_k = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  k_rsrc, kh_off, (kt * KB + 16 * i) * a.ld_k * 2, 0));
+    };
+    auto load_v = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  v_rsrc, vh_off, (32 * i * a.ld_vt + kt * KB) * 2, 0));
+    };
+    auto store_k = [&](int stage) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) *(uint4 *)(kh_dst + stage * KS_ELEMS + 16 * i * KSTR) = rk[i];
+    };
+    auto store_v = [&](int stage) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            uint16_t *d = vh_dst + stage * VS_ELEMS + 32 * i * VSTR;
+            *(uint2 *)d = make_uint2(rv[i].x, rv[i].y);
+            *(uint2 *)(d + 4) = make_uint2(rv[i].z, rv[i].w);
+        }
+    };
+    if (nkt > 1) load_k(1);
+    load_v(0);
 
     /* Q fragments (B operand): lane holds query lr of the wave's 32, d = ds*16 + lg*8 .. +7 */
-    const int q_row = qblk * QB + wave * QW + lr;
     bf16x8 qf[8];
+    /* Q prologue: the wave's 32 rows row by row, 16 lanes per row and 8 dims
+     * per lane (coalesced reads of the projection and of the pair tables; the
+     * arithmetic of the K pass), staged in LDS as [32][KSTR] and read back in
+     * the B-operand layout. All loads are issued before any arithmetic. */
+    auto q_prologue = [&]() {
+        uint16_t *qs = smem + QS_OFF + wave * 32 * KSTR;
+        const int rl = lane >> 4, hl = lane & 15, d0 = hl * 8;
+        u16x8 raw[8];
+        float4 c4[8], s4[8];
 #pragma unroll
-    for (int ds = 0; ds < 8; ds++) {
-        u16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (q_row < sq) v = *(const u16x8 *)(Q + (size_t)q_row * a.ld_q + ds * 16 + lg * 8);
-        qf[ds] = __builtin_bit_cast(bf16x8, v);
+        for (int pass = 0; pass < 8; pass++) {
+            const int row = wave_q0 + pass * 4 + rl;
+            raw[pass] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+            if (row < sq) raw[pass] = *(const u16x8 *)(Q + (size_t)row * a.ld_q + d0);
+            c4[pass] = make_float4(1, 1, 1, 1);
+            s4[pass] = make_float4(0, 0, 0, 0);
+            if (a.rope_cos) {
+                const size_t tr = (size_t)(row < sq ? row : 0) * (HD / 2) + hl * 4;
+                c4[pass] = *(const float4 *)(a.rope_cos + tr);
+                s4[pass] = *(const float4 *)(a.rope_sin + tr);
+            }
+        }
+        const float4 wa0 = *(const float4 *)(a.qn_wA + d0), wa1 = *(const float4 *)(a.qn_wA + d0 + 4);
+        const float4 wb0 = *(const float4 *)(a.qn_wB + d0), wb1 = *(const float4 *)(a.qn_wB + d0 + 4);
+#pragma unroll
+        for (int pass = 0; pass < 8; pass++) {
+            const int rw = pass * 4 + rl, row = wave_q0 + rw;
+            float x[8], ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[pass][j]); ss += x[j] * x[j]; }
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+            const float inv = 1.0f / sqrtf(ss / 128.0f + a.qn_eps);
+            const bool sa = row < a.qn_split;
+            const float ww[8] = {sa ? wa0.x : wb0.x, sa ? wa0.y : wb0.y, sa ? wa0.z : wb0.z, sa ? wa0.w : wb0.w,
+                                 sa ? wa1.x : wb1.x, sa ? wa1.y : wb1.y, sa ? wa1.z : wb1.z, sa ? wa1.w : wb1.w};
+            const float c[4] = {c4[pass].x, c4[pass].y, c4[pass].z, c4[pass].w};
+            const float sn[4] = {s4[pass].x, s4[pass].y, s4[pass].z, s4[pass].w};
+            u16x8 out;
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                const float x0 = x[j] * inv * ww[j], x1 = x[j + 1] * inv * ww[j + 1];
+                out[j] = f2bf(x0 * c[j >> 1] - x1 * sn[j >> 1]);
+                out[j + 1] = f2bf(x1 * c[j >> 1] + x0 * sn[j >> 1]);
+            }
+            *(u16x8 *)(qs + rw * KSTR + d0) = out;
+        }
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));   /* the wave's own LDS writes, read by its other lanes */
+#pragma unroll
+        for (int ds = 0; ds < 8; ds++) qf[ds] = *(const bf16x8 *)(qs + lr * KSTR + (ds * 2 + lg) * 8);
+    };
+    if (!FUSEQ) {
+#pragma unroll
+        for (int ds = 0; ds < 8; ds++) {
+            u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (q_row < sq) raw = *(const u16x8 *)(Q + (size_t)q_row * a.ld_q + ds * 16 + lg * 8);
+            qf[ds] = __builtin_bit_cast(bf16x8, raw);
+        }
+    } else {
+        q_prologue();
     }
 
     f32x16 o[4];
@@ -92,44 +230,34 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     /* running max of the lane's query column (same in both lanes of the column)
      * and this lane's partial row sum over its half of each tile's keys */
     float m_run = -1e30f, l_run = 0.0f;
+    f32x16 s[2];
+    bf16x8 pf[4];
 
-    /* staging: 2 K chunks (16B) and 2 V^T chunks per thread per tile */
-    const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)K, (short)0, (int)(((size_t)(sk - 1) * a.ld_k + HD) * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)VT, (short)0, (int)((size_t)HD * a.ld_vt * 2), 0x00020000);
-    const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;     /* rows tid/16 (+32) */
-    const int v_off = ((tid >> 3) * a.ld_vt + (tid & 7) * 8) * 2;     /* d rows tid/8 (+64) */
-    uint4 rk[2], rv[2];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  k_rsrc, k_off, (kt * KB + 32 * i) * a.ld_k * 2, 0));
-            rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  v_rsrc, v_off, (64 * i * a.ld_vt + kt * KB) * 2, 0));
-        }
-    };
-    auto sstore = [&](int buf) {
-        uint16_t *kd = KBUF(buf) + (tid >> 4) * KSTR + (tid & 15) * 8;
-        uint16_t *vd = VBUF(buf) + (tid >> 3) * VSTR + (tid & 7) * 8;
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            *(uint4 *)(kd + 32 * i * KSTR) = rk[i];
-            *(uint2 *)(vd + 64 * i * VSTR) = make_uint2(rv[i].x, rv[i].y);
-            *(uint2 *)(vd + 64 * i * VSTR + 4) = make_uint2(rv[i].z, rv[i].w);
-        }
+    auto bar = [&]() {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
     };
 
-    gload(0);
-    sstore(0);
-    if (nkt > 1) gload(1);
-    __syncthreads();
-
-    for (int kt = 0; kt < nkt; ++kt) {
-        const int cur = kt & 1, k0 = kt * KB;
-        /* S^T for the tile: 2 key sub-tiles of 32 x the wave's 32 queries */
-        f32x16 s[2];
+    /* PV of the tile in V stage vst: O^T += V^T P^T */
+    auto pv = [&](int vst) {
+        const uint16_t *vb = VBUF(vst);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+#pragma unroll
+            for (int dsub = 0; dsub < 4; dsub++) {
+                const int d = dsub * 32 + lr;
+                const uint2 lo = *(const uint2 *)(&vb[d * VSTR + (4 * j + lg) * 4]);
+                const uint2 hi = *(const uint2 *)(&vb[d * VSTR + (4 * j + 2 + lg) * 4]);
+                const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[dsub], 0, 0, 0);
+            }
+        }
+    };
+    /* S^T of the tile in K stage kst */
+    auto qk = [&](int kst) {
+        const uint16_t *kb = KBUF(kst);
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
@@ -138,30 +266,43 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
         for (int ds = 0; ds < 8; ds++) {
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                const bf16x8 kf = *(const bf16x8 *)(&KBUF(cur)[(ks * 32 + lr) * KSTR + (ds * 2 + lg) * 8]);
+                const bf16x8 kf = *(const bf16x8 *)(&kb[(ks * 32 + lr) * KSTR + (ds * 2 + lg) * 8]);
                 s[ks] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ds], s[ks], 0, 0, 0);
             }
         }
-        /* the stage read in step kt-1 is free: tile kt+1 goes there, tile kt+2's loads start */
-        if (kt + 1 < nkt) sstore(cur ^ 1);
-        if (kt + 2 < nkt) gload(kt + 2);
+    };
+    /* one wave issues the MFMAs of an M phase alone on its SIMD, so fragment
+     * reads run 4 ahead of the products that use them: DS reads, then
+     * alternating MFMA / DS read */
+    auto interleave = [&](int n_mfma) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+        for (int i = 0; i < n_mfma - 4; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    };
 
+    /* V phase of tile t: masks, max, lazy rescale, P = exp2(S - m) as bf16
+     * B-operand fragments, row sums */
+    auto v_phase = [&](int t) {
+        const int k0 = t * KB;
         const bool full = k0 + KB <= sk && ((k0 >= a.kv_lo0 && k0 + KB <= a.kv_hi0) ||
                                             (k0 >= a.kv_lo1 && k0 + KB <= a.kv_hi1)) &&
-                          !(a.causal && k0 + KB - 1 > wave_q0);
+                          !(CAUSAL && k0 + KB - 1 > wave_q0);
         if (!full) {
 #pragma unroll
             for (int ks = 0; ks < 2; ks++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int key = k0 + ks * 32 + (r >> 2) * 8 + lg * 4 + (r & 3);
-                    const bool ok = (key < sk) & (((key >= a.kv_lo0) & (key < a.kv_hi0)) |
-                                                  ((key >= a.kv_lo1) & (key < a.kv_hi1))) &
-                                    (!a.causal | (key <= q_row));
+                    bool ok = (key < sk) & (((key >= a.kv_lo0) & (key < a.kv_hi0)) |
+                                            ((key >= a.kv_lo1) & (key < a.kv_hi1)));
+                    if (CAUSAL) ok = ok & (key <= q_row);
                     s[ks][r] = ok ? s[ks][r] : -INFINITY;
                 }
         }
-        if (a.key_bias != 0.0f && k0 + KB > a.bias_from) {
+        if (BIAS && k0 + KB > a.bias_from) {
             /* logit bias on keys >= bias_from, in units of the raw scores */
             const float bs = a.key_bias / a.scale;
 #pragma unroll
@@ -177,7 +318,10 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
         for (int ks = 0; ks < 2; ks++)
 #pragma unroll
             for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[ks][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
+        {   /* max with the other half-wave's keys of the same query columns */
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+            mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * scale_log2;
+        }
         if (__any(mx > m_run + RESCALE_LOG2)) {
             const float m_new = fmaxf(m_run, mx);
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -188,9 +332,6 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[dsub][r] *= alpha;
         }
-
-        /* P = exp2(S - m) as bf16 B-operand fragments; O^T += V^T P^T */
-        bf16x8 pf[4];
         float rs = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -204,19 +345,38 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
             pf[j] = v;
         }
         l_run += rs;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-#pragma unroll
-            for (int dsub = 0; dsub < 4; dsub++) {
-                const int d = dsub * 32 + lr;
-                const uint2 lo = *(const uint2 *)(&VBUF(cur)[d * VSTR + (4 * j + lg) * 4]);
-                const uint2 hi = *(const uint2 *)(&VBUF(cur)[d * VSTR + (4 * j + 2 + lg) * 4]);
-                const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-                o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[dsub], 0, 0, 0);
-            }
-        }
-        __syncthreads();
+    };
+
+    /* In its M(t) phase a group stages K(t+1) and V(t) from registers, loads
+     * K(t+2) and V(t+1) (indices clamped to the last tile near the end: a
+     * clamped K lands in a stage nothing reads again), then runs PV(t-1) and
+     * QK(t). Group 0: M(0) V(0) M(1) ... V(nkt-1) M(nkt); group 1 one phase
+     * later. Both execute 2 nkt + 3 barriers. */
+    bar();   /* K(0) staged */
+    if (grp) bar();
+    if (nkt > 1) store_k(1);
+    store_v(0);
+    if (nkt > 2) load_k(2);
+    if (nkt > 1) load_v(1);
+    qk(0);
+    bar();
+    v_phase(0);
+    bar();
+    for (int t = 1; t < nkt; t++) {
+        store_k((t + 1) & 1);
+        store_v(t & 1);
+        load_k(min(t + 2, nkt - 1));
+        load_v(min(t + 1, nkt - 1));
+        pv((t - 1) & 1);
+        qk(t & 1);
+        interleave(32);
+        bar();
+        v_phase(t);
+        bar();
     }
+    pv((nkt - 1) & 1);
+    bar();
+    if (!grp) bar();
 
     /* normalise and store O[q][d]: lane holds query lr, d = dsub*32 + (r>>2)*8 + lg*4 + (r&3) */
     const float l = l_run + __shfl_xor(l_run, 32, 64);
@@ -237,6 +397,22 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
 #undef VBUF
 }
 
+template <int FEAT>
+int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, int total) {
+    constexpr size_t smem = (FEAT & F_FUSEQ) ? SMEM_FUSEQ_BYTES : SMEM_BYTES;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (iris_check(hipFuncSetAttribute((const void *)flash_attn_kernel<FEAT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
+                       "attention smem attribute"))
+            return -1;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(flash_attn_kernel<FEAT>, dim3(8 * per_xcd), dim3(NT), smem, iris_stream(), *a,
+                       scale_log2, nqb, per_xcd, total);
+    return iris_launch_check("flash_attn_kernel");
+}
+
 }  // namespace
 
 extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
@@ -249,20 +425,23 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
         return iris_set_error("attention: %d heads not a multiple of kv_group %d", a->heads, a->kv_group);
     if (((uintptr_t)a->q | (uintptr_t)a->k | (uintptr_t)a->vt) & 15)
         return iris_set_error("attention: operands must be 16-byte aligned");
+    const bool fuseq = a->qn_wA != nullptr;
+    if (fuseq && (!a->qn_wB || ((uintptr_t)a->qn_wA | (uintptr_t)a->qn_wB | (uintptr_t)a->rope_cos |
+                                (uintptr_t)a->rope_sin) & 15 || (a->rope_cos && !a->rope_sin)))
+        return iris_set_error("attention: Q prologue needs both norm weight sets and 16-byte aligned tables");
     const int nqb = (a->sq + QB - 1) / QB;
     const long long total = (long long)nqb * a->heads * a->batch;
     if (total > (1LL << 28)) return iris_set_error("attention: grid too large");
     const int per_xcd = (int)((total + 7) / 8);
     const float scale_log2 = a->scale * 1.4426950408889634f;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (iris_check(hipFuncSetAttribute((const void *)flash_attn_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_BYTES),
-                       "attention smem attribute"))
-            return -1;
-        attr_set = true;
+    const int feat = (fuseq ? F_FUSEQ : 0) | (a->causal ? F_CAUSAL : 0) | (a->key_bias != 0.0f ? F_BIAS : 0);
+    switch (feat) {
+    case 0: return launch<0>(a, scale_log2, nqb, per_xcd, (int)total);
+    case F_FUSEQ: return launch<F_FUSEQ>(a, scale_log2, nqb, per_xcd, (int)total);
+    case F_CAUSAL: return launch<F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total);
+    case F_FUSEQ | F_CAUSAL: return launch<F_FUSEQ | F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total);
+    case F_BIAS: return launch<F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total);
+    case F_FUSEQ | F_BIAS: return launch<F_FUSEQ | F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total);
+    default: return iris_set_error("attention: causal masking with a key bias is not supported");
     }
-    hipLaunchKernelGGL(flash_attn_kernel, dim3(8 * per_xcd), dim3(NT), SMEM_BYTES, iris_stream(), *a, scale_log2,
-                       nqb, per_xcd, (int)total);
-    return iris_launch_check("flash_attn_kernel");
 }

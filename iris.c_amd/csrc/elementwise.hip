@@ -224,6 +224,74 @@ __global__ __launch_bounds__(NT) void v_transpose_kernel(const iris_qkprep_args_
     }
 }
 
+/* K RMSNorm + RoPE and V^T of one 64-row block of one K / V head. K: 16
+ * lanes per row, 8 dims per lane (a 16-byte load and store), the row's sum
+ * of squares a 16-lane shuffle reduction; V: through LDS as in
+ * v_transpose_kernel. Rows past the end are written as zeros in V^T. */
+__global__ __launch_bounds__(NT) void kv_prepare_kernel(const iris_qkprep_args_t a) {
+    __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
+    const int r0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
+    const int kvh = a.kv_heads ? a.kv_heads : a.heads;
+    const int d0 = (tid & 15) * 8;
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+        const int row = r0 + it * 16 + (tid >> 4);
+        if (row >= a.rows) break;                          /* uniform per 16-lane row group */
+        const int prow = a.period ? row % a.period : row;
+        const u16x8 raw = *(const u16x8 *)(a.qkv + (size_t)row * a.ld_qkv + a.col_k + head * 128 + d0);
+        float x[8], ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[j]); ss += x[j] * x[j]; }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+        const float *w = prow >= a.split ? a.wkB : a.wkA;
+        const float4 w0 = *(const float4 *)(w + d0), w1 = *(const float4 *)(w + d0 + 4);
+        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        float c[8] = {1, 1, 1, 1, 1, 1, 1, 1}, sn[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        const float *ct = a.kcos_t ? a.kcos_t : a.cos_t, *st = a.kcos_t ? a.ksin_t : a.sin_t;
+        if (ct) {
+            const float4 c0 = *(const float4 *)(ct + (size_t)prow * 128 + d0);
+            const float4 c1 = *(const float4 *)(ct + (size_t)prow * 128 + d0 + 4);
+            const float4 s0 = *(const float4 *)(st + (size_t)prow * 128 + d0);
+            const float4 s1 = *(const float4 *)(st + (size_t)prow * 128 + d0 + 4);
+            c[0] = c0.x; c[2] = c0.z; c[4] = c1.x; c[6] = c1.z;
+            sn[0] = s0.x; sn[2] = s0.z; sn[4] = s1.x; sn[6] = s1.z;
+        }
+        u16x8 out;
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+            const float x0 = x[j] * inv * ww[j], x1 = x[j + 1] * inv * ww[j + 1];
+            out[j] = f2bf(x0 * c[j] - x1 * sn[j]);
+            out[j + 1] = f2bf(x1 * c[j] + x0 * sn[j]);
+        }
+        *(u16x8 *)(a.k_out + (size_t)row * kvh * 128 + head * 128 + d0) = out;
+    }
+#pragma unroll
+    for (int it = 0; it < 2; it++) {                       /* 32 row pairs x 16 chunks of 8 dims */
+        const int item = tid + NT * it, p = item >> 4, ch = item & 15;
+        const int ra = r0 + 2 * p;
+        const uint16_t *src = a.qkv + (size_t)ra * a.ld_qkv + a.col_v + head * 128 + ch * 8;
+        u16x8 va = {0, 0, 0, 0, 0, 0, 0, 0}, vb = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (ra < a.rows) va = *(const u16x8 *)src;
+        if (ra + 1 < a.rows) vb = *(const u16x8 *)(src + a.ld_qkv);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int d = ch * 8 + j;
+            const int col = (2 * p) ^ (((d >> 3) & 7) << 3);
+            *(uint32_t *)(&t[d * 72 + col]) = (uint32_t)va[j] | ((uint32_t)vb[j] << 16);
+        }
+    }
+    __syncthreads();
+    uint16_t *dst = a.vt_out + (size_t)head * 128 * a.ld_vt + r0;
+#pragma unroll
+    for (int it = 0; it < 4; it++) {                       /* 128 d x 8 chunks of 8 rows */
+        const int item = tid + NT * it, d = item >> 3, c8 = item & 7;
+        const uint4 v = *(const uint4 *)(&t[d * 72 + ((c8 ^ ((d >> 3) & 7)) << 3)]);
+        *(uint4 *)(dst + (size_t)d * a.ld_vt + c8 * 8) = v;
+    }
+}
+
 /* one wave per output row */
 __global__ __launch_bounds__(NT) void gemv_kernel(float *y, const uint16_t *W, const float *x, const float *bias,
                                                   int N, int K, int act_in) {
@@ -412,6 +480,21 @@ int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
     const int kvh = a->kv_heads ? a->kv_heads : a->heads;
     hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
     return iris_launch_check("v_transpose_kernel");
+}
+
+int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
+    if (a->rows <= 0) return 0;
+    if (a->ld_qkv % 8 || a->col_k % 8 || a->col_v % 8) return iris_set_error("kv_prepare: layout not 16-byte aligned");
+    if (a->ld_vt < a->rows || a->ld_vt % 64) return iris_set_error("kv_prepare: ld_vt=%d", a->ld_vt);
+    if (a->heads <= 0 || a->kv_heads < 0 || a->kv_heads > a->heads)
+        return iris_set_error("kv_prepare: heads=%d kv_heads=%d", a->heads, a->kv_heads);
+    if (!a->wkA || !a->wkB) return iris_set_error("kv_prepare: K norm weights missing");
+    if (((uintptr_t)a->qkv | (uintptr_t)a->k_out | (uintptr_t)a->vt_out | (uintptr_t)a->wkA | (uintptr_t)a->wkB |
+         (uintptr_t)a->cos_t | (uintptr_t)a->sin_t | (uintptr_t)a->kcos_t | (uintptr_t)a->ksin_t) & 15)
+        return iris_set_error("kv_prepare: buffers must be 16-byte aligned");
+    const int kvh = a->kv_heads ? a->kv_heads : a->heads;
+    hipLaunchKernelGGL(kv_prepare_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
+    return iris_launch_check("kv_prepare_kernel");
 }
 
 int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias, int N, int K, int act_in) {

@@ -131,13 +131,44 @@ void par_memcpy(void *dst, const void *src, size_t n) {
     memcpy(dst, src, n < per ? n : per);
     for (int i = 0; i < used; i++) th[i].join();
 }
+
+/* Small uploads (per-step inputs such as the timestep sinusoid): the source
+ * is copied into one of SM_SLOTS pinned slots and the DMA reads the slot, so
+ * the call returns with the source free for reuse and the copy stays
+ * asynchronous; a slot is refilled only after the event behind its last copy
+ * has fired. */
+constexpr size_t SM_SLOT = 64u << 10;
+constexpr int SM_SLOTS = 16;
+char *g_sm_buf;
+hipEvent_t g_sm_ev[SM_SLOTS];
+int g_sm_state, g_sm_next;
+
+int sm_init() {
+    if (g_sm_state) return g_sm_state > 0 ? 0 : -1;
+    g_sm_state = -1;
+    if (hipHostMalloc((void **)&g_sm_buf, SM_SLOT * SM_SLOTS, hipHostMallocDefault) != hipSuccess) return -1;
+    for (int i = 0; i < SM_SLOTS; i++)
+        if (hipEventCreateWithFlags(&g_sm_ev[i], hipEventDisableTiming) != hipSuccess) return -1;
+    g_sm_state = 1;
+    return 0;
+}
 }  // namespace
 
 int iris_hip_memcpy_h2d(void *dst, const void *src, size_t bytes) {
     if (!bytes) return 0;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    if (bytes < UP_MIN || hipStreamIsCapturing(g_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone ||
-        up_init())
+    const bool capturing = hipStreamIsCapturing(g_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone;
+    if (!capturing && bytes <= SM_SLOT && sm_init() == 0) {
+        std::lock_guard<std::mutex> lock(g_up_mutex);
+        const int b = g_sm_next;
+        g_sm_next = (g_sm_next + 1) % SM_SLOTS;
+        char *slot = g_sm_buf + (size_t)b * SM_SLOT;
+        if (iris_check(hipEventSynchronize(g_sm_ev[b]), "small upload slot wait")) return -1;
+        memcpy(slot, src, bytes);
+        return iris_check(hipMemcpyAsync(dst, slot, bytes, hipMemcpyHostToDevice, g_stream), "memcpy h2d") ||
+               iris_check(hipEventRecord(g_sm_ev[b], g_stream), "small upload event");
+    }
+    if (bytes < UP_MIN || capturing || up_init())
         return iris_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream), "memcpy h2d");
     std::lock_guard<std::mutex> lock(g_up_mutex);
     size_t i = 0;

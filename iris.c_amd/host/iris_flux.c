@@ -84,6 +84,7 @@ typedef struct {
     float *lat;              /* [C][I] target then refs, NCHW per image */
     float *vel;              /* [B][C][I0] */
     float *rope_cos, *rope_sin;   /* [S][128] */
+    float *rp_cos, *rp_sin;       /* [S][64]: one value per rotation pair (the attention's Q prologue) */
     float *krope_cos, *krope_sin; /* [S][128] K side: the reference rows' H/W bands scaled (SREF) */
     float kshf, kslf;             /* band scales the K tables hold */
     float kgamma;                 /* SREF strength the captured graph applies */
@@ -91,7 +92,8 @@ typedef struct {
     float *tsin;             /* [256] */
     float *tmp, *temb;       /* [h] */
     float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
-    float *tsin_host;        /* pinned */
+    float *tsin_host;        /* host copy of the timestep sinusoid (small uploads are staged out of
+                              * it into pinned slots before iris_hip_memcpy_h2d returns) */
     void *graph;
 } work_t;
 
@@ -421,7 +423,8 @@ int iris_transformer_text_dim(iris_transformer_t *tf) { return tf->text_dim; }
 static void work_free(work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
-                    w->rope_cos, w->rope_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp, w->temb, w->mod};
+                    w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp,
+                    w->temb, w->mod};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -527,6 +530,8 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
     DA(w->krope_cos, S * 128 * 4);
     DA(w->krope_sin, S * 128 * 4);
     DA(w->rope_sin, S * 128 * 4);
+    DA(w->rp_cos, S * 64 * 4);
+    DA(w->rp_sin, S * 64 * 4);
     DA(w->tsin, 256 * 4);
     DA(w->tmp, (size_t)h * 4);
     DA(w->temb, (size_t)h * 4);
@@ -546,9 +551,13 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
             iris_rope_img(c + off, s + off, refs[r].h, refs[r].w, tf->axis_dim, tf->theta, refs[r].t_offset);
             off += (size_t)refs[r].h * refs[r].w * 128;
         }
-        int rc = iris_hip_memcpy_h2d(w->rope_cos, c, S * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, S * 128 * 4) ||
-                 iris_hip_sync() || fill_ktables(tf, c, s);
-        free(c); free(s);
+        float *pc = (float *)malloc(S * 64 * sizeof(float)), *ps = (float *)malloc(S * 64 * sizeof(float));
+        int rc = !pc || !ps;
+        if (!rc) iris_rope_pairs(pc, ps, c, s, S);
+        rc = rc || iris_hip_memcpy_h2d(w->rope_cos, c, S * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, S * 128 * 4) ||
+             iris_hip_memcpy_h2d(w->rp_cos, pc, S * 64 * 4) || iris_hip_memcpy_h2d(w->rp_sin, ps, S * 64 * 4) ||
+             iris_hip_sync() || fill_ktables(tf, c, s);
+        free(c); free(s); free(pc); free(ps);
         if (rc) goto fail;
     }
     w->valid = 1;
@@ -574,9 +583,12 @@ static iris_gemm_problem_t prob(const void *A, int lda, const uint16_t *W, int l
     return p;
 }
 
-/* QK-RMSNorm + RoPE of each stream and V^T for every batch slot */
-static int qk_prepare(iris_transformer_t *tf, const float *wqA, const float *wkA, const float *wqB,
-                      const float *wkB, int split) {
+/* K-RMSNorm + RoPE of each stream and V^T for every batch slot (the Q half
+ * runs in the attention kernel's prologue). kside: K rotates with the K-side
+ * tables (the SREF band control), which the reference applies in
+ * single-stream blocks only (iris_transformer_flux.c:3866-3873); its double
+ * blocks rotate K with the plain tables (:2449-2450). */
+static int kv_prepare(iris_transformer_t *tf, const float *wkA, const float *wkB, int split, int kside) {
     work_t *w = &tf->w;
     int h = tf->hidden;
     for (int b = 0; b < w->B; b++) {
@@ -584,32 +596,36 @@ static int qk_prepare(iris_transformer_t *tf, const float *wqA, const float *wkA
         memset(&a, 0, sizeof(a));
         a.qkv = w->qkv + (size_t)b * w->S * 3 * h;
         a.ld_qkv = 3 * h; a.col_k = h; a.col_v = 2 * h;
-        a.q_out = w->q + (size_t)b * w->S * h;
         a.k_out = w->k + (size_t)b * w->S * h;
         a.vt_out = w->vt + (size_t)b * tf->heads * 128 * w->S_pad;
         a.ld_vt = w->S_pad;
         a.rows = w->S; a.heads = tf->heads;
-        a.wqA = wqA; a.wkA = wkA; a.wqB = wqB; a.wkB = wkB; a.split = split;
+        a.wkA = wkA; a.wkB = wkB; a.split = split;
         a.cos_t = w->rope_cos; a.sin_t = w->rope_sin;
-        a.kcos_t = w->krope_cos; a.ksin_t = w->krope_sin;
+        if (kside) { a.kcos_t = w->krope_cos; a.ksin_t = w->krope_sin; }
         a.eps = 1e-6f;
-        CK(iris_hip_qk_prepare(&a));
+        CK(iris_hip_kv_prepare(&a));
     }
     return 0;
 }
 
-static int attention(iris_transformer_t *tf, uint16_t *o, int ld_o) {
+/* joint attention over the resident sequence; Q (columns [0, h) of qkv) is
+ * QK-normalised (wqA for rows < split, else wqB) and rotated in the kernel's
+ * prologue */
+static int attention(iris_transformer_t *tf, const float *wqA, const float *wqB, int split, uint16_t *o, int ld_o) {
     work_t *w = &tf->w;
     int h = tf->hidden;
     iris_attn_args_t a;
     memset(&a, 0, sizeof(a));
-    a.q = w->q; a.k = w->k; a.vt = w->vt; a.o = o;
-    a.ld_q = h; a.ld_k = h; a.ld_vt = w->S_pad; a.ld_o = ld_o;
+    a.q = w->qkv; a.k = w->k; a.vt = w->vt; a.o = o;
+    a.ld_q = 3 * h; a.ld_k = h; a.ld_vt = w->S_pad; a.ld_o = ld_o;
     a.sq = w->S; a.sk = w->S; a.heads = tf->heads; a.batch = w->B;
-    a.q_bstride = (long long)w->S * h; a.k_bstride = (long long)w->S * h;
+    a.q_bstride = (long long)w->S * 3 * h; a.k_bstride = (long long)w->S * h;
     a.vt_bstride = (long long)tf->heads * 128 * w->S_pad; a.o_bstride = (long long)w->S * ld_o;
     a.scale = 1.0f / sqrtf(128.0f);
     a.kv_lo0 = 0; a.kv_hi0 = w->S;
+    a.qn_wA = wqA; a.qn_wB = wqB; a.qn_split = split; a.qn_eps = 1e-6f;
+    a.rope_cos = w->rp_cos; a.rope_sin = w->rp_sin;
     /* SREF strength (sref_set_strength_bias, iris_transformer_flux.c:1328-1338):
      * log gamma on the logits of the reference keys, the trailing I - I0 tokens */
     if (w->n_refs > 0 && tf->sref_strength != 1.0f) {
@@ -650,9 +666,9 @@ static int double_block_forward(iris_transformer_t *tf, int i) {
                       IRIS_EPI_BF16);
     }
     CK(gemm(p, n));
-    CK(qk_prepare(tf, bw->txt_nq, bw->txt_nk, bw->img_nq, bw->img_nk, T));
+    CK(kv_prepare(tf, bw->txt_nk, bw->img_nk, T, 0));
     /* joint attention over [txt, img] -> cat[:, 0:h] */
-    CK(attention(tf, w->cat, hm));
+    CK(attention(tf, bw->txt_nq, bw->img_nq, T, w->cat, hm));
     /* output projections, gated residual (gate1) */
     n = 0;
     for (int b = 0; b < B; b++) {
@@ -696,8 +712,8 @@ static int single_block_forward(iris_transformer_t *tf, int i) {
     p[0] = prob(w->a, h, bw->qkv_mlp, h, w->qkv, 3 * h, NULL, BS, 3 * h, h, IRIS_EPI_BF16);
     p[1] = prob(w->a, h, bw->qkv_mlp + (size_t)3 * h * h, h, w->cat + h, hm, NULL, BS, 2 * mlp, h, IRIS_EPI_SWIGLU);
     CK(gemm(p, 2));
-    CK(qk_prepare(tf, bw->nq, bw->nk, bw->nq, bw->nk, w->S));
-    CK(attention(tf, w->cat, hm));
+    CK(kv_prepare(tf, bw->nk, bw->nk, w->S, 1));
+    CK(attention(tf, bw->nq, bw->nq, w->S, w->cat, hm));
     /* [attn | mlp] . W_out^T, gated residual */
     p[0] = prob(w->cat, hm, bw->out, hm, w->x, h, ms + 2 * h, BS, h, hm, IRIS_EPI_GATED_ADD);
     CK(gemm(p, 1));
@@ -851,6 +867,8 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
     if (!strcmp(name, "krope_cos")) return w->krope_cos;
     if (!strcmp(name, "krope_sin")) return w->krope_sin;
     if (!strcmp(name, "rope_sin")) return w->rope_sin;
+    if (!strcmp(name, "rope_pair_cos")) return w->rp_cos;
+    if (!strcmp(name, "rope_pair_sin")) return w->rp_sin;
     if (!strcmp(name, "t_emb")) return w->temb;
     if (!strcmp(name, "mod")) return w->mod;
     if (!strcmp(name, "a")) return w->a;
@@ -1004,12 +1022,12 @@ fail:
 }
 
 /* The reference's adapter setters (iris_transformer_flux.c:5131-5201), kept
- * so a caller links unchanged. The HIP forward implements none of the
- * adapters other than SREF: while one is attached (LoRA, CSD style delta,
- * IP-Adapter) every forward fails with a message
- * instead of silently ignoring it. Ownership follows the reference: the
- * transformer takes what it is given and releases it on replacement or free
- * through the reference's own release functions when those are linked in. */
+ * so a caller links unchanged. LoRA, the CSD style delta and the SREF
+ * controls are applied; while an IP-Adapter is attached every forward fails
+ * with a message instead of silently ignoring it. Ownership follows the
+ * reference: the transformer takes what it is given and releases it on
+ * replacement or free through the reference's own release functions when
+ * those are linked in. */
 void lora_free(void *lora) __attribute__((weak));
 void iris_ip_adapter_free(void *ip) __attribute__((weak));
 int iris_ip_adapter_set_schedule(void *ip, const char *spec) __attribute__((weak));

@@ -12,7 +12,8 @@
  * Here every linear is the bf16 MFMA GEMM (fused epilogues: the residual adds
  * are IRIS_EPI_GATED_ADD without a gate, silu(gate)*up is IRIS_EPI_SWIGLU
  * over gate/up rows interleaved in 32-row groups), Q/K norm + rotary
- * embedding is iris_hip_qk_prepare, and attention is the flash kernel with
+ * embedding is iris_hip_kv_prepare for K and the attention kernel's prologue
+ * for Q, and attention is the flash kernel with
  * its causal and grouped-query modes. The split-half rotation pairs dims d
  * and d+64 of a head; the upload permutes each head's Q and K rows (and the
  * Q/K norm weights) to the order 0, 64, 1, 65, ... so those pairs are
@@ -53,6 +54,7 @@ struct qwen3_model {
     float *x, *out;           /* x [S][h] residual stream; out [S][3h] */
     uint16_t *a, *qkv, *q, *k, *vt, *attn, *mlp;
     float *rope_cos, *rope_sin;   /* [S][128], value of pair p at 2p and 2p+1 */
+    float *rp_cos, *rp_sin;       /* [S][64], value of pair p at p (the attention's Q prologue) */
     float *ws;                    /* split-K partial products */
     size_t ws_bytes;
 };
@@ -175,7 +177,7 @@ static void free_model(qwen3_model_t *m) {
     iris_hip_free(m->ids); iris_hip_free(m->x); iris_hip_free(m->out);
     iris_hip_free(m->a); iris_hip_free(m->qkv); iris_hip_free(m->q); iris_hip_free(m->k); iris_hip_free(m->vt);
     iris_hip_free(m->attn); iris_hip_free(m->mlp);
-    iris_hip_free(m->rope_cos); iris_hip_free(m->rope_sin); iris_hip_free(m->ws);
+    iris_hip_free(m->rope_cos); iris_hip_free(m->rope_sin); iris_hip_free(m->rp_cos); iris_hip_free(m->rp_sin); iris_hip_free(m->ws);
     free(m);
 }
 
@@ -207,9 +209,19 @@ static int build_rope(qwen3_model_t *m) {
         }
     m->rope_cos = (float *)iris_hip_malloc((size_t)S * HD * sizeof(float));
     m->rope_sin = (float *)iris_hip_malloc((size_t)S * HD * sizeof(float));
-    if (!m->rope_cos || !m->rope_sin) goto out;
-    if (iris_hip_memcpy_h2d(m->rope_cos, c, (size_t)S * HD * 4) || iris_hip_memcpy_h2d(m->rope_sin, sn, (size_t)S * HD * 4) ||
-        iris_hip_sync())
+    m->rp_cos = (float *)iris_hip_malloc((size_t)S * (HD / 2) * sizeof(float));
+    m->rp_sin = (float *)iris_hip_malloc((size_t)S * (HD / 2) * sizeof(float));
+    if (!m->rope_cos || !m->rope_sin || !m->rp_cos || !m->rp_sin) goto out;
+    if (iris_hip_memcpy_h2d(m->rope_cos, c, (size_t)S * HD * 4) || iris_hip_memcpy_h2d(m->rope_sin, sn, (size_t)S * HD * 4))
+        goto out;
+    /* the pair tables: entry i = column 2i */
+    for (int pos = 0; pos < S; pos++)
+        for (int i = 0; i < HD / 2; i++) {
+            c[(size_t)pos * (HD / 2) + i] = c[(size_t)pos * HD + 2 * i];
+            sn[(size_t)pos * (HD / 2) + i] = sn[(size_t)pos * HD + 2 * i];
+        }
+    if (iris_hip_memcpy_h2d(m->rp_cos, c, (size_t)S * (HD / 2) * 4) ||
+        iris_hip_memcpy_h2d(m->rp_sin, sn, (size_t)S * (HD / 2) * 4) || iris_hip_sync())
         goto out;
     rc = 0;
 out:
@@ -401,15 +413,18 @@ static int layer_forward(qwen3_model_t *m, const qlayer_t *l, int S, int n_real)
     iris_qkprep_args_t q;
     memset(&q, 0, sizeof(q));
     q.qkv = m->qkv; q.ld_qkv = qd + 2 * kd; q.col_k = qd; q.col_v = qd + kd;
-    q.q_out = m->q; q.k_out = m->k; q.vt_out = m->vt; q.ld_vt = S_pad;
+    q.k_out = m->k; q.vt_out = m->vt; q.ld_vt = S_pad;
     q.rows = S; q.heads = m->heads; q.kv_heads = m->kv_heads;
-    q.wqA = q.wqB = l->q_norm; q.wkA = q.wkB = l->k_norm; q.split = S;
+    q.wkA = q.wkB = l->k_norm; q.split = S;
     q.cos_t = m->rope_cos; q.sin_t = m->rope_sin; q.eps = QWEN3_RMS_NORM_EPS;
-    CK(iris_hip_qk_prepare(&q));
+    CK(iris_hip_kv_prepare(&q));
+    /* Q: RMSNorm + rotary in the attention kernel's prologue */
     iris_attn_args_t at;
     memset(&at, 0, sizeof(at));
-    at.q = m->q; at.k = m->k; at.vt = m->vt; at.o = m->attn;
-    at.ld_q = qd; at.ld_k = kd; at.ld_vt = S_pad; at.ld_o = qd;
+    at.q = m->qkv; at.k = m->k; at.vt = m->vt; at.o = m->attn;
+    at.ld_q = qd + 2 * kd; at.ld_k = kd; at.ld_vt = S_pad; at.ld_o = qd;
+    at.qn_wA = at.qn_wB = l->q_norm; at.qn_split = S; at.qn_eps = QWEN3_RMS_NORM_EPS;
+    at.rope_cos = m->rp_cos; at.rope_sin = m->rp_sin;
     at.sq = S; at.sk = S; at.heads = m->heads; at.batch = 1;
     at.scale = 1.0f / sqrtf((float)HD);
     at.kv_lo0 = 0; at.kv_hi0 = n_real;          /* padding keys (:408-414) */

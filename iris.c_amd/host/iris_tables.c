@@ -105,3 +105,14 @@ void iris_timestep_sincos(float *out, float t, int dim, float max_period) {
         out[i + half] = sinf(a);
     }
 }
+
+/* Per-pair copies of [rows][128] tables whose pairs (2i, 2i+1) hold one
+ * value: [rows][64], entry i = column 2i (the attention kernel's Q prologue
+ * reads one value per rotation pair). */
+void iris_rope_pairs(float *pc, float *ps, const float *c, const float *s, size_t rows) {
+    for (size_t r = 0; r < rows; r++)
+        for (int i = 0; i < 64; i++) {
+            pc[r * 64 + i] = c[r * 128 + 2 * i];
+            ps[r * 64 + i] = s[r * 128 + 2 * i];
+        }
+}

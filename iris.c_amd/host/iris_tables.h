@@ -11,6 +11,7 @@ void iris_rope_txt(float *cos_out, float *sin_out, int txt_seq, int axis_dim, fl
 void iris_rope_zimage(float *cos_out, float *sin_out, const int *pos, int seq, const int *axes,
                       const int *lens, float theta);
 void iris_timestep_sincos(float *out, float t, int dim, float max_period);
+void iris_rope_pairs(float *pc, float *ps, const float *c, const float *s, size_t rows);
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,7 @@ typedef struct {
     int valid, lh, lw, cap_len;
     int I, Ip, Cp, U, U_pad;
     float *x, *y, *rope_cos, *rope_sin, *tsin, *tmp, *temb, *mods, *fscale, *lat, *vel, *capf, *fout;
+    float *rp_cos, *rp_sin;       /* [U][64]: one value per rotation pair (the attention's Q prologue) */
     uint16_t *a, *qkv, *q, *k, *vt, *attn, *ffn, *patches;
     float *tsin_host;
     void *graph;
@@ -338,7 +339,7 @@ zi_transformer_t *zi_transformer_create_synthetic(int dim, int n_heads, int n_la
 
 static void zwork_free(zi_work_t *w) {
     iris_hip_graph_destroy(w->graph);
-    void *p[] = {w->x, w->y, w->rope_cos, w->rope_sin, w->tsin, w->tmp, w->temb, w->mods, w->fscale, w->lat, w->vel,
+    void *p[] = {w->x, w->y, w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->tsin, w->tmp, w->temb, w->mods, w->fscale, w->lat, w->vel,
                  w->capf, w->fout, w->a, w->qkv, w->q, w->k, w->vt, w->attn, w->ffn, w->patches};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     free(w->tsin_host);
@@ -369,6 +370,8 @@ int zi_prepare(zi_transformer_t *tf, int lh, int lw, int cap_len) {
     DA(w->x, U * d * 4);
     DA(w->y, U * d * 4);
     DA(w->rope_cos, U * 128 * 4);
+    DA(w->rp_cos, U * 64 * 4);
+    DA(w->rp_sin, U * 64 * 4);
     DA(w->rope_sin, U * 128 * 4);
     DA(w->tsin, 256 * 4);
     DA(w->tmp, (size_t)tf->t_mid * 4);
@@ -401,9 +404,13 @@ int zi_prepare(zi_transformer_t *tf, int lh, int lw, int cap_len) {
         }
         for (int j = 0; j < w->Cp; j++) pos[(w->Ip + j) * 3] = 1 + j;
         iris_rope_zimage(c, s, pos, (int)U, tf->axes, tf->lens, tf->theta);
-        int rc = iris_hip_memcpy_h2d(w->rope_cos, c, U * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, U * 128 * 4) ||
-                 iris_hip_sync();
-        free(pos); free(c); free(s);
+        float *pc = (float *)malloc(U * 64 * 4), *ps = (float *)malloc(U * 64 * 4);
+        int rc = !pc || !ps;
+        if (!rc) iris_rope_pairs(pc, ps, c, s, U);
+        rc = rc || iris_hip_memcpy_h2d(w->rope_cos, c, U * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, U * 128 * 4) ||
+             iris_hip_memcpy_h2d(w->rp_cos, pc, U * 64 * 4) || iris_hip_memcpy_h2d(w->rp_sin, ps, U * 64 * 4) ||
+             iris_hip_sync();
+        free(pos); free(c); free(s); free(pc); free(ps);
         if (rc) goto fail;
     }
     w->valid = 1;
@@ -457,19 +464,22 @@ static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const
     iris_qkprep_args_t q;
     memset(&q, 0, sizeof(q));
     q.qkv = w->qkv; q.ld_qkv = 3 * d; q.col_k = d; q.col_v = 2 * d;
-    q.q_out = w->q; q.k_out = w->k; q.vt_out = w->vt; q.ld_vt = w->U_pad;
+    q.k_out = w->k; q.vt_out = w->vt; q.ld_vt = w->U_pad;
     q.rows = n; q.heads = tf->heads;
-    q.wqA = b->nq; q.wkA = b->nk; q.wqB = b->nq; q.wkB = b->nk; q.split = n;
+    q.wkA = b->nk; q.wkB = b->nk; q.split = n;
     q.cos_t = w->rope_cos + (size_t)r0 * 128; q.sin_t = w->rope_sin + (size_t)r0 * 128;
     q.eps = ZI_EPS;
-    CK(iris_hip_qk_prepare(&q));
+    CK(iris_hip_kv_prepare(&q));
+    /* Q: zi_qk_norm + zi_apply_rope in the attention kernel's prologue */
     iris_attn_args_t at;
     memset(&at, 0, sizeof(at));
-    at.q = w->q; at.k = w->k; at.vt = w->vt; at.o = w->attn;
-    at.ld_q = d; at.ld_k = d; at.ld_vt = w->U_pad; at.ld_o = d;
+    at.q = w->qkv; at.k = w->k; at.vt = w->vt; at.o = w->attn;
+    at.ld_q = 3 * d; at.ld_k = d; at.ld_vt = w->U_pad; at.ld_o = d;
     at.sq = n; at.sk = n; at.heads = tf->heads; at.batch = 1;
     at.scale = 1.0f / sqrtf(128.0f);
     at.kv_lo0 = klo0; at.kv_hi0 = khi0; at.kv_lo1 = klo1; at.kv_hi1 = khi1;
+    at.qn_wA = b->nq; at.qn_wB = b->nq; at.qn_split = n; at.qn_eps = ZI_EPS;
+    at.rope_cos = w->rp_cos + (size_t)r0 * 64; at.rope_sin = w->rp_sin + (size_t)r0 * 64;
     CK(iris_hip_attention(&at));
     p = zprob(w->attn, d, b->o, w->y, d, NULL, n, d, d, IRIS_EPI_F32);
     CK(iris_hip_gemm(&p, 1));
@@ -535,6 +545,25 @@ static int zi_enqueue(zi_transformer_t *tf) {
     CK(iris_hip_gemm(&p, 1));
     CK(iris_hip_unpatchify(w->vel, w->fout, tf->in_ch, w->lh, w->lw, tf->ps));
     return 0;
+}
+
+/* One block outside the captured graph (the forward's rows, masks and
+ * modulation GEMV for that block). */
+int zi_block_forward_resident(zi_transformer_t *tf, int kind, int idx) {
+    zi_work_t *w = &tf->w;
+    const int d = tf->dim;
+    if (!w->valid || kind < 0 || kind > 2 || idx < 0 || idx >= (kind == 2 ? tf->layers : tf->refiners)) return -1;
+    if (kind == 1) {
+        if (zi_block_forward(tf, &tf->cr[idx], NULL, w->Ip, w->Cp, 0, w->cap_len, 0, 0)) return -1;
+        return iris_hip_sync();
+    }
+    const zi_dev_block_t *b = kind == 0 ? &tf->nr[idx] : &tf->ly[idx];
+    float *mod = w->mods + (size_t)(kind == 0 ? idx : tf->refiners + idx) * 4 * d;
+    if (iris_hip_gemv(mod, b->ada_w, w->temb, b->ada_b, 4 * d, tf->adaln_dim, 0)) return -1;
+    if (kind == 0 ? zi_block_forward(tf, b, mod, 0, w->Ip, 0, w->I, 0, 0)
+                  : zi_block_forward(tf, b, mod, 0, w->U, 0, w->I, w->Ip, w->Ip + w->cap_len))
+        return -1;
+    return iris_hip_sync();
 }
 
 /* -------------------------------------------------------- step entry points */

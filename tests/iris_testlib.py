@@ -102,7 +102,9 @@ class AttnArgs(ctypes.Structure):
                 ("vt_bstride", ctypes.c_longlong), ("o_bstride", ctypes.c_longlong),
                 ("scale", ctypes.c_float), ("kv_lo0", ctypes.c_int), ("kv_hi0", ctypes.c_int),
                 ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int), ("causal", ctypes.c_int),
-                ("kv_group", ctypes.c_int), ("bias_from", ctypes.c_int), ("key_bias", ctypes.c_float)]
+                ("kv_group", ctypes.c_int), ("bias_from", ctypes.c_int), ("key_bias", ctypes.c_float),
+                ("qn_wA", ctypes.c_void_p), ("qn_wB", ctypes.c_void_p), ("qn_split", ctypes.c_int),
+                ("qn_eps", ctypes.c_float), ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p)]
 
 
 class Conv3x3(ctypes.Structure):

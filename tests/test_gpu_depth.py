@@ -1,0 +1,180 @@
+"""Parity at real widths and full depth (HIP build vs the oracle).
+
+* The Flux.2-Klein-4B-shaped denoiser at full depth (5 double + 20 single
+  blocks, hidden 3072, 24 heads, text 7680) sampling a 512x512 image (32x32
+  latent = 1024 image tokens + 512 text tokens) over the reference's 4-step
+  official schedule from the reference's seed-42 noise: each step's velocity
+  on the oracle's own trajectory (rel-L2 < 1e-2, cosine > 0.999), and the
+  product sampler's final latent against the oracle's Euler loop
+  (iris_sample.c:313-405; cosine >= 0.999, rel-L2 <= 1e-2).
+* The 4B-shaped forward with two reference images (T offsets 1, 2) at 4B
+  widths (iris_transformer_flux.c:4579-4829).
+* Z-Image-Turbo widths block by block (noise refiner, context refiner, main
+  layer; iris_transformer_zimage.c:790-870), each within rel-L2 1e-2.
+
+The 4-step sample is checked against the oracle's output committed in
+tests/golden/ (the oracle needs minutes of host time at this size); the
+other two run the oracle live on the host cores.
+"""
+import ctypes
+import os
+import sys
+import time
+
+import numpy as np
+import pytest
+
+import iris_testlib as tl
+
+pytestmark = pytest.mark.gpu
+F = ctypes.c_float
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return tl.hip()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    o = tl.oracle()
+    o.orc_zi_create_synth.restype = ctypes.c_void_p
+    o.orc_zi_create_synth.argtypes = [ctypes.c_int] * 7 + [F, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                           ctypes.c_uint64]
+    o.orc_zi_block.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, tl.FP, tl.IP, tl.IP, tl.FP, ctypes.c_int]
+    o.orc_zi_set_reference_aliasing(0)
+    return o
+
+
+def take(lib, p, n):
+    assert p, lib.iris_hip_last_error()
+    out = np.ctypeslib.as_array(ctypes.cast(p, tl.FP), shape=(n,)).copy()
+    ctypes.CDLL(None).free(ctypes.c_void_p(p))
+    return out
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+DEPTH = os.path.join(tl.GOLDEN, "oracle_4b_c2_sample.npz")
+
+
+def test_4b_full_depth_four_step_sample(lib):
+    """Against tests/golden/oracle_4b_c2_sample.npz (the oracle's sample on the
+    same seeded weights, noise, schedule and text; tests/golden/
+    make_golden_depth.py): each step's velocity on the oracle's trajectory,
+    then the product sampler from the same noise."""
+    g = np.load(DEPTH, allow_pickle=False)
+    h, H, nd, ns, td, T = 3072, 24, 5, 20, 7680, 512
+    lh = lw = 32
+    n = 128 * lh * lw
+    t0 = time.time()
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(h, H, nd, ns, td, 128, 3.0, 2000.0, 4242))
+    assert tf.value, lib.iris_hip_last_error()
+    lib.iris_official_schedule.argtypes = [ctypes.c_int, ctypes.c_int]
+    sched = take(lib, lib.iris_official_schedule(4, lh * lw), 5)
+    np.testing.assert_array_equal(sched, g["schedule"])
+    lib.iris_init_noise.argtypes = [ctypes.c_int] * 4 + [ctypes.c_int64]
+    z0 = take(lib, lib.iris_init_noise(1, 128, lh, lw, 42), n)
+    np.testing.assert_array_equal(z0, g["noise"])
+    txt = tl.synth_f32((T, td), 4243)
+    log(f"model ready {time.time() - t0:.1f} s; schedule {sched}")
+    z = z0.copy()
+    worst = 0.0
+    for i in range(4):
+        ref = g[f"velocity_{i}"]
+        got = take(lib, lib.iris_transformer_forward(tf, tl.fptr(z), lh, lw, tl.fptr(txt), T, F(sched[i])), n)
+        rel, cos = tl.rel_l2(got, ref), tl.cosine(got, ref)
+        worst = max(worst, rel)
+        log(f"step {i}: t={sched[i]:.6f} velocity rel_l2 {rel:.3e} cosine {cos:.6f}")
+        assert rel < 1e-2 and cos > 0.999, (i, rel, cos)
+        z = z + np.float32(sched[i + 1] - sched[i]) * ref
+    np.testing.assert_array_equal(z, g["final_latent"])
+    lib.iris_sample_euler.argtypes = [ctypes.c_void_p, ctypes.c_void_p, tl.FP, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, tl.FP, ctypes.c_int, tl.FP, ctypes.c_int,
+                                      ctypes.c_void_p]
+    zin = z0.copy()
+    got = take(lib, lib.iris_sample_euler(tf, None, tl.fptr(zin), 1, 128, lh, lw, tl.fptr(txt), T, tl.fptr(sched), 4,
+                                          None), n)
+    lib.iris_transformer_free(tf)
+    want = g["final_latent"]
+    rel, cos = tl.rel_l2(got, want), tl.cosine(got, want)
+    log(f"final latent after 4 steps: rel_l2 {rel:.3e} cosine {cos:.6f} (worst step velocity {worst:.3e})")
+    assert cos >= 0.999 and rel <= 1e-2
+
+
+def test_4b_multi_reference_forward(lib, orc):
+    """1 double + 2 single blocks at 4B widths; a 32x32 target plus two 32x32
+    reference latents with T offsets 1 and 2 (S = 512 + 3 x 1024)."""
+    seed = 77
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 2, 7680, 128, 3.0, 2000.0, seed))
+    m = ctypes.c_void_p(orc.orc_flux_create_synth(3072, 24, 1, 2, 7680, 128, 3.0, 2000.0, seed))
+    lat, txt = tl.synth_f32((128, 32, 32), 171), tl.synth_f32((512, 7680), 172)
+    r1, r2 = tl.synth_f32((128, 32, 32), 173), tl.synth_f32((128, 32, 32), 174)
+    refs = (tl.IrisRef * 2)(tl.IrisRef(tl.fptr(r1), 32, 32, 1), tl.IrisRef(tl.fptr(r2), 32, 32, 2))
+
+    class OrcRef(ctypes.Structure):
+        _fields_ = [("latent", tl.FP), ("h", ctypes.c_int), ("w", ctypes.c_int), ("t_offset", ctypes.c_int)]
+    orefs = (OrcRef * 2)(OrcRef(tl.fptr(r1), 32, 32, 1), OrcRef(tl.fptr(r2), 32, 32, 2))
+    n = 128 * 1024
+    got = take(lib, lib.iris_transformer_forward_with_multi_refs(tf, tl.fptr(lat), 32, 32, refs, 2, tl.fptr(txt), 512,
+                                                                 F(0.85)), n)
+    ref = tl.take_f32(orc, orc.orc_flux_forward_refs(m, tl.fptr(lat), 32, 32, orefs, 2, tl.fptr(txt), 512,
+                                                     F(0.85)), n)
+    plain = tl.take_f32(orc, orc.orc_flux_forward(m, tl.fptr(lat), 32, 32, tl.fptr(txt), 512, F(0.85)), n)
+    lib.iris_transformer_free(tf)
+    orc.orc_flux_free(m)
+    rel, cos = tl.rel_l2(got, ref), tl.cosine(got, ref)
+    log(f"4B multi-ref forward: rel_l2 {rel:.3e} cosine {cos:.6f}; the references move the velocity by "
+        f"{tl.rel_l2(ref, plain):.3e}")
+    assert rel < 1e-2 and cos > 0.999
+    # the references' own contribution, not only the shared part
+    assert tl.cosine(got - plain, ref - plain) > 0.99
+
+
+def test_zimage_full_width_blocks(lib, orc):
+    """Z-Image-Turbo widths (dim 3840, 30 heads, FFN 10240, caption 2560):
+    a noise refiner, a context refiner and a main layer, each on the same
+    resident input as the oracle's block, at a 64x64 latent (1024 image
+    tokens) with 300 caption tokens (padded to 320: masked keys)."""
+    d, Hh = 3840, 30
+    axes = (ctypes.c_int * 3)(32, 48, 48)
+    args = (d, Hh, 1, 1, 2560, 16, 2, F(256.0), axes, 10240, 1024, 9)
+    tf = ctypes.c_void_p(lib.zi_transformer_create_synthetic(*args))
+    m = ctypes.c_void_p(orc.orc_zi_create_synth(*args))
+    assert tf.value and m.value, lib.iris_hip_last_error()
+    lh = lw = 64
+    cap_len = 300
+    assert lib.zi_prepare(tf, lh, lw, cap_len) == 0
+    I, Ip, Cp = 1024, 1024, 320
+    U = Ip + Cp
+    pos = np.zeros((U, 3), np.int32)
+    pos[:I, 0], pos[:I, 1], pos[:I, 2] = Cp + 1, np.arange(I) // 32, np.arange(I) % 32
+    pos[Ip:, 0] = 1 + np.arange(Cp)
+    mask = np.zeros(U, np.int32)
+    mask[:I], mask[Ip:Ip + cap_len] = 1, 1
+    temb = tl.synth_f32((256,), 191)
+    xbuf, tbuf = lib.zi_device_buffer(tf, b"x"), lib.zi_device_buffer(tf, b"t_emb")
+    assert xbuf and tbuf
+    assert lib.iris_hip_memcpy_h2d(tbuf, temb.ctypes.data, temb.nbytes) == 0
+    for kind, (r0, r1), name in ((0, (0, Ip), "noise refiner"), (1, (Ip, U), "context refiner"),
+                                 (2, (0, U), "main layer")):
+        x = tl.synth_f32((U, d), 200 + kind)
+        assert lib.iris_hip_memcpy_h2d(xbuf, x.ctypes.data, x.nbytes) == 0
+        assert lib.zi_block_forward_resident(tf, kind, 0) == 0, lib.iris_hip_last_error()
+        got = tl.d2h_f32(lib, xbuf, (U, d))[r0:r1]
+        x0 = x[r0:r1].copy()
+        ref = x[r0:r1].copy()           # the oracle updates its rows in place
+        p = pos[r0:r1].copy()
+        mk = mask[r0:r1].copy()
+        orc.orc_zi_block(m, kind, 0, tl.fptr(ref), p.ctypes.data_as(tl.IP), mk.ctypes.data_as(tl.IP),
+                         tl.fptr(temb), r1 - r0)
+        rel, drel = tl.rel_l2(got, ref), tl.rel_l2(got - x0, ref - x0)
+        log(f"Z-Image {name}: rel_l2 {rel:.3e}, residual delta rel_l2 {drel:.3e}")
+        rows = mk.astype(bool)          # padding rows are computed but not compared by the model's output
+        assert tl.rel_l2(got[rows], ref[rows]) < 1e-2
+        assert tl.rel_l2((got - x0)[rows], (ref - x0)[rows]) < 3e-2
+    lib.zi_transformer_free(tf)
+    orc.orc_zi_free(m)

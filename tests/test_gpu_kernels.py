@@ -31,8 +31,8 @@ def run_gemm(lib, problems):
     assert lib.iris_hip_sync() == 0
 
 
-# The launcher picks a 256x256 or 288x192 block tile per launch from the tile
-# count; (4096, 4096) and (4608, 9216) take 256x256, the others 288x192.
+# One 256x256x64 block tile; the shapes cover partial row and column tiles,
+# N not a multiple of 4 or 64, K of one step and K up to 12288.
 @pytest.mark.parametrize("M,N,K", [(256, 256, 64), (384, 3072, 3072), (1000, 520, 128), (64, 27648, 256),
                                    (4608, 256, 12288), (17, 33 * 8, 192), (4096, 4096, 128), (4608, 3072, 1024),
                                    (4608, 9216, 192)])
@@ -323,6 +323,97 @@ def test_qk_prepare(lib, ktables):
     vref = tl.to_bf16(qkv[:, 2 * h:]).reshape(S, H, 128).transpose(1, 2, 0)
     np.testing.assert_array_equal(vt[:, :, :S], vref)
     assert np.all(vt[:, :, S:] == 0)
+
+
+def norm_rope_ref(x, w, cos, sin, eps=1e-6):
+    """float64 RMSNorm over 128 dims x w, then rotation of the pairs (2i, 2i+1)"""
+    n = x / np.sqrt((x ** 2).mean(1, keepdims=True) + eps) * w
+    r0 = n[:, 0::2] * cos[:, 0::2] - n[:, 1::2] * sin[:, 0::2]
+    r1 = n[:, 1::2] * cos[:, 0::2] + n[:, 0::2] * sin[:, 0::2]
+    return np.stack([r0, r1], 2).reshape(x.shape[0], 128)
+
+
+@pytest.mark.parametrize("S,H,kvh,period", [(200, 3, 3, 0), (130, 8, 2, 0), (300, 2, 2, 150)])
+def test_kv_prepare(lib, S, H, kvh, period):
+    """K RMSNorm + rotary (set A below split, per row % period) and V^T with
+    the padding columns zero-filled, K-side tables when given."""
+    rng = np.random.default_rng(S + kvh)
+    qd, kd = H * 128, kvh * 128
+    ld = qd + 2 * kd
+    split = 60
+    qkv = rng.standard_normal((S, ld), np.float32)
+    wkA, wkB = (1 + 0.1 * rng.standard_normal(128).astype(np.float32) for _ in range(2))
+    rows_t = period or S
+    ang = rng.uniform(-3, 3, (rows_t, 64)).astype(np.float32)
+    cos = np.repeat(np.cos(ang), 2, 1).astype(np.float32)
+    sin = np.repeat(np.sin(ang), 2, 1).astype(np.float32)
+    S_pad = (S + 63) // 64 * 64
+    k, vt = tl.Dev(S * kd * 2), tl.Dev(kvh * 128 * S_pad * 2)
+    vt.put(np.full(kvh * 128 * S_pad, 0x7FC0, np.uint16))     # poison: padding must be rewritten
+    dqkv, dc, ds, da, db = (tl.Dev.of(v) for v in (tl.to_bf16(qkv), cos, sin, wkA, wkB))
+    a = tl.QkPrepArgs(dqkv.ptr, ld, qd, qd + kd, None, k.ptr, vt.ptr, S_pad, S, H, None, da.ptr, None, db.ptr,
+                      split, dc.ptr, ds.ptr, period, 1e-6, kvh if kvh != H else 0, None, None)
+    assert lib.iris_hip_kv_prepare(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    x = bf(qkv).astype(np.float64)
+    got = tl.bf16_to_f32(k.get(np.uint16, (S, kd)))
+    prow = np.arange(S) % period if period else np.arange(S)
+    w = np.where(prow[:, None] < split, wkA, wkB)
+    for hh in range(kvh):
+        ref = norm_rope_ref(x[:, qd + hh * 128: qd + (hh + 1) * 128], w, cos[prow], sin[prow])
+        assert tl.rel_l2(got[:, hh * 128:(hh + 1) * 128], ref) < 4e-3, hh
+    v = vt.get(np.uint16, (kvh, 128, S_pad))
+    np.testing.assert_array_equal(v[:, :, :S], tl.to_bf16(qkv[:, qd + kd:]).reshape(S, kvh, 128).transpose(1, 2, 0))
+    assert np.all(v[:, :, S:] == 0)
+
+
+@pytest.mark.parametrize("S,H,batch,split,rope,causal,group", [
+    (4608, 2, 1, 512, True, 0, 0), (700, 3, 2, 100, True, 0, 0), (333, 2, 1, 333, False, 0, 0),
+    (300, 4, 1, 300, True, 1, 2), (65, 2, 1, 10, True, 0, 0)])
+def test_flash_attention_fused_q(lib, S, H, batch, split, rope, causal, group):
+    """Q prologue: the raw projection rows (bf16, inside a [q | k | v] row of
+    stride ld_q) RMS-normalised with weight set A below split and B above,
+    rotated by the per-pair RoPE tables, then attention; against float64
+    numpy of the normalised, rotated Q."""
+    rng = np.random.default_rng(S * 3 + H)
+    kvh = H // group if group else H
+    hd, kd = H * 128, kvh * 128
+    ld = hd + 2 * kd
+    S_pad = (S + 63) // 64 * 64
+    raw = rng.standard_normal((batch, S, ld), np.float32)
+    k = rng.standard_normal((batch, S, kd), np.float32)
+    v = rng.standard_normal((batch, S, kd), np.float32)
+    wA, wB = (1 + 0.3 * rng.standard_normal(128).astype(np.float32) for _ in range(2))
+    ang = rng.uniform(-3, 3, (S, 64)).astype(np.float32)
+    cos = np.repeat(np.cos(ang), 2, 1).astype(np.float32) if rope else np.ones((S, 128), np.float32)
+    sin = np.repeat(np.sin(ang), 2, 1).astype(np.float32) if rope else np.zeros((S, 128), np.float32)
+    vt = np.zeros((batch, kvh, 128, S_pad), np.float32)
+    for b in range(batch):
+        for h in range(kvh):
+            vt[b, h, :, :S] = v[b, :, h * 128:(h + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(raw)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    # the kernel reads one value per rotation pair: [S][64]
+    dwa, dwb = tl.Dev.of(wA), tl.Dev.of(wB)
+    dc, dsn = tl.Dev.of(np.ascontiguousarray(cos[:, 0::2])), tl.Dev.of(np.ascontiguousarray(sin[:, 0::2]))
+    do = tl.Dev(batch * S * hd * 2)
+    a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, do.ptr, ld, kd, S_pad, hd, S, S, H, batch, S * ld, S * kd,
+                    kvh * 128 * S_pad, S * hd, 1 / math.sqrt(128), 0, S, 0, 0, causal, group, 0, 0.0,
+                    dwa.ptr, dwb.ptr, split, 1e-6, dc.ptr if rope else None, dsn.ptr if rope else None)
+    assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    got = tl.bf16_to_f32(do.get(np.uint16, (batch, S, hd)))
+    w = np.where(np.arange(S)[:, None] < split, wA, wB)
+    allowed = np.tril(np.ones((S, S), bool)) if causal else np.ones((S, S), bool)
+    for b in range(batch):
+        x = bf(raw[b]).astype(np.float64)
+        for h in range(H):
+            kl = slice((h // (group or 1)) * 128, (h // (group or 1) + 1) * 128)
+            q = norm_rope_ref(x[:, h * 128:(h + 1) * 128], w, cos, sin)
+            sc = q @ bf(k[b][:, kl]).astype(np.float64).T / math.sqrt(128)
+            sc = np.where(allowed, sc, -np.inf)
+            p = np.exp(sc - sc.max(1, keepdims=True))
+            ref = (p / p.sum(1, keepdims=True)) @ bf(v[b][:, kl]).astype(np.float64)
+            assert tl.rel_l2(got[b, :, h * 128:(h + 1) * 128], ref) < 1e-2, (b, h)
 
 
 @pytest.mark.parametrize("N,K,act", [(18432, 3072, 1), (3072, 256, 0), (100, 3840, 1)])
