@@ -81,6 +81,18 @@ int iris_hip_gemm(const iris_gemm_problem_t *problems, int n_problems);
  * kernel sums the chunks in order (deterministic) and applies the epilogue. */
 int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *d_workspace, size_t workspace_bytes);
 
+/* No counterpart in the reference. iris_hip_gemm_splitk without a
+ * workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * f32 partials go to a device array the library holds, of
+ * IRIS_NOALLOC_SCRATCH_BYTES per GPU, kept until the process ends. Calls no
+ * allocating routine. Rejects problems whose chunks x M x N f32 partials
+ * exceed the array (error, -1). Every call on one GPU shares its array:
+ * calls that overlap on one GPU race. Results equal iris_hip_gemm_splitk's
+ * bit for bit. */
+#define IRIS_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int iris_hip_gemm_splitk_noalloc(const iris_gemm_problem_t *problem, int splits);
+
 /* 3x3 convolution, stride 1, zero padding 1, as an implicit GEMM on the MFMA
  * kernel above (replaces vae_conv2d -> iris_conv2d for the 3x3 convolutions,
  * iris_vae.c:148-166, iris_kernels.c:363): the A tiles are gathered from the

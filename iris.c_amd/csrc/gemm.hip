@@ -36,6 +36,7 @@
  */
 #include "iris_internal.h"
 
+#include <mutex>
 #include <string.h>
 
 namespace {
@@ -505,6 +506,55 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     P.per_xcd = (total + 7) / 8;
     hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
+}
+
+/* Split-K partials without a caller workspace: a file-scope device array of
+ * IRIS_NOALLOC_SCRATCH_BYTES, held by each GPU the library runs on until the
+ * process ends. Host code never passes the array's name to a kernel (on the
+ * host it is a stand-in, not a device address): its device address is looked
+ * up once per device with hipGetSymbolAddress and kept per device. Every
+ * call on a GPU shares that GPU's array, so calls that overlap on one GPU
+ * (different streams, threads) race. Each chunk's partial overwrites its
+ * whole M x N region, so nothing is cleared between calls. */
+__device__ __align__(256) float scratch[IRIS_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+void *g_scratch_ptr[MAX_DEVICES];
+std::mutex g_scratch_mutex;
+
+float *scratch_ptr() {
+    int dev = -1;
+    if (iris_check(hipGetDevice(&dev), "noalloc: hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= MAX_DEVICES) {
+        iris_set_error("noalloc: device %d outside 0..%d", dev, MAX_DEVICES - 1);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        if (iris_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "noalloc: hipGetSymbolAddress")) return nullptr;
+        g_scratch_ptr[dev] = ptr;
+    }
+    return (float *)g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int iris_hip_gemm_splitk_noalloc(const iris_gemm_problem_t *p, int splits) {
+    if (!p) return iris_set_error("gemm_splitk_noalloc: null problem");
+    if (splits <= 1) return iris_hip_gemm(p, 1);
+    if (p->M <= 0 || p->N <= 0) return 0;
+    if (check_problem(*p)) return -1;
+    const int nk = p->K / BK;
+    const int kchunk = (nk + splits - 1) / splits * BK;
+    const size_t chunks = (size_t)((p->K + kchunk - 1) / kchunk);
+    const size_t need = chunks * (size_t)p->M * (size_t)p->N * sizeof(float);
+    if (need > IRIS_NOALLOC_SCRATCH_BYTES)
+        return iris_set_error("gemm_splitk_noalloc: %zu chunks x %d x %d f32 partials need %zu bytes, the scratch "
+                              "holds %zu", chunks, p->M, p->N, need, (size_t)IRIS_NOALLOC_SCRATCH_BYTES);
+    float *ws = scratch_ptr();
+    if (!ws) return -1;
+    return iris_hip_gemm_splitk(p, splits, ws, IRIS_NOALLOC_SCRATCH_BYTES);
 }
 
 extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, float *ws, size_t ws_bytes) {
