@@ -7,12 +7,14 @@
  *   rms_gated_add  Z-Image x += gate * RMSNorm(y) (:818-836)
  *   qk_prepare     apply_qk_norm + apply_rope_2d (:1464-1518, :1026-1048),
  *                  zi_qk_norm + zi_apply_rope (zimage :620-682), and the
- *                  transposed V layout the attention kernel reads
+ *                  transposed V layout the attention kernel reads; the K
+ *                  and V half alone for attention calls that normalise Q in
+ *                  their prologue
  *   gemv           timestep MLP and modulation (:1366-1379, :4059-4069)
  *   layout         NCHW -> tokens (:3986-3993), patchify (zimage :1634-1684),
  *                  f32 <-> bf16, Euler update (iris_sample.c:359, :472-474)
- * One wave per row for the row kernels (wave-shuffle reductions, no block
- * barriers); float4 / 16-byte accesses throughout.
+ * One block per row for the normalisations, one wave per row for the other
+ * row kernels; float4 / 16-byte accesses throughout.
  */
 #include "iris_internal.h"
 
@@ -20,72 +22,87 @@ namespace {
 
 constexpr int NT = 256;
 
-/* One wave per row: lane owns float4 columns lane, lane + 64, ... (V of them),
- * so both reductions are wave shuffles with no block barrier. */
-template <int V>
+/* One block of 256 threads per row: thread t owns float4 columns t, t + 256,
+ * ... (V of them); each reduction is a wave shuffle plus a 4-entry LDS sum.
+ * A wave per row leaves each wave a long chain (load, two reductions, store)
+ * over 12 KB; spreading the row over four waves shortens it and keeps more
+ * rows' loads in flight (5.5 TB/s against 4.8 for wave-per-row at
+ * 4608 x 3072 f32 -> bf16). */
+template <int V, int MODE>
 __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
-    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= a.rows) return;
+    __shared__ float red[2][NT / IRIS_WAVE];
+    const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
     const float *x = a.x + (size_t)row * a.ldx;
     const int nv = a.cols >> 2;
     float4 v[V];
-    float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = lane + i * IRIS_WAVE;
+        const int c = t + i * NT;
         v[i] = c < nv ? ((const float4 *)x)[c] : make_float4(0, 0, 0, 0);
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
     const bool use_b = (a.period ? row % a.period : row) >= a.split;
     const float *shift = use_b ? a.shiftB : a.shiftA;
     const float *scale = use_b ? a.scaleB : a.scaleA;
     const float *w = use_b ? a.wB : a.wA;
+    auto block_sum = [&](float q, int k) {
+        q = wave_sum(q);
+        if (lane == 0) red[k][wv] = q;
+        __syncthreads();
+        return (red[k][0] + red[k][1]) + (red[k][2] + red[k][3]);
+    };
     float mean = 0.0f, inv;
-    if (a.mode == IRIS_NORM_RMS) {
+    if (MODE == IRIS_NORM_RMS) {
         float q = 0.0f;
 #pragma unroll
         for (int i = 0; i < V; i++) q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-        inv = 1.0f / sqrtf(wave_sum(q) / a.cols + a.eps);
+        inv = 1.0f / sqrtf(block_sum(q, 0) / a.cols + a.eps);
     } else {
-        mean = wave_sum(s) / a.cols;
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < V; i++) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+        mean = block_sum(s, 0) / a.cols;
         float q = 0.0f;
 #pragma unroll
         for (int i = 0; i < V; i++) {
-            const int c = lane + i * IRIS_WAVE;
+            const int c = t + i * NT;
             if (c < nv) {
                 float d0 = v[i].x - mean, d1 = v[i].y - mean, d2 = v[i].z - mean, d3 = v[i].w - mean;
                 q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
             }
         }
-        inv = 1.0f / sqrtf(wave_sum(q) / a.cols + a.eps);
+        inv = 1.0f / sqrtf(block_sum(q, 1) / a.cols + a.eps);
     }
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = lane + i * IRIS_WAVE;
+        const int c = t + i * NT;
         if (c >= nv) continue;
         float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
         float y[4];
         float4 sc4 = make_float4(0, 0, 0, 0), sh4 = make_float4(0, 0, 0, 0), w4 = make_float4(1, 1, 1, 1);
-        if (scale) sc4 = ((const float4 *)scale)[c];
-        if (a.mode == IRIS_NORM_LN_MOD) sh4 = ((const float4 *)shift)[c];
-        if (a.mode == IRIS_NORM_RMS) w4 = ((const float4 *)w)[c];
+        if (MODE == IRIS_NORM_LN_MOD) {
+            sc4 = ((const float4 *)scale)[c];
+            sh4 = ((const float4 *)shift)[c];
+        } else {
+            if (scale) sc4 = ((const float4 *)scale)[c];
+            if (MODE == IRIS_NORM_RMS) w4 = ((const float4 *)w)[c];
+        }
         const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w}, sh[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
         const float ww[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            if (a.mode == IRIS_NORM_LN_MOD) {
+            if (MODE == IRIS_NORM_LN_MOD) {
                 const float n = (e[j] - mean) * inv;
                 y[j] = (1.0f + sc[j]) * n + sh[j];
-            } else if (a.mode == IRIS_NORM_LN_SCALE) {
+            } else if (MODE == IRIS_NORM_LN_SCALE) {
                 y[j] = (e[j] - mean) * inv * sc[j];
             } else {
-                float t = e[j] * inv * ww[j];
-                if (scale) t *= sc[j];
-                y[j] = t;
+                float tt = e[j] * inv * ww[j];
+                if (scale) tt *= sc[j];
+                y[j] = tt;
             }
         }
         if (a.out_bf16) {
-            u16x4 o = {f2bf(y[0]), f2bf(y[1]), f2bf(y[2]), f2bf(y[3])};
+            u16x4 o = {f2bf_hw(y[0]), f2bf_hw(y[1]), f2bf_hw(y[2]), f2bf_hw(y[3])};
             *(u16x4 *)((uint16_t *)a.out + (size_t)row * a.ldo + 4 * c) = o;
         } else {
             *(float4 *)((float *)a.out + (size_t)row * a.ldo + 4 * c) = make_float4(y[0], y[1], y[2], y[3]);
@@ -93,12 +110,13 @@ __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
     }
 }
 
+/* x += g * RMSNorm(y) * w, one block of 256 threads per row (as rownorm). */
 template <int V>
 __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float *y, const float *w,
                                                            const float *gate, int rows, int cols, float eps,
                                                            int gate_tanh) {
-    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= rows) return;
+    __shared__ float red[NT / IRIS_WAVE];
+    const int row = blockIdx.x, t = threadIdx.x, wv = t >> 6, lane = t & 63;
     const int nv = cols >> 2;
     const float *yr = y + (size_t)row * cols;
     float *xr = x + (size_t)row * cols;
@@ -106,14 +124,17 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = lane + i * IRIS_WAVE;
+        const int c = t + i * NT;
         v[i] = c < nv ? ((const float4 *)yr)[c] : make_float4(0, 0, 0, 0);
         q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
-    const float inv = 1.0f / sqrtf(wave_sum(q) / cols + eps);
+    q = wave_sum(q);
+    if (lane == 0) red[wv] = q;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / cols + eps);
 #pragma unroll
     for (int i = 0; i < V; i++) {
-        const int c = lane + i * IRIS_WAVE;
+        const int c = t + i * NT;
         if (c >= nv) continue;
         float4 xo = ((float4 *)xr)[c];
         const float4 w4 = ((const float4 *)w)[c];
@@ -133,7 +154,9 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
 
 /* One wave per row: 16 lanes per head, lane owns dims d0..d0+7 (four rotation
  * pairs); a 16-byte load covers 4 heads per wave, the head's sum of squares is
- * a 16-lane shuffle reduction. */
+ * a 16-lane shuffle reduction. The row's table values are loaded once for all
+ * its heads. KONLY: K alone (Q is normalised in the attention prologue). */
+template <bool KONLY>
 __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args_t a) {
     const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= a.rows) return;
@@ -153,7 +176,7 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
         for (int j = 0; j < 8; j++) { c[j] = 1.0f; sn[j] = 0.0f; }
     }
 #pragma unroll
-    for (int which = 0; which < 2; which++) {
+    for (int which = KONLY ? 1 : 0; which < 2; which++) {
         if (which && a.kcos_t) {   /* K-side tables (reference-key band control) */
             const float4 c0 = *(const float4 *)(a.kcos_t + (size_t)prow * 128 + d0);
             const float4 c1 = *(const float4 *)(a.kcos_t + (size_t)prow * 128 + d0 + 4);
@@ -199,74 +222,6 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
 __global__ __launch_bounds__(NT) void v_transpose_kernel(const iris_qkprep_args_t a) {
     __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
     const int r0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
-#pragma unroll
-    for (int it = 0; it < 2; it++) {                       /* 32 row pairs x 16 chunks of 8 dims */
-        const int item = tid + NT * it, p = item >> 4, ch = item & 15;
-        const int ra = r0 + 2 * p;
-        const uint16_t *src = a.qkv + (size_t)ra * a.ld_qkv + a.col_v + head * 128 + ch * 8;
-        u16x8 va = {0, 0, 0, 0, 0, 0, 0, 0}, vb = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (ra < a.rows) va = *(const u16x8 *)src;
-        if (ra + 1 < a.rows) vb = *(const u16x8 *)(src + a.ld_qkv);
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int d = ch * 8 + j;
-            const int col = (2 * p) ^ (((d >> 3) & 7) << 3);
-            *(uint32_t *)(&t[d * 72 + col]) = (uint32_t)va[j] | ((uint32_t)vb[j] << 16);
-        }
-    }
-    __syncthreads();
-    uint16_t *dst = a.vt_out + (size_t)head * 128 * a.ld_vt + r0;
-#pragma unroll
-    for (int it = 0; it < 4; it++) {                       /* 128 d x 8 chunks of 8 rows */
-        const int item = tid + NT * it, d = item >> 3, c8 = item & 7;
-        const uint4 v = *(const uint4 *)(&t[d * 72 + ((c8 ^ ((d >> 3) & 7)) << 3)]);
-        *(uint4 *)(dst + (size_t)d * a.ld_vt + c8 * 8) = v;
-    }
-}
-
-/* K RMSNorm + RoPE and V^T of one 64-row block of one K / V head. K: 16
- * lanes per row, 8 dims per lane (a 16-byte load and store), the row's sum
- * of squares a 16-lane shuffle reduction; V: through LDS as in
- * v_transpose_kernel. Rows past the end are written as zeros in V^T. */
-__global__ __launch_bounds__(NT) void kv_prepare_kernel(const iris_qkprep_args_t a) {
-    __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
-    const int r0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
-    const int kvh = a.kv_heads ? a.kv_heads : a.heads;
-    const int d0 = (tid & 15) * 8;
-#pragma unroll
-    for (int it = 0; it < 4; it++) {
-        const int row = r0 + it * 16 + (tid >> 4);
-        if (row >= a.rows) break;                          /* uniform per 16-lane row group */
-        const int prow = a.period ? row % a.period : row;
-        const u16x8 raw = *(const u16x8 *)(a.qkv + (size_t)row * a.ld_qkv + a.col_k + head * 128 + d0);
-        float x[8], ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[j]); ss += x[j] * x[j]; }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
-        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
-        const float *w = prow >= a.split ? a.wkB : a.wkA;
-        const float4 w0 = *(const float4 *)(w + d0), w1 = *(const float4 *)(w + d0 + 4);
-        const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        float c[8] = {1, 1, 1, 1, 1, 1, 1, 1}, sn[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        const float *ct = a.kcos_t ? a.kcos_t : a.cos_t, *st = a.kcos_t ? a.ksin_t : a.sin_t;
-        if (ct) {
-            const float4 c0 = *(const float4 *)(ct + (size_t)prow * 128 + d0);
-            const float4 c1 = *(const float4 *)(ct + (size_t)prow * 128 + d0 + 4);
-            const float4 s0 = *(const float4 *)(st + (size_t)prow * 128 + d0);
-            const float4 s1 = *(const float4 *)(st + (size_t)prow * 128 + d0 + 4);
-            c[0] = c0.x; c[2] = c0.z; c[4] = c1.x; c[6] = c1.z;
-            sn[0] = s0.x; sn[2] = s0.z; sn[4] = s1.x; sn[6] = s1.z;
-        }
-        u16x8 out;
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-            const float x0 = x[j] * inv * ww[j], x1 = x[j + 1] * inv * ww[j + 1];
-            out[j] = f2bf(x0 * c[j] - x1 * sn[j]);
-            out[j + 1] = f2bf(x1 * c[j] + x0 * sn[j]);
-        }
-        *(u16x8 *)(a.k_out + (size_t)row * kvh * 128 + head * 128 + d0) = out;
-    }
 #pragma unroll
     for (int it = 0; it < 2; it++) {                       /* 32 row pairs x 16 chunks of 8 dims */
         const int item = tid + NT * it, p = item >> 4, ch = item & 15;
@@ -423,46 +378,57 @@ __global__ void merge_rows_kernel(uint16_t *W, int cols, const int *rowmap, cons
 
 extern "C" {
 
-#define IRIS_ROWS_V(KERNEL, v, grid, ...)                                                                  \
-    do {                                                                                                   \
-        switch (v) {                                                                                       \
-        case 1: hipLaunchKernelGGL(KERNEL<1>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
-        case 2: hipLaunchKernelGGL(KERNEL<2>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
-        case 4: hipLaunchKernelGGL(KERNEL<4>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
-        case 8: hipLaunchKernelGGL(KERNEL<8>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;       \
-        case 10: hipLaunchKernelGGL(KERNEL<10>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
-        case 12: hipLaunchKernelGGL(KERNEL<12>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
-        case 16: hipLaunchKernelGGL(KERNEL<16>, grid, dim3(NT), 0, iris_stream(), __VA_ARGS__); break;     \
-        default: return iris_set_error(#KERNEL ": unsupported width");                                     \
-        }                                                                                                  \
-    } while (0)
-
-/* float4 columns per lane: the smallest instantiated count covering cols */
-static int lanes_v(int cols) {
-    const int need = (cols / 4 + IRIS_WAVE - 1) / IRIS_WAVE;
-    static const int vs[] = {1, 2, 4, 8, 10, 12, 16};
-    for (int v : vs)
-        if (v >= need) return v;
-    return 0;
-}
-
 int iris_hip_rownorm(const iris_norm_args_t *a) {
     if (a->rows <= 0) return 0;
-    const int v = lanes_v(a->cols);
-    if (a->cols % 4 || !v) return iris_set_error("rownorm: cols=%d", a->cols);
+    /* float4 columns per thread of a 256-thread block */
+    const int need = (a->cols / 4 + NT - 1) / NT;
+    static const int vs[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    int v = 0;
+    for (int c : vs)
+        if (!v && c >= need) v = c;
+    if (a->cols % 4 || a->cols <= 0 || !v) return iris_set_error("rownorm: cols=%d", a->cols);
     if (a->ldx % 4 || a->ldo % 4) return iris_set_error("rownorm: ld must be multiple of 4");
-    const dim3 grid((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE));
-    IRIS_ROWS_V(rownorm_kernel, v, grid, *a);
+    if (a->mode < IRIS_NORM_LN_MOD || a->mode > IRIS_NORM_RMS) return iris_set_error("rownorm: mode %d", a->mode);
+    /* a set that no row selects may be left NULL: it stands in for the other */
+    iris_norm_args_t b = *a;
+    const bool only_a = !b.period && b.split >= b.rows, only_b = !b.period && b.split <= 0;
+    if (only_a) { b.shiftB = b.shiftA; b.scaleB = b.scaleA; b.wB = b.wA; }
+    if (only_b) { b.shiftA = b.shiftB; b.scaleA = b.scaleB; b.wA = b.wB; }
+    if (b.mode == IRIS_NORM_LN_MOD && (!b.scaleA || !b.shiftA || !b.scaleB || !b.shiftB))
+        return iris_set_error("rownorm: LN_MOD needs scale and shift for the row sets in use");
+    if (b.mode == IRIS_NORM_RMS && (!b.wA || !b.wB)) return iris_set_error("rownorm: RMS needs weights");
+    if (b.mode == IRIS_NORM_LN_SCALE && (!b.scaleA || !b.scaleB)) return iris_set_error("rownorm: LN_SCALE needs scales");
+    const dim3 grid(a->rows);
+#define ROWNORM_CASE(VV)                                                                                          \
+    case VV:                                                                                                      \
+        if (a->mode == IRIS_NORM_LN_MOD)                                                                          \
+            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_LN_MOD>), grid, dim3(NT), 0, iris_stream(), b);      \
+        else if (a->mode == IRIS_NORM_LN_SCALE)                                                                   \
+            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_LN_SCALE>), grid, dim3(NT), 0, iris_stream(), b);    \
+        else                                                                                                      \
+            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_RMS>), grid, dim3(NT), 0, iris_stream(), b);         \
+        break;
+    switch (v) {
+        ROWNORM_CASE(1) ROWNORM_CASE(2) ROWNORM_CASE(3) ROWNORM_CASE(4)
+        ROWNORM_CASE(6) ROWNORM_CASE(8) ROWNORM_CASE(12) ROWNORM_CASE(16)
+    }
+#undef ROWNORM_CASE
     return iris_launch_check("rownorm_kernel");
 }
 
 int iris_hip_rms_gated_add(float *x, const float *y, const float *w, const float *gate, int rows, int cols,
                            float eps, int gate_tanh) {
     if (rows <= 0) return 0;
-    const int v = lanes_v(cols);
-    if (cols % 4 || !v) return iris_set_error("rms_gated_add: cols=%d", cols);
-    const dim3 grid((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE));
-    IRIS_ROWS_V(rms_gated_add_kernel, v, grid, x, y, w, gate, rows, cols, eps, gate_tanh);
+    const int need = (cols / 4 + NT - 1) / NT;
+    if (cols % 4 || cols <= 0 || need > 16) return iris_set_error("rms_gated_add: cols=%d", cols);
+    const dim3 grid(rows);
+    switch (need) {
+    case 1: hipLaunchKernelGGL(rms_gated_add_kernel<1>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 2: hipLaunchKernelGGL(rms_gated_add_kernel<2>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 3: hipLaunchKernelGGL(rms_gated_add_kernel<3>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 4: hipLaunchKernelGGL(rms_gated_add_kernel<4>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    default: hipLaunchKernelGGL(rms_gated_add_kernel<16>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    }
     return iris_launch_check("rms_gated_add_kernel");
 }
 
@@ -474,7 +440,7 @@ int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
         return iris_set_error("qk_prepare: heads=%d kv_heads=%d", a->heads, a->kv_heads);
     if (((uintptr_t)a->qkv | (uintptr_t)a->q_out | (uintptr_t)a->k_out | (uintptr_t)a->vt_out) & 15)
         return iris_set_error("qk_prepare: buffers must be 16-byte aligned");
-    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+    hipLaunchKernelGGL(qk_norm_rope_kernel<false>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
                        iris_stream(), *a);
     if (iris_launch_check("qk_norm_rope_kernel")) return -1;
     const int kvh = a->kv_heads ? a->kv_heads : a->heads;
@@ -493,8 +459,11 @@ int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
          (uintptr_t)a->cos_t | (uintptr_t)a->sin_t | (uintptr_t)a->kcos_t | (uintptr_t)a->ksin_t) & 15)
         return iris_set_error("kv_prepare: buffers must be 16-byte aligned");
     const int kvh = a->kv_heads ? a->kv_heads : a->heads;
-    hipLaunchKernelGGL(kv_prepare_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
-    return iris_launch_check("kv_prepare_kernel");
+    hipLaunchKernelGGL(qk_norm_rope_kernel<true>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+                       iris_stream(), *a);
+    if (iris_launch_check("qk_norm_rope_kernel<K>")) return -1;
+    hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
+    return iris_launch_check("v_transpose_kernel");
 }
 
 int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias, int N, int K, int act_in) {
