@@ -69,6 +69,12 @@ typedef struct {
     int M, N, K;         /* K % 64 == 0                             */
     int lda, ldw, ldo;
     int epi;
+    /* optional second K segment accumulated into the same product (K2 = 0:
+     * none; K2 % 64 == 0): out = A W^T + A2 W2^T with A2 bf16 [M][lda2] and
+     * W2 bf16 [N][ldw2]. A low-rank adapter runs as [x | x A^T] [W | s B]^T,
+     * in f32 accumulation before the epilogue. Not for split-K. */
+    const uint16_t *A2, *W2;
+    int K2, lda2, ldw2;
 } iris_gemm_problem_t;
 
 /* Up to 4 independent problems in one launch (e.g. the txt and img streams). */
@@ -120,11 +126,6 @@ typedef struct {
     size_t ws_bytes;
 } iris_conv3x3_t;
 int iris_hip_conv3x3(const iris_conv3x3_t *c);
-
-/* LoRA merge (lora_apply's out += scale * B (A x), iris_lora.c:43-90, folded
- * into the weights): W[rowmap[o]][i] = bf16(W + scale * dW[o][i]), W bf16
- * [.][cols], dW f32 [rows][cols], rowmap device int [rows]. */
-int iris_hip_merge_rows(uint16_t *d_W, int cols, const int *d_rowmap, const float *d_dW, int rows, float scale);
 
 /* ---- VAE decoder kernels (vae.hip), channels-last (NHWC) activations ---- */
 /* GroupNorm (iris_group_norm, iris_kernels.c:542) in three launches:

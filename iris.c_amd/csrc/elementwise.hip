@@ -362,17 +362,6 @@ int grid1d(size_t n) {
 }
 
 
-/* W[rowmap[o]][i] = bf16(W[rowmap[o]][i] + scale * dW[o][i]): a low-rank
- * adapter's product merged into resident bf16 weights (rows mapped into the
- * fused / interleaved layouts). */
-__global__ void merge_rows_kernel(uint16_t *W, int cols, const int *rowmap, const float *dW, int rows, float scale) {
-    const size_t n = (size_t)rows * cols;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (size_t)gridDim.x * blockDim.x) {
-        const int o = (int)(e / cols), c = (int)(e % cols);
-        uint16_t *w = W + (size_t)rowmap[o] * cols + c;
-        *w = f2bf(bf2f(*w) + scale * dW[e]);
-    }
-}
 
 }  // namespace
 
@@ -537,10 +526,3 @@ int iris_hip_copy_rows(float *dst, int ld_dst, const float *src, int ld_src, int
 
 }  /* extern "C" */
 
-extern "C" int iris_hip_merge_rows(uint16_t *W, int cols, const int *rowmap, const float *dW, int rows, float scale) {
-    if (!W || !rowmap || !dW || rows <= 0 || cols <= 0) return iris_set_error("merge_rows: bad arguments");
-    const size_t n = (size_t)rows * cols;
-    const unsigned blocks = (unsigned)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536);
-    hipLaunchKernelGGL(merge_rows_kernel, dim3(blocks), dim3(256), 0, iris_stream(), W, cols, rowmap, dW, rows, scale);
-    return iris_launch_check("merge_rows_kernel");
-}

@@ -79,12 +79,13 @@ constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 1
 typedef __attribute__((address_space(3))) void lds_void;
 
 /* MODE 0: GEMM; 1: 3x3 convolution, stride 1, input optionally read through
- * a nearest 2x upsample; 2: 3x3 convolution, stride 2, right/bottom padding.
- * The modes are separate kernels: the load-issue phase has no cycles to
- * spare for the address arithmetic of the modes it does not run. */
+ * a nearest 2x upsample; 2: 3x3 convolution, stride 2, right/bottom padding;
+ * 3: GEMM with a second K segment (A2, W2) after the first. The modes are
+ * separate kernels: the load-issue phase has no cycles to spare for the
+ * address arithmetic of the modes it does not run. */
 template <int MODE>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
-    constexpr bool CONV = MODE != 0;
+    constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3;
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
      * the other */
@@ -155,6 +156,19 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         a_chunk[par] = c * 16;
     }
     const int a_step = DMA_ROWS * pr.lda * 2, w_step = DMA_ROWS * pr.ldw * 2;
+    /* second segment (MODE 3): the same lane layout over A2 / W2; a lane's
+     * offset there is its first-segment offset + row * (ld2 - ld) * 2, formed
+     * at each load from scalars chosen by the K step, so the two segments
+     * share one load sequence and no registers are held for the second */
+    const int nk1 = pr.K / BK;
+    const int dma_row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
+    __amdgpu_buffer_rsrc_t a2_rsrc = a_rsrc, w2_rsrc = w_rsrc;
+    if (SEG2) {
+        a2_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)(pr.A2 + (size_t)m0 * pr.lda2), (short)0,
+                                                    a_rows * pr.lda2 * 2, 0x00020000);
+        w2_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)(pr.W2 + (size_t)n0 * pr.ldw2), (short)0,
+                                                    w_rows * pr.ldw2 * 2, 0x00020000);
+    }
     /* convolution: the output pixel of each row this lane loads, y << 16 | x;
      * rows past M get y = 0x4000, outside every image */
     uint32_t pix[DMA_PER_WAVE];
@@ -189,6 +203,15 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
                                                          ok ? src : (int)0x80000000u, soff, 0, 0);
             }
+        } else if (SEG2) {
+            const bool s2 = kt >= nk1;
+            const __amdgpu_buffer_rsrc_t r = s2 ? a2_rsrc : a_rsrc;
+            const int extra = s2 ? dma_row * ((pr.lda2 - pr.lda) * 2) : 0;
+            const int step = s2 ? DMA_ROWS * pr.lda2 * 2 : a_step, ks = (s2 ? kt - nk1 : kt) * BK * 2;
+#pragma unroll
+            for (int i = 0; i < DMA_PER_WAVE; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
+                                                         a_voff[i & 1] + extra + i * step, ks, 0, 0);
         } else {
 #pragma unroll
             for (int i = 0; i < DMA_PER_WAVE; i++)
@@ -197,10 +220,23 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         }
     };
     auto dma_w = [&](uint16_t *stage, int kt) {
+        if (SEG2) {
+            const bool s2 = kt >= nk1;
+            const __amdgpu_buffer_rsrc_t r = s2 ? w2_rsrc : w_rsrc;
+            const int extra = s2 ? dma_row * ((pr.ldw2 - pr.ldw) * 2) : 0;
+            const int step = s2 ? DMA_ROWS * pr.ldw2 * 2 : w_step, ks = (s2 ? kt - nk1 : kt) * BK * 2;
 #pragma unroll
-        for (int i = 0; i < DMA_PER_WAVE; i++)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512), 16,
-                                                     w_voff[i & 1] + i * w_step, kt * BK * 2, 0, 0);
+            for (int i = 0; i < DMA_PER_WAVE; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r,
+                                                         (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512),
+                                                         16, w_voff[i & 1] + extra + i * step, ks, 0, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < DMA_PER_WAVE; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc,
+                                                         (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512),
+                                                         16, w_voff[i & 1] + i * w_step, kt * BK * 2, 0, 0);
+        }
     };
 
     f32x4 acc[FM][FN];
@@ -211,7 +247,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
-    const int nk = pr.K / BK;
+    const int nk = (pr.K + (SEG2 ? pr.K2 : 0)) / BK;
     /* fragments of one K-step: two 32-wide slices */
     bf16x8 a[2][FM], w[2][FN];
     auto frags = [&](const uint16_t *stage) {
@@ -474,6 +510,15 @@ int check_problem(const iris_gemm_problem_t &p) {
     if (!p.A || !p.W || !p.out) return iris_set_error("gemm: null operand");
     if (p.epi == IRIS_EPI_SWIGLU && (p.N % 64)) return iris_set_error("gemm: SwiGLU needs N %% 64 == 0");
     if (p.epi < 0 || p.epi > IRIS_EPI_ADD) return iris_set_error("gemm: epilogue %d", p.epi);
+    if (p.K2 < 0 || p.K2 % BK) return iris_set_error("gemm: K2=%d must be a multiple of %d", p.K2, BK);
+    if (p.K2 > 0) {
+        if (!p.A2 || !p.W2 || (((uintptr_t)p.A2 | (uintptr_t)p.W2) & 15))
+            return iris_set_error("gemm: second segment operands null or not 16-byte aligned");
+        if (p.lda2 % 8 || p.ldw2 % 8 || p.lda2 < p.K2 || p.ldw2 < p.K2)
+            return iris_set_error("gemm: lda2=%d ldw2=%d must be multiples of 8 and >= K2=%d", p.lda2, p.ldw2, p.K2);
+        if ((long long)BM * p.lda2 * 2 >= (1LL << 31) || (long long)BN * p.ldw2 * 2 >= (1LL << 31))
+            return iris_set_error("gemm: second segment leading dimension too large");
+    }
     const int ldo_need = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.epi == IRIS_EPI_F32_T ? p.M : p.N;
     if (p.ldo < ldo_need) return iris_set_error("gemm: ldo=%d < %d", p.ldo, ldo_need);
     /* 32-bit buffer offsets: one tile's rows must span < 2 GiB */
@@ -504,7 +549,12 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    bool seg2 = false;
+    for (int i = 0; i < n; i++) seg2 = seg2 || probs[i].K2 > 0;
+    if (seg2)
+        hipLaunchKernelGGL(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    else
+        hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
 }
 
@@ -561,6 +611,7 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     if (splits <= 1) return iris_hip_gemm(p, 1);
     if (p->M <= 0 || p->N <= 0) return 0;
     if (check_problem(*p)) return -1;
+    if (p->K2) return iris_set_error("gemm_splitk: no second K segment");
     const int nk = p->K / BK;
     const int kchunk = (nk + splits - 1) / splits * BK;
     const int chunks = (p->K + kchunk - 1) / kchunk;
@@ -604,6 +655,7 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     if (in_bytes >= (1ull << 31)) return iris_set_error("conv3x3: input of %zu bytes (< 2 GiB)", in_bytes);
     if ((long long)c->H * c->W >= (1LL << 31)) return iris_set_error("conv3x3: too many pixels");
     iris_gemm_problem_t p;
+    memset(&p, 0, sizeof(p));
     p.A = c->in;
     p.W = c->wt;
     p.out = c->out;

@@ -48,10 +48,14 @@ typedef struct {
     int scratch_len, max_rank;
 } lora_state_t;
 
+/* One adapted linear on the device: its adapters' down projections stacked
+ * (dn, bf16 [rp][in], zero rows up to rp) and scale * B scattered into the
+ * weight's own row order (up, bf16 [rows][rp], zero where no adapter writes).
+ * The GEMM runs as [x | u] [W | up]^T with u = x dn^T. rp == 0: no adapter. */
 typedef struct {
-    uint16_t *w, *orig;   /* device weight and its copy before the merge */
-    size_t bytes;
-} lora_backup_t;
+    uint16_t *dn, *up;
+    int in, rows, rp;
+} lora_dev_t;
 
 typedef struct {
     uint16_t *img_qkv, *img_o, *img_ffin, *img_down;    /* ffin rows gate/up interleaved by 32 */
@@ -106,11 +110,16 @@ struct iris_transformer {
     work_t w;
     /* adapters set through the reference's setters (owned, not applied) */
     void *lora, *ip, *ip_embeds;
-    void *lora_merged;                /* the LoRA state merged into the weights, or NULL */
-    int lora_dirty;                   /* set_lora was called since the last merge */
+    void *lora_built;                 /* the LoRA state the device adapters hold, or NULL */
+    int lora_dirty;                   /* set_lora was called since the last build */
+    lora_dev_t *ldev;                 /* 4 per double block (img qkv, img proj, txt qkv, txt proj),
+                                       * then 2 per single block (linear1, linear2); NULL: none */
+    int lrp_max;                      /* widest rp of ldev, the row stride of lu */
+    uint16_t *lu;                     /* [rows][lrp_max] bf16: u = x dn^T of the current linear */
+    float *lws;                       /* split-K partials of the u products */
+    size_t lu_rows, lws_floats;
+    int lora_stale;                   /* the step graph may hold LoRA buffers since changed or freed */
     float *d_csd;                     /* device copy of the CSD style delta [hidden] */
-    lora_backup_t *lora_bk;
-    int n_lora_bk, cap_lora_bk;
     float *csd_delta;
     int csd_skip;
     float sref_shf, sref_slf, sref_strength;
@@ -328,12 +337,16 @@ static void work_free(work_t *w);
 static void release_adapters(iris_transformer_t *tf);
 static int adapter_active(const iris_transformer_t *tf);
 static int lora_sync(iris_transformer_t *tf);
+static int lora_work(iris_transformer_t *tf);
+static void lora_dev_free(iris_transformer_t *tf);
+static const lora_dev_t *lora_at(const iris_transformer_t *tf, int idx);
+static int lora_down(iris_transformer_t *tf, const lora_dev_t *d, const uint16_t *x, int ldx, size_t r0, int M);
+static void lora_seg(const iris_transformer_t *tf, iris_gemm_problem_t *p, const lora_dev_t *d, size_t r0, int row0);
 
 void iris_transformer_free(iris_transformer_t *tf) {
     if (!tf) return;
     work_free(&tf->w);
-    for (int i = 0; i < tf->n_lora_bk; i++) iris_hip_free(tf->lora_bk[i].orig);
-    free(tf->lora_bk);
+    lora_dev_free(tf);
     iris_hip_free(tf->d_csd);
     iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
     iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
@@ -484,6 +497,7 @@ static int capture(iris_transformer_t *tf) {
     if (w->graph) { iris_hip_graph_destroy(w->graph); w->graph = NULL; }
     w->kgamma = tf->sref_strength;
     w->csd_on = tf->csd_delta && !tf->csd_skip;
+    tf->lora_stale = 0;
     if (w->csd_on && !tf->d_csd && !(tf->d_csd = (float *)iris_hip_malloc((size_t)tf->hidden * 4))) return -1;
     if (iris_hip_graph_begin()) return -1;
     if (enqueue_forward(tf)) {
@@ -561,7 +575,7 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
         if (rc) goto fail;
     }
     w->valid = 1;
-    if (capture(tf)) goto fail;
+    if (lora_work(tf) < 0 || capture(tf)) goto fail;
     return 0;
 fail:
     fprintf(stderr, "iris_flux_prepare: %s\n", iris_hip_last_error());
@@ -578,6 +592,7 @@ static int gemm(const iris_gemm_problem_t *p, int n) { return iris_hip_gemm(p, n
 static iris_gemm_problem_t prob(const void *A, int lda, const uint16_t *W, int ldw, void *out, int ldo,
                                 const float *vec, int M, int N, int K, int epi) {
     iris_gemm_problem_t p;
+    memset(&p, 0, sizeof(p));
     p.A = (const uint16_t *)A; p.lda = lda; p.W = W; p.ldw = ldw; p.out = out; p.ldo = ldo;
     p.vec = vec; p.M = M; p.N = N; p.K = K; p.epi = epi;
     return p;
@@ -656,14 +671,20 @@ static int double_block_forward(iris_transformer_t *tf, int i) {
     const float *mi = w->mod, *mt = w->mod + 6 * h;      /* shift1 scale1 gate1 shift2 scale2 gate2 */
     iris_gemm_problem_t p[4];
     int n;
+    const lora_dev_t *l_iq = lora_at(tf, 4 * i), *l_ip = lora_at(tf, 4 * i + 1);
+    const lora_dev_t *l_tq = lora_at(tf, 4 * i + 2), *l_tp = lora_at(tf, 4 * i + 3);
     /* AdaLN (shift1, scale1) -> Q, K, V per stream */
     CK(adaln(tf, mt, mt + h, mi, mi + h, T));
     n = 0;
     for (int b = 0; b < B; b++) {
         size_t r0 = (size_t)b * S;
-        p[n++] = prob(w->a + r0 * h, h, bw->txt_qkv, h, w->qkv + r0 * 3 * h, 3 * h, NULL, T, 3 * h, h, IRIS_EPI_BF16);
-        p[n++] = prob(w->a + (r0 + T) * h, h, bw->img_qkv, h, w->qkv + (r0 + T) * 3 * h, 3 * h, NULL, I, 3 * h, h,
-                      IRIS_EPI_BF16);
+        CK(lora_down(tf, l_tq, w->a + r0 * h, h, r0, T));
+        CK(lora_down(tf, l_iq, w->a + (r0 + T) * h, h, r0 + T, I));
+        p[n] = prob(w->a + r0 * h, h, bw->txt_qkv, h, w->qkv + r0 * 3 * h, 3 * h, NULL, T, 3 * h, h, IRIS_EPI_BF16);
+        lora_seg(tf, &p[n++], l_tq, r0, 0);
+        p[n] = prob(w->a + (r0 + T) * h, h, bw->img_qkv, h, w->qkv + (r0 + T) * 3 * h, 3 * h, NULL, I, 3 * h, h,
+                    IRIS_EPI_BF16);
+        lora_seg(tf, &p[n++], l_iq, r0 + T, 0);
     }
     CK(gemm(p, n));
     CK(kv_prepare(tf, bw->txt_nk, bw->img_nk, T, 0));
@@ -673,9 +694,13 @@ static int double_block_forward(iris_transformer_t *tf, int i) {
     n = 0;
     for (int b = 0; b < B; b++) {
         size_t r0 = (size_t)b * S;
-        p[n++] = prob(w->cat + r0 * hm, hm, bw->txt_o, h, w->x + r0 * h, h, mt + 2 * h, T, h, h, IRIS_EPI_GATED_ADD);
-        p[n++] = prob(w->cat + (r0 + T) * hm, hm, bw->img_o, h, w->x + (r0 + T) * h, h, mi + 2 * h, I, h, h,
-                      IRIS_EPI_GATED_ADD);
+        CK(lora_down(tf, l_tp, w->cat + r0 * hm, hm, r0, T));
+        CK(lora_down(tf, l_ip, w->cat + (r0 + T) * hm, hm, r0 + T, I));
+        p[n] = prob(w->cat + r0 * hm, hm, bw->txt_o, h, w->x + r0 * h, h, mt + 2 * h, T, h, h, IRIS_EPI_GATED_ADD);
+        lora_seg(tf, &p[n++], l_tp, r0, 0);
+        p[n] = prob(w->cat + (r0 + T) * hm, hm, bw->img_o, h, w->x + (r0 + T) * h, h, mi + 2 * h, I, h, h,
+                    IRIS_EPI_GATED_ADD);
+        lora_seg(tf, &p[n++], l_ip, r0 + T, 0);
     }
     CK(gemm(p, n));
     /* AdaLN (shift2, scale2) -> SwiGLU FFN -> gated residual (gate2) */
@@ -706,16 +731,22 @@ static int single_block_forward(iris_transformer_t *tf, int i) {
     const dev_single_t *bw = &tf->sgl[i];
     int h = tf->hidden, mlp = tf->mlp, hm = h + mlp, BS = w->B * w->S;
     const float *ms = w->mod + 12 * h;                   /* shift scale gate */
+    const lora_dev_t *l1 = lora_at(tf, 4 * tf->n_double + 2 * i), *l2 = lora_at(tf, 4 * tf->n_double + 2 * i + 1);
     CK(adaln(tf, ms, ms + h, ms, ms + h, w->S));
     /* fused projection: Q,K,V rows -> qkv; gate/up rows -> SwiGLU -> cat[:, h:] */
     iris_gemm_problem_t p[2];
+    CK(lora_down(tf, l1, w->a, h, 0, BS));
     p[0] = prob(w->a, h, bw->qkv_mlp, h, w->qkv, 3 * h, NULL, BS, 3 * h, h, IRIS_EPI_BF16);
+    lora_seg(tf, &p[0], l1, 0, 0);
     p[1] = prob(w->a, h, bw->qkv_mlp + (size_t)3 * h * h, h, w->cat + h, hm, NULL, BS, 2 * mlp, h, IRIS_EPI_SWIGLU);
+    lora_seg(tf, &p[1], l1, 0, 3 * h);
     CK(gemm(p, 2));
     CK(kv_prepare(tf, bw->nk, bw->nk, w->S, 1));
     CK(attention(tf, bw->nq, bw->nq, w->S, w->cat, hm));
     /* [attn | mlp] . W_out^T, gated residual */
+    CK(lora_down(tf, l2, w->cat, hm, 0, BS));
     p[0] = prob(w->cat, hm, bw->out, hm, w->x, h, ms + 2 * h, BS, h, hm, IRIS_EPI_GATED_ADD);
+    lora_seg(tf, &p[0], l2, 0, 0);
     CK(gemm(p, 1));
     return 0;
 }
@@ -779,12 +810,14 @@ static int enqueue_forward(iris_transformer_t *tf) {
  * (double_block_forward :2366, single_block_forward :3761) as C entry points. */
 int iris_flux_double_block_forward(iris_transformer_t *tf, int idx) {
     if (!tf->w.valid || idx < 0 || idx >= tf->n_double) return -1;
+    if (lora_sync(tf) < 0 || lora_work(tf) < 0) return -1;
     if (double_block_forward(tf, idx)) return -1;
     return iris_hip_sync();
 }
 
 int iris_flux_single_block_forward(iris_transformer_t *tf, int idx) {
     if (!tf->w.valid || idx < 0 || idx >= tf->n_single) return -1;
+    if (lora_sync(tf) < 0 || lora_work(tf) < 0) return -1;
     if (single_block_forward(tf, idx)) return -1;
     return iris_hip_sync();
 }
@@ -822,7 +855,8 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
         if (rc) return -1;
     }
     const int csd_on = tf->csd_delta && !tf->csd_skip;
-    if ((w->kgamma != tf->sref_strength || w->csd_on != csd_on) && capture(tf)) return -1;
+    /* adapters rebuilt (the graph holds the old GEMM problems), SREF strength or CSD switched */
+    if ((tf->lora_stale || w->kgamma != tf->sref_strength || w->csd_on != csd_on) && capture(tf)) return -1;
     if (csd_on && (iris_hip_memcpy_h2d(tf->d_csd, tf->csd_delta, (size_t)tf->hidden * 4) || iris_hip_sync()))
         return -1;
     /* get_timestep_embedding(t * 1000), :3967 */
@@ -885,140 +919,222 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
 
 /* ------------------------------------------------------------------ LoRA */
 
-/* The reference adds scale * B (A x) to the output of each adapted linear
- * (lora_apply, iris_lora.c:43-90; call sites iris_transformer_flux.c:2430-2532,
- * :3819, :3910). The linears have no bias, so this equals the linear with
- * W + scale * B A: the product is formed once with the MFMA GEMM (A and B in
- * bf16, rank padded to 64) and merged into the resident bf16 weights through
- * a row map into the fused / SwiGLU-interleaved layouts. The weights before
- * the merge are kept and restored when the LoRA is replaced or removed. */
-static int lora_backup(iris_transformer_t *tf, uint16_t *w, size_t bytes) {
-    for (int i = 0; i < tf->n_lora_bk; i++)
-        if (tf->lora_bk[i].w == w) return 0;
-    if (tf->n_lora_bk == tf->cap_lora_bk) {
-        const int cap = tf->cap_lora_bk ? 2 * tf->cap_lora_bk : 64;
-        lora_backup_t *n = (lora_backup_t *)realloc(tf->lora_bk, cap * sizeof(*n));
-        if (!n) return -1;
-        tf->lora_bk = n;
-        tf->cap_lora_bk = cap;
+/* The reference adds scale * B (A x) in f32 to the output of each adapted
+ * linear (lora_apply, iris_lora.c:43-90; call sites iris_transformer_flux.c:
+ * 2429-2434, :2482-2487, :2529-2532, :3818-3819, :3909-3910). Here each
+ * adapted linear runs as one GEMM over the concatenated K axis,
+ *     [x | u] [W | scale B]^T,   u = x A^T (bf16 [rows][rp]),
+ * so the low-rank term is accumulated in f32 with the product itself, before
+ * the epilogue (bf16 store, SwiGLU, gated residual), and the weights stay
+ * untouched. The adapters of one fused linear (Q, K, V of a stream) share u:
+ * their A rows are stacked in dn and each B fills its own columns of up.
+ * u is formed by a split-K GEMM per adapted linear and call. */
+static void lora_dev_free(iris_transformer_t *tf) {
+    const int n = 4 * tf->n_double + 2 * tf->n_single;
+    if (tf->ldev || tf->lu || tf->lws) tf->lora_stale = 1;
+    for (int i = 0; tf->ldev && i < n; i++) {
+        iris_hip_free(tf->ldev[i].dn);
+        iris_hip_free(tf->ldev[i].up);
     }
-    uint16_t *o = (uint16_t *)iris_hip_malloc(bytes);
-    if (!o || iris_hip_memcpy_d2d(o, w, bytes)) { iris_hip_free(o); return -1; }
-    tf->lora_bk[tf->n_lora_bk++] = (lora_backup_t){w, o, bytes};
-    return 0;
+    free(tf->ldev);
+    tf->ldev = NULL;
+    tf->lrp_max = 0;
+    iris_hip_free(tf->lu);
+    iris_hip_free(tf->lws);
+    tf->lu = NULL;
+    tf->lws = NULL;
+    tf->lu_rows = tf->lws_floats = 0;
+    tf->lora_built = NULL;
 }
 
-static int lora_restore(iris_transformer_t *tf) {
-    int rc = 0;
-    for (int i = 0; i < tf->n_lora_bk; i++) {
-        rc |= iris_hip_memcpy_d2d(tf->lora_bk[i].w, tf->lora_bk[i].orig, tf->lora_bk[i].bytes);
-        rc |= iris_hip_sync();
-        iris_hip_free(tf->lora_bk[i].orig);
-    }
-    tf->n_lora_bk = 0;
-    tf->lora_merged = NULL;
-    return rc ? -1 : 0;
-}
+/* one adapter of a fused linear: rows row0 .. row0 + out of the logical
+ * output (before the SwiGLU interleave) */
+typedef struct {
+    const lora_adapter_t *ad;
+    int row0, out;
+} lora_part_t;
 
-/* W (total_rows x cols, bf16) += scale * B A for output rows o -> row map(o):
- * row0 + o, except rows >= il_from, which are the SwiGLU gate / up halves
- * (il_len rows each) interleaved in groups of SWIGLU_GROUP */
-static int lora_merge(iris_transformer_t *tf, uint16_t *W, size_t total_rows, int cols, const lora_adapter_t *ad,
-                      float scale, int row0, int il_from, int il_len) {
-    if (!ad || !ad->lora_A || !ad->lora_B || ad->rank <= 0) return 0;
-    if (ad->in_dim != cols) {
-        fprintf(stderr, "iris_hip: LoRA adapter in_dim %d, the linear has %d\n", ad->in_dim, cols);
-        return -1;
-    }
-    const int r = ad->rank, rp = (r + 63) / 64 * 64, out = ad->out_dim;
-    uint16_t *hb = (uint16_t *)calloc((size_t)out * rp, 2), *ha = (uint16_t *)calloc((size_t)cols * rp, 2);
-    int *map = (int *)malloc((size_t)out * sizeof(int));
-    uint16_t *db = NULL, *da = NULL;
-    float *dw = NULL;
-    int *dmap = NULL, rc = -1;
-    if (!hb || !ha || !map) goto out;
-    for (int o = 0; o < out; o++)
-        for (int k = 0; k < r; k++) hb[(size_t)o * rp + k] = iris_f32_to_bf16(ad->lora_B[(size_t)o * r + k]);
-    for (int i = 0; i < cols; i++)
-        for (int k = 0; k < r; k++) ha[(size_t)i * rp + k] = iris_f32_to_bf16(ad->lora_A[(size_t)k * cols + i]);
-    for (int o = 0; o < out; o++) {
-        int m = row0 + o;
-        if (il_len > 0 && o >= il_from) {
-            const int q = o - il_from, up = q >= il_len, g = (up ? q - il_len : q);
-            m = row0 + il_from + (g / SWIGLU_GROUP) * 2 * SWIGLU_GROUP + up * SWIGLU_GROUP + g % SWIGLU_GROUP;
+static int lora_valid(const lora_adapter_t *ad) { return ad && ad->lora_A && ad->lora_B && ad->rank > 0; }
+
+/* Build one adapted linear (in inputs, rows outputs; logical rows >= il_from
+ * are the SwiGLU gate / up halves, il_len each, interleaved in groups of
+ * SWIGLU_GROUP in the weight). Adapters whose in_dim or out_dim does not match
+ * the linear are rejected (-1), as the reference's loader skips them
+ * (iris_lora.c:151-164). */
+static int lora_build(lora_dev_t *d, const lora_part_t *parts, int n, int in, int rows, int il_from, int il_len,
+                      float scale, const char *what, int blk) {
+    memset(d, 0, sizeof(*d));
+    int rsum = 0;
+    for (int j = 0; j < n; j++) {
+        const lora_adapter_t *ad = parts[j].ad;
+        if (!lora_valid(ad)) continue;
+        if (ad->in_dim != in || ad->out_dim != parts[j].out) {
+            fprintf(stderr, "iris_hip: LoRA %s of block %d: adapter %d x %d (in x out), the linear takes %d x %d\n",
+                    what, blk, ad->in_dim, ad->out_dim, in, parts[j].out);
+            return -1;
         }
-        if (m < 0 || (size_t)m >= total_rows) { fprintf(stderr, "iris_hip: LoRA adapter rows out of range\n"); goto out; }
-        map[o] = m;
+        rsum += ad->rank;
     }
-    db = (uint16_t *)iris_hip_malloc((size_t)out * rp * 2);
-    da = (uint16_t *)iris_hip_malloc((size_t)cols * rp * 2);
-    dw = (float *)iris_hip_malloc((size_t)out * cols * 4);
-    dmap = (int *)iris_hip_malloc((size_t)out * sizeof(int));
-    if (!db || !da || !dw || !dmap || lora_backup(tf, W, total_rows * (size_t)cols * 2) ||
-        iris_hip_memcpy_h2d(db, hb, (size_t)out * rp * 2) || iris_hip_memcpy_h2d(da, ha, (size_t)cols * rp * 2) ||
-        iris_hip_memcpy_h2d(dmap, map, (size_t)out * sizeof(int)))
+    if (!rsum) return 0;
+    const int rp = (rsum + 63) / 64 * 64;
+    uint16_t *hdn = (uint16_t *)calloc((size_t)rp * in, 2), *hup = (uint16_t *)calloc((size_t)rows * rp, 2);
+    int rc = -1;
+    if (!hdn || !hup) goto out;
+    for (int j = 0, c0 = 0; j < n; j++) {
+        const lora_adapter_t *ad = parts[j].ad;
+        if (!lora_valid(ad)) continue;
+        const int r = ad->rank;
+        for (size_t e = 0; e < (size_t)r * in; e++) hdn[(size_t)c0 * in + e] = iris_f32_to_bf16(ad->lora_A[e]);
+        for (int o = 0; o < ad->out_dim; o++) {
+            const int q = parts[j].row0 + o;
+            int m = q;
+            if (il_len > 0 && q >= il_from) {
+                const int g = q - il_from, up = g >= il_len, gi = up ? g - il_len : g;
+                m = il_from + (gi / SWIGLU_GROUP) * 2 * SWIGLU_GROUP + up * SWIGLU_GROUP + gi % SWIGLU_GROUP;
+            }
+            if (m < 0 || m >= rows) {
+                fprintf(stderr, "iris_hip: LoRA %s of block %d: output row %d outside 0..%d\n", what, blk, m, rows - 1);
+                goto out;
+            }
+            for (int k = 0; k < r; k++)
+                hup[(size_t)m * rp + c0 + k] = iris_f32_to_bf16(scale * ad->lora_B[(size_t)o * r + k]);
+        }
+        c0 += r;
+    }
+    d->dn = (uint16_t *)iris_hip_malloc((size_t)rp * in * 2);
+    d->up = (uint16_t *)iris_hip_malloc((size_t)rows * rp * 2);
+    if (!d->dn || !d->up || iris_hip_memcpy_h2d(d->dn, hdn, (size_t)rp * in * 2) ||
+        iris_hip_memcpy_h2d(d->up, hup, (size_t)rows * rp * 2) || iris_hip_sync())
         goto out;
-    {
-        iris_gemm_problem_t p = {db, da, dw, NULL, out, cols, rp, rp, rp, cols, IRIS_EPI_F32};
-        if (iris_hip_gemm(&p, 1) || iris_hip_merge_rows(W, cols, dmap, dw, out, scale) || iris_hip_sync()) goto out;
-    }
+    d->in = in;
+    d->rows = rows;
+    d->rp = rp;
     rc = 0;
 out:
-    iris_hip_free(db);
-    iris_hip_free(da);
-    iris_hip_free(dw);
-    iris_hip_free(dmap);
-    free(hb);
-    free(ha);
-    free(map);
+    if (rc) {
+        iris_hip_free(d->dn);
+        iris_hip_free(d->up);
+        memset(d, 0, sizeof(*d));
+    }
+    free(hdn);
+    free(hup);
     return rc;
 }
 
-/* make the resident weights match tf->lora (restore, then merge the new one) */
+/* split count for u = x dn^T: enough 256-row tiles x K chunks for the chip */
+static int lora_splits(int M, int K) {
+    const int tm = (M + 255) / 256, nk = K / 64;
+    int s = 256 / tm;
+    if (s > nk) s = nk;
+    return s < 1 ? 1 : s;
+}
+
+/* u and split-K buffers for the prepared geometry; 1 if reallocated (a
+ * captured graph holds the old addresses: lora_stale is set), 0 if
+ * unchanged, -1 on error */
+static int lora_work(iris_transformer_t *tf) {
+    if (!tf->ldev || !tf->lrp_max || !tf->w.valid) return 0;
+    const size_t rows = (size_t)tf->w.B * tf->w.S;
+    /* chunks * M <= 256 x 256 whenever the product is split (lora_splits) */
+    const size_t wsf = (size_t)65536 * tf->lrp_max;
+    if (rows <= tf->lu_rows && wsf <= tf->lws_floats) return 0;
+    tf->lora_stale = 1;
+    iris_hip_free(tf->lu);
+    iris_hip_free(tf->lws);
+    tf->lu = (uint16_t *)iris_hip_malloc(rows * tf->lrp_max * 2);
+    tf->lws = (float *)iris_hip_malloc(wsf * 4);
+    if (!tf->lu || !tf->lws) {
+        iris_hip_free(tf->lu);
+        iris_hip_free(tf->lws);
+        tf->lu = NULL;
+        tf->lws = NULL;
+        tf->lu_rows = tf->lws_floats = 0;
+        return -1;
+    }
+    tf->lu_rows = rows;
+    tf->lws_floats = wsf;
+    return 1;
+}
+
+/* Device adapters for tf->lora; 0 when they match it, -1 on error (none are
+ * applied then and the next forward tries again). Any change of the device
+ * state sets lora_stale: the step graph must be captured again before its
+ * next launch, also after a failed build freed the previous adapters. */
 static int lora_sync(iris_transformer_t *tf) {
-    if (!tf->lora_dirty && tf->lora == tf->lora_merged) return 0;
+    if (!tf->lora_dirty && tf->lora == tf->lora_built) return 0;
     tf->lora_dirty = 0;
-    if (lora_restore(tf)) return -1;
+    lora_dev_free(tf);
     const lora_state_t *L = (const lora_state_t *)tf->lora;
     if (!L || L->scale == 0.0f) {
-        tf->lora_merged = tf->lora;
+        tf->lora_built = tf->lora;
         return 0;
     }
-    const int h = tf->hidden, mlp = tf->mlp;
+    const int h = tf->hidden, mlp = tf->mlp, nd = tf->n_double, ns = tf->n_single;
     const float sc = L->scale;
-    for (int i = 0; i < tf->n_double && i < L->num_double_blocks; i++) {
-        dev_double_t *b = &tf->dbl[i];
-        const lora_adapter_t *iq = L->double_img_q ? &L->double_img_q[i] : NULL;
-        const lora_adapter_t *ik = L->double_img_k ? &L->double_img_k[i] : NULL;
-        const lora_adapter_t *iv = L->double_img_v ? &L->double_img_v[i] : NULL;
-        const lora_adapter_t *ip = L->double_img_proj ? &L->double_img_proj[i] : NULL;
-        const lora_adapter_t *tq = L->double_txt_q ? &L->double_txt_q[i] : NULL;
-        const lora_adapter_t *tk = L->double_txt_k ? &L->double_txt_k[i] : NULL;
-        const lora_adapter_t *tv = L->double_txt_v ? &L->double_txt_v[i] : NULL;
-        const lora_adapter_t *tp = L->double_txt_proj ? &L->double_txt_proj[i] : NULL;
-        if (lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, iq, sc, 0, 0, 0) ||
-            lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, ik, sc, h, 0, 0) ||
-            lora_merge(tf, b->img_qkv, 3 * (size_t)h, h, iv, sc, 2 * h, 0, 0) ||
-            lora_merge(tf, b->img_o, h, h, ip, sc, 0, 0, 0) ||
-            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tq, sc, 0, 0, 0) ||
-            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tk, sc, h, 0, 0) ||
-            lora_merge(tf, b->txt_qkv, 3 * (size_t)h, h, tv, sc, 2 * h, 0, 0) ||
-            lora_merge(tf, b->txt_o, h, h, tp, sc, 0, 0, 0))
+    tf->ldev = (lora_dev_t *)calloc((size_t)4 * nd + 2 * ns, sizeof(lora_dev_t));
+    if (!tf->ldev) return -1;
+#define AD(arr, n, i) ((arr) && (i) < (n) ? &(arr)[i] : NULL)
+    for (int i = 0; i < nd; i++) {
+        const int n = L->num_double_blocks;
+        lora_part_t iq[3] = {{AD(L->double_img_q, n, i), 0, h}, {AD(L->double_img_k, n, i), h, h},
+                             {AD(L->double_img_v, n, i), 2 * h, h}};
+        lora_part_t tq[3] = {{AD(L->double_txt_q, n, i), 0, h}, {AD(L->double_txt_k, n, i), h, h},
+                             {AD(L->double_txt_v, n, i), 2 * h, h}};
+        lora_part_t ip = {AD(L->double_img_proj, n, i), 0, h}, tp = {AD(L->double_txt_proj, n, i), 0, h};
+        lora_dev_t *d = &tf->ldev[4 * i];
+        if (lora_build(d + 0, iq, 3, h, 3 * h, 0, 0, sc, "img qkv", i) ||
+            lora_build(d + 1, &ip, 1, h, h, 0, 0, sc, "img proj", i) ||
+            lora_build(d + 2, tq, 3, h, 3 * h, 0, 0, sc, "txt qkv", i) ||
+            lora_build(d + 3, &tp, 1, h, h, 0, 0, sc, "txt proj", i))
             goto fail;
     }
-    for (int i = 0; i < tf->n_single && i < L->num_single_blocks; i++) {
-        dev_single_t *b = &tf->sgl[i];
-        const lora_adapter_t *l1 = L->single_linear1 ? &L->single_linear1[i] : NULL;
-        const lora_adapter_t *l2 = L->single_linear2 ? &L->single_linear2[i] : NULL;
-        if (lora_merge(tf, b->qkv_mlp, 3 * (size_t)h + 2 * (size_t)mlp, h, l1, sc, 0, 3 * h, mlp) ||
-            lora_merge(tf, b->out, h, h + mlp, l2, sc, 0, 0, 0))
+    for (int i = 0; i < ns; i++) {
+        const int n = L->num_single_blocks;
+        lora_part_t l1 = {AD(L->single_linear1, n, i), 0, 3 * h + 2 * mlp}, l2 = {AD(L->single_linear2, n, i), 0, h};
+        lora_dev_t *d = &tf->ldev[4 * nd + 2 * i];
+        if (lora_build(d + 0, &l1, 1, h, 3 * h + 2 * mlp, 3 * h, mlp, sc, "linear1", i) ||
+            lora_build(d + 1, &l2, 1, h + mlp, h, 0, 0, sc, "linear2", i))
             goto fail;
     }
-    tf->lora_merged = tf->lora;
+#undef AD
+    for (int i = 0; i < 4 * nd + 2 * ns; i++)
+        if (tf->ldev[i].rp > tf->lrp_max) tf->lrp_max = tf->ldev[i].rp;
+    if (!tf->lrp_max) {
+        free(tf->ldev);
+        tf->ldev = NULL;
+    }
+    if (lora_work(tf) < 0) goto fail;
+    tf->lora_built = tf->lora;
+    tf->lora_stale = 1;
     return 0;
 fail:
-    lora_restore(tf);
+    lora_dev_free(tf);
+    tf->lora_dirty = 1;   /* try again (and fail loudly again) at the next forward */
     return -1;
+}
+
+/* u rows [r0, r0 + M) = x dn^T for the adapted linear d (x bf16, row stride
+ * ldx); no-op without an adapter */
+static int lora_down(iris_transformer_t *tf, const lora_dev_t *d, const uint16_t *x, int ldx, size_t r0, int M) {
+    if (!d || !d->rp || M <= 0) return 0;
+    iris_gemm_problem_t p;
+    memset(&p, 0, sizeof(p));
+    p.A = x; p.lda = ldx; p.W = d->dn; p.ldw = d->in;
+    p.out = tf->lu + r0 * tf->lrp_max; p.ldo = tf->lrp_max;
+    p.M = M; p.N = d->rp; p.K = d->in; p.epi = IRIS_EPI_BF16;
+    return iris_hip_gemm_splitk(&p, lora_splits(M, d->in), tf->lws, tf->lws_floats * 4);
+}
+
+/* add the adapter's second K segment (u rows from r0, up rows from row0) */
+static void lora_seg(const iris_transformer_t *tf, iris_gemm_problem_t *p, const lora_dev_t *d, size_t r0, int row0) {
+    if (!d || !d->rp) return;
+    p->A2 = tf->lu + r0 * tf->lrp_max; p->lda2 = tf->lrp_max;
+    p->W2 = d->up + (size_t)row0 * d->rp; p->ldw2 = d->rp;
+    p->K2 = d->rp;
+}
+
+static const lora_dev_t *lora_at(const iris_transformer_t *tf, int idx) {
+    return tf->ldev && tf->ldev[idx].rp ? &tf->ldev[idx] : NULL;
 }
 
 /* The reference's adapter setters (iris_transformer_flux.c:5131-5201), kept
@@ -1052,7 +1168,7 @@ void iris_transformer_set_lora(iris_transformer_t *tf, void *lora) {
     if (!tf) return;
     if (tf->lora && tf->lora != lora && lora_free) lora_free(tf->lora);
     tf->lora = lora;
-    tf->lora_dirty = 1;   /* merged at the next forward (a freed state's address may come back) */
+    tf->lora_dirty = 1;   /* built at the next forward (a freed state's address may come back) */
 }
 
 void iris_transformer_set_csd_delta(iris_transformer_t *tf, float *delta) {

@@ -434,6 +434,7 @@ fail:
 static iris_gemm_problem_t zprob(const void *A, int lda, const uint16_t *W, void *out, int ldo, const float *vec,
                                  int M, int N, int K, int epi) {
     iris_gemm_problem_t p;
+    memset(&p, 0, sizeof(p));
     p.A = (const uint16_t *)A; p.lda = lda; p.W = W; p.ldw = K; p.out = out; p.ldo = ldo; p.vec = vec;
     p.M = M; p.N = N; p.K = K; p.epi = epi;
     return p;

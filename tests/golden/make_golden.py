@@ -107,6 +107,11 @@ def flux_goldens(r, d, res):
     r.iris_transformer_set_lora(tf, tl.make_lora(cfg, seed=5, std=0.2))
     p = r.iris_transformer_forward(tf, tl.fptr(lat), 8, 8, tl.fptr(temb_txt), T, f(0.8))
     res["flux_fwd_lora"] = tl.take_f32(r, p, 128 * 64)
+    # a LoRA of a trained adapter's size: rank 16, A and B entries of std
+    # 0.0125, so scale * B A is about 1 % of W (entries of std 1/sqrt(fan_in))
+    r.iris_transformer_set_lora(tf, tl.make_lora(cfg, seed=6, rank=16, std=0.0125))
+    p = r.iris_transformer_forward(tf, tl.fptr(lat), 8, 8, tl.fptr(temb_txt), T, f(0.8))
+    res["flux_fwd_lora_r16"] = tl.take_f32(r, p, 128 * 64)
     r.iris_transformer_set_lora(tf, None)
     # CSD style delta on the time embedding (iris_transformer_set_csd_delta)
     r.iris_transformer_set_csd_delta.argtypes = [ctypes.c_void_p, ctypes.c_void_p]

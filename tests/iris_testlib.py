@@ -73,7 +73,9 @@ def oracle():
 class GemmProblem(ctypes.Structure):
     _fields_ = [("A", ctypes.c_void_p), ("W", ctypes.c_void_p), ("out", ctypes.c_void_p), ("vec", ctypes.c_void_p),
                 ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("lda", ctypes.c_int),
-                ("ldw", ctypes.c_int), ("ldo", ctypes.c_int), ("epi", ctypes.c_int)]
+                ("ldw", ctypes.c_int), ("ldo", ctypes.c_int), ("epi", ctypes.c_int),
+                ("A2", ctypes.c_void_p), ("W2", ctypes.c_void_p), ("K2", ctypes.c_int), ("lda2", ctypes.c_int),
+                ("ldw2", ctypes.c_int)]
 
 
 class NormArgs(ctypes.Structure):

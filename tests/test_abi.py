@@ -70,3 +70,41 @@ def test_no_oracle_symbols_in_product():
     lib = ctypes.CDLL(tl.HIP_SO)
     for n in ("orc_flux_forward", "orc_zi_forward", "orc_set_blas", "orc_linear"):
         assert not hasattr(lib, n), n
+
+
+# ctypes mirrors of the header structs the tests and bench.py pass through the
+# C-ABI, checked field by field against the compiler's own layout
+MIRRORS = [("iris_gemm_problem_t", "iris_hip.h", tl.GemmProblem),
+           ("iris_conv3x3_t", "iris_hip.h", tl.Conv3x3),
+           ("iris_norm_args_t", "iris_hip.h", tl.NormArgs),
+           ("iris_qkprep_args_t", "iris_hip.h", tl.QkPrepArgs),
+           ("iris_attn_args_t", "iris_hip.h", tl.AttnArgs),
+           ("iris_ref_t", "iris_transformer.h", tl.IrisRef)]
+
+
+C_NAME = {"inp": "in"}      # Python keywords renamed in the mirrors
+
+
+def test_struct_mirrors_match_headers(tmp_path):
+    import shutil
+    import subprocess
+    if not shutil.which("gcc"):
+        pytest.skip("gcc not found")
+    lines = ["#include <stddef.h>", "#include <stdint.h>", "#include <stdio.h>"]
+    lines += sorted({f'#include "{h}"' for _, h, _ in MIRRORS})
+    lines.append("int main(void) {")
+    for cname, _, cls in MIRRORS:
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {C_NAME.get(f, f)}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", INCLUDE, str(src), "-o", str(exe)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                         text=True).stdout.splitlines())
+    for cname, _, cls in MIRRORS:
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(cls), cname
+        for f, _ in cls._fields_:
+            assert int(got[f"{cname} {f}"]) == getattr(cls, f).offset, (cname, f)

@@ -161,6 +161,96 @@ def test_gemm_splitk_epilogues(lib, M, N, K, splits):
     assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) != 0
 
 
+def test_gemm_second_segment(lib):
+    """out = A W^T + A2 W2^T (the low-rank adapter's concatenated K axis):
+    F32 + bias, gated residual and SwiGLU epilogues over ragged tiles, A2 row
+    stride wider than K2, a one-step first segment, and a problem without a
+    second segment in the same launch."""
+    rng = np.random.default_rng(11)
+    M, K, N, mlp = 1000, 256, 520, 256
+    A = rng.standard_normal((M, K), np.float32)
+    W = rng.standard_normal((N, K), np.float32) * 0.05
+    A2 = np.zeros((M, 128), np.float32)
+    A2[:, :64] = rng.standard_normal((M, 64), np.float32)
+    A2[:, 64:] = np.nan                               # beyond K2: never read
+    W2 = rng.standard_normal((N, 64), np.float32) * 0.05
+    vec = rng.standard_normal(N).astype(np.float32)
+    x0 = rng.standard_normal((M, N), np.float32)
+    Wg = rng.standard_normal((2 * mlp, 64), np.float32) * 0.05       # one-step first segment (K 64)
+    Wg2 = rng.standard_normal((2 * mlp, 128), np.float32) * 0.05     # two-step second segment
+    As2 = rng.standard_normal((M, 128), np.float32)
+    dA, dW, dA2, dW2, dAs2 = (tl.Dev.of(tl.to_bf16(v)) for v in (A, W, A2, W2, As2))
+    dWg, dWg2, dV = tl.Dev.of(tl.to_bf16(Wg)), tl.Dev.of(tl.to_bf16(Wg2)), tl.Dev.of(vec)
+    dO, dO0, dX = tl.Dev(M * N * 4), tl.Dev(M * N * 4), tl.Dev.of(x0)
+    dSw = tl.Dev(M * mlp * 2)
+    P = tl.GemmProblem
+    run_gemm(lib, [P(dA.ptr, dW.ptr, dO.ptr, dV.ptr, M, N, K, K, K, N, EPI_F32, dA2.ptr, dW2.ptr, 64, 128, 64),
+                   P(dA.ptr, dW.ptr, dO0.ptr, None, M, N, K, K, K, N, EPI_F32),
+                   P(dA.ptr, dW.ptr, dX.ptr, dV.ptr, M, N, K, K, K, N, EPI_GATED_ADD, dA2.ptr, dW2.ptr, 64, 128, 64),
+                   P(dA.ptr, dWg.ptr, dSw.ptr, None, M, 2 * mlp, 64, K, 64, mlp, EPI_SWIGLU, dAs2.ptr, dWg2.ptr, 128,
+                     128, 128)])
+    a64, a264 = bf(A).astype(np.float64), bf(A2[:, :64]).astype(np.float64)
+    base = a64 @ bf(W).astype(np.float64).T
+    ref = base + a264 @ bf(W2).astype(np.float64).T
+    assert tl.rel_l2(dO.get(np.float32, (M, N)), ref + vec) < 1e-5
+    assert tl.rel_l2(dO0.get(np.float32, (M, N)), base) < 1e-5
+    assert tl.rel_l2(dX.get(np.float32, (M, N)), x0 + vec * ref) < 1e-5
+    y = a64[:, :64] @ bf(Wg).astype(np.float64).T + bf(As2).astype(np.float64) @ bf(Wg2).astype(np.float64).T
+    g = np.concatenate([y[:, c * 64:c * 64 + 32] for c in range(mlp // 32)], 1)
+    u = np.concatenate([y[:, c * 64 + 32:c * 64 + 64] for c in range(mlp // 32)], 1)
+    assert tl.rel_l2(tl.bf16_to_f32(dSw.get(np.uint16, (M, mlp))), g / (1 + np.exp(-g)) * u) < 4e-3
+
+
+def test_gemm_second_segment_rejects(lib):
+    """K2 not a multiple of 64, a missing operand and a row stride below K2
+    are errors, not launches."""
+    d = tl.Dev(1 << 16)
+    P = tl.GemmProblem
+    for k2, a2, lda2 in ((32, d.ptr, 64), (64, None, 64), (64, d.ptr, 32)):
+        pr = P(d.ptr, d.ptr, d.ptr, None, 16, 16, 64, 64, 64, 16, EPI_F32, a2, d.ptr, k2, lda2, 64)
+        assert lib.iris_hip_gemm(ctypes.byref(pr), 1) != 0
+
+
+def test_lora_low_rank_segment_fidelity(lib):
+    """A LoRA of a trained adapter's size on one linear: rank 16, A and B
+    entries of std 0.009 (scale 1), so scale B A is about 1 % of W (std
+    1/sqrt(K), K 1024). The product path the transformer runs (u = x A^T by the
+    split-K GEMM into bf16, then [x | u] [W | s B]^T in one accumulation)
+    reproduces the adapter's effect scale B (A x) (lora_apply,
+    iris_lora.c:43-90, f32) to rel-L2 <= 5e-2; the same delta rounded into
+    the bf16 weights would not."""
+    rng = np.random.default_rng(16)
+    M, K, N, r, rp = 512, 1024, 768, 16, 64
+    x = bf(rng.standard_normal((M, K), np.float32))
+    W = bf(rng.standard_normal((N, K), np.float32) / np.sqrt(K))
+    La = rng.standard_normal((r, K), np.float32) * 0.009
+    Lb = rng.standard_normal((N, r), np.float32) * 0.009
+    dWl = Lb.astype(np.float64) @ La.astype(np.float64)
+    print(f"|scale B A| / |W| = {np.linalg.norm(dWl) / np.linalg.norm(W):.4f}")
+    dn = np.zeros((rp, K), np.float32)
+    dn[:r] = La
+    up = np.zeros((N, rp), np.float32)
+    up[:, :r] = Lb
+    dx, dWd, ddn, dup = (tl.Dev.of(tl.to_bf16(v)) for v in (x, W, dn, up))
+    du, dyb, dyl = tl.Dev(M * rp * 2), tl.Dev(M * N * 4), tl.Dev(M * N * 4)
+    ws_bytes = 8 * M * rp * 4
+    ws = tl.Dev(ws_bytes)
+    lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    P = tl.GemmProblem
+    pu = P(dx.ptr, ddn.ptr, du.ptr, None, M, rp, K, K, K, rp, EPI_BF16)
+    assert lib.iris_hip_gemm_splitk(ctypes.byref(pu), 8, ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+    run_gemm(lib, [P(dx.ptr, dWd.ptr, dyb.ptr, None, M, N, K, K, K, N, EPI_F32),
+                   P(dx.ptr, dWd.ptr, dyl.ptr, None, M, N, K, K, K, N, EPI_F32, du.ptr, dup.ptr, rp, rp, rp)])
+    effect = dyl.get(np.float32, (M, N)).astype(np.float64) - dyb.get(np.float32, (M, N))
+    want = x.astype(np.float64) @ dWl.T
+    err = tl.rel_l2(effect, want)
+    merged = bf((W + dWl).astype(np.float32)).astype(np.float64) - W
+    err_merge = tl.rel_l2(x.astype(np.float64) @ merged.T, want)
+    print(f"LoRA effect rel_l2: low-rank segment {err:.3e}, bf16 weight merge {err_merge:.3e}")
+    assert err <= 5e-2
+    assert err_merge > 2 * err
+
+
 def attention_ref(q, k, v, scale, valid=None):
     s = q.astype(np.float64) @ k.astype(np.float64).T * scale
     if valid is not None:
