@@ -91,6 +91,14 @@ void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
                            const float *img_cos, const float *img_sin,
                            const float *txt_cos, const float *txt_sin,
                            int seq, int img_offset);
+void orc_flux_single_block_k(orc_flux_t *m, int idx, float *x, const float *t_emb,
+                             const float *img_cos, const float *img_sin,
+                             const float *kimg_cos, const float *kimg_sin,
+                             const float *txt_cos, const float *txt_sin,
+                             int seq, int img_offset);
+/* SREF band control (reference rows' K-side RoPE bands, single blocks only) */
+void orc_flux_set_sref_bands(orc_flux_t *m, float shf, float slf);
+void orc_sref_band_scale(float *c, float *s, int ref_start, int rows, int axis_dim, float shf, float slf);
 
 /* --- Z-Image S3-DiT --- */
 orc_zi_t *orc_zi_load(const char *model_dir, int dim, int heads, int layers, int refiners,

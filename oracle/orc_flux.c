@@ -27,6 +27,9 @@ struct orc_flux {
     float *mod_dimg, *mod_dtxt, *mod_single, *final_mod, *proj_out;
     orc_dbl_t *dbl;
     orc_sgl_t *sgl;
+    /* SREF RoPE band control (iris_transformer_flux.c:326-335); off when both are 1 */
+    float sref_shf, sref_slf;
+    int sref_set;   /* 0: never set (calloc), bands off */
 };
 
 /* ------------------------------------------------------------------ config */
@@ -433,12 +436,15 @@ void orc_flux_double_block(orc_flux_t *m, int idx, float *img, float *txt,
     free(ck); free(cv); free(iattn); free(tattn); free(iproj); free(tproj);
 }
 
-/* single_block_forward, iris_transformer_flux.c:3761-3928 (SREF/LoRA/IP off).
- * seq = txt + img rows, img_offset = txt rows. */
-void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
-                           const float *img_cos, const float *img_sin,
-                           const float *txt_cos, const float *txt_sin,
-                           int seq, int img_offset) {
+/* single_block_forward, iris_transformer_flux.c:3761-3928 (LoRA/IP off).
+ * seq = txt + img rows, img_offset = txt rows. K of the img rows rotates with
+ * kimg_cos/kimg_sin: the SREF band-scaled table when band control is on
+ * (:3869-3875), else the Q table. */
+void orc_flux_single_block_k(orc_flux_t *m, int idx, float *x, const float *t_emb,
+                             const float *img_cos, const float *img_sin,
+                             const float *kimg_cos, const float *kimg_sin,
+                             const float *txt_cos, const float *txt_sin,
+                             int seq, int img_offset) {
     const orc_sgl_t *b = &m->sgl[idx];
     int h = m->hidden, H = m->heads, hd = m->head_dim, mlp = m->mlp;
     int fused = 3 * h + 2 * mlp, I = seq - img_offset, T = img_offset;
@@ -470,7 +476,7 @@ void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
     apply_rope(q, txt_cos, txt_sin, T, H, hd);
     apply_rope(k, txt_cos, txt_sin, T, H, hd);
     apply_rope(q + (size_t)T * h, img_cos, img_sin, I, H, hd);
-    apply_rope(k + (size_t)T * h, img_cos, img_sin, I, H, hd);
+    apply_rope(k + (size_t)T * h, kimg_cos, kimg_sin, I, H, hd);
     float *attn = (float *)malloc((size_t)seq * h * sizeof(float));
     attention(attn, q, k, v, seq, seq, H, hd);
     orc_silu_mul(g, u, (size_t)seq * mlp);
@@ -483,6 +489,41 @@ void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
     gated_add(x, gate, norm, seq, h);
     free(ts); free(mod); free(norm); free(q); free(k); free(v); free(g); free(u);
     free(attn); free(cat);
+}
+
+void orc_flux_single_block(orc_flux_t *m, int idx, float *x, const float *t_emb,
+                           const float *img_cos, const float *img_sin,
+                           const float *txt_cos, const float *txt_sin,
+                           int seq, int img_offset) {
+    orc_flux_single_block_k(m, idx, x, t_emb, img_cos, img_sin, img_cos, img_sin, txt_cos, txt_sin, seq,
+                            img_offset);
+}
+
+/* iris_transformer_set_sref_bands, iris_transformer_flux.c:5153-5157: out-of-range values switch off */
+void orc_flux_set_sref_bands(orc_flux_t *m, float shf, float slf) {
+    m->sref_shf = (shf >= 0.0f && shf <= 1.0f) ? shf : 1.0f;
+    m->sref_slf = (slf >= 1.0f) ? slf : 1.0f;
+    m->sref_set = 1;
+}
+
+/* band_scale_ref_krope, iris_transformer_flux.c:1271-1292: the H (axis 1)
+ * and W (axis 2) rotation pairs d of rows [ref_start, rows) scaled by
+ * shf + (slf - shf) (d / (half - 1))^2, tables [rows][4 * axis_dim] */
+void orc_sref_band_scale(float *c, float *s, int ref_start, int rows, int axis_dim, float shf, float slf) {
+    const int half = axis_dim / 2;
+    float sd[64];
+    for (int d = 0; d < half && d < 64; d++) {
+        const float dn = half > 1 ? (float)d / (float)(half - 1) : 0.0f;
+        sd[d] = shf + (slf - shf) * dn * dn;
+    }
+    for (int r = ref_start; r < rows; r++) {
+        float *cr = c + (size_t)r * axis_dim * 4, *sr = s + (size_t)r * axis_dim * 4;
+        for (int d = 0; d < half; d++) {
+            const int a = axis_dim + 2 * d, b = 2 * axis_dim + 2 * d;
+            cr[a] *= sd[d]; cr[a + 1] *= sd[d]; sr[a] *= sd[d]; sr[a + 1] *= sd[d];
+            cr[b] *= sd[d]; cr[b + 1] *= sd[d]; sr[b] *= sd[d]; sr[b + 1] *= sd[d];
+        }
+    }
 }
 
 /* ---------------------------------------------------------------- forward */
@@ -511,6 +552,17 @@ static float *forward_impl(orc_flux_t *m, const float *latent, int ih, int iw,
     float *tcos = (float *)malloc((size_t)T * hd * sizeof(float));
     float *tsin = (float *)malloc((size_t)T * hd * sizeof(float));
     orc_rope_txt(tcos, tsin, T, ad, m->theta);
+    /* SREF K-side table (set_kside_krope, :1297-1322, built at :4660): a copy
+     * of the image table with the reference rows band-scaled; single blocks
+     * rotate K with it, double blocks with the plain table */
+    float *kcos = icos, *ksin = isin;
+    if (n_refs > 0 && m->sref_set && !(m->sref_shf == 1.0f && m->sref_slf == 1.0f)) {
+        kcos = (float *)malloc((size_t)I * hd * sizeof(float));
+        ksin = (float *)malloc((size_t)I * hd * sizeof(float));
+        memcpy(kcos, icos, (size_t)I * hd * sizeof(float));
+        memcpy(ksin, isin, (size_t)I * hd * sizeof(float));
+        orc_sref_band_scale(kcos, ksin, I0, I, ad, m->sref_shf, m->sref_slf);
+    }
     /* NCHW -> NLC, :3986-3993 and :4667-4689 */
     float *tok = (float *)malloc((size_t)I * C * sizeof(float));
     for (int p = 0; p < I0; p++)
@@ -536,7 +588,8 @@ static float *forward_impl(orc_flux_t *m, const float *latent, int ih, int iw,
     memcpy(cat, txth, (size_t)T * h * sizeof(float));
     memcpy(cat + (size_t)T * h, img, (size_t)I * h * sizeof(float));
     for (int i = 0; i < m->n_single; i++)
-        orc_flux_single_block(m, i, cat, t_emb, icos, isin, tcos, tsin, S, T);
+        orc_flux_single_block_k(m, i, cat, t_emb, icos, isin, kcos, ksin, tcos, tsin, S, T);
+    if (kcos != icos) { free(kcos); free(ksin); }
     /* final layer, :4254-4301: (scale, shift) order */
     float *fm = (float *)malloc((size_t)2 * h * sizeof(float));
     orc_flux_modulation(m, t_emb, NULL, NULL, NULL, fm);

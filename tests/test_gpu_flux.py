@@ -370,8 +370,9 @@ def test_sref_bands(lib, tiny):
     own (golden vector flux_fwd_refs_sref_bands from oracle/_ref) at the
     forward bar. On this random-init model the bands move the velocity by
     0.15 %, below the bf16 difference between two GPU forwards, so the
-    direction of the change is printed, not asserted; the K-side rotation
-    itself is pinned by test_qk_prepare[True]."""
+    direction of the change is printed here and asserted at the block level
+    (test_sref_bands_block_effect); the K-side rotation itself is pinned by
+    test_qk_prepare[True]."""
     lib.iris_transformer_set_sref_bands.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_float]
     lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
     r1, r2 = tl.synth_f32((128, 8, 8), 23), tl.synth_f32((128, 4, 6), 24)
@@ -405,6 +406,59 @@ def test_sref_bands(lib, tiny):
           f"cosine {tl.cosine(d_gpu, d_ref):.4f}")
     ref = G["flux_fwd_refs_sref_bands"]
     assert tl.rel_l2(on, ref) < 1e-2 and tl.cosine(on, ref) > 0.999
+
+
+def test_sref_bands_block_effect(lib, orc, tiny, tiny_orc):
+    """The bands' effect where it is large enough to compare: one single
+    block on the resident multi-reference stream (32 txt + 64 target + 88
+    reference rows) with bands (0, 8) and (1, 1), against the oracle's single
+    block with the K-side table (iris_transformer_flux.c:3869-3875; the
+    oracle's band control is pinned against the reference's forward in
+    test_oracle.py::test_flux_sref_bands): the change of the block output
+    within rel-L2 5e-2. A double block ignores the bands (:2449-2450): its
+    output is bit-identical with and without them."""
+    lib.iris_transformer_set_sref_bands.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_float]
+    orc.orc_flux_single_block_k.argtypes = [ctypes.c_void_p, ctypes.c_int] + [tl.FP] * 8 + [ctypes.c_int] * 2
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    r1, r2 = tl.synth_f32((128, 8, 8), 23), tl.synth_f32((128, 4, 6), 24)
+    refs = (tl.IrisRef * 2)(tl.IrisRef(tl.fptr(r1), 8, 8, 1), tl.IrisRef(tl.fptr(r2), 4, 6, 2))
+    T, h = 32, 256
+    S = T + 64 + 64 + 24
+    x, temb = tl.synth_f32((S, h), 81), tl.synth_f32((h,), 82)
+    sgl = np.zeros(3 * h, np.float32)
+    orc.orc_flux_modulation(tiny_orc, tl.fptr(temb), None, None, tl.fptr(sgl), None)
+    dmod = tl.synth_f32((12 * h,), 83, 0.0, 0.5)
+
+    def tables(name):
+        t = np.empty((S, 128), np.float32)
+        lib.iris_hip_memcpy_d2h(t.ctypes.data, buf(lib, tiny, name), t.nbytes)
+        return t
+
+    out = {}
+    for bands in ((0.0, 8.0), (1.0, 1.0)):
+        lib.iris_transformer_set_sref_bands(tiny, *bands)
+        take(lib, lib.iris_transformer_forward_with_multi_refs(tiny, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(txt), 32,
+                                                               F(0.6)), 8192)
+        put(lib, buf(lib, tiny, "x"), x)
+        put(lib, buf(lib, tiny, "mod"), np.concatenate([dmod, sgl]))
+        assert lib.iris_flux_single_block_forward(tiny, 1) == 0, lib.iris_hip_last_error()
+        got = tl.d2h_f32(lib, buf(lib, tiny, "x"), (S, h))
+        put(lib, buf(lib, tiny, "x"), x)
+        assert lib.iris_flux_double_block_forward(tiny, 1) == 0, lib.iris_hip_last_error()
+        dbl = tl.d2h_f32(lib, buf(lib, tiny, "x"), (S, h))
+        qc, qs, kc, ks = (tables(n) for n in ("rope_cos", "rope_sin", "krope_cos", "krope_sin"))
+        ref = x.copy()
+        orc.orc_flux_single_block_k(tiny_orc, 1, tl.fptr(ref), tl.fptr(temb), tl.fptr(qc[T:]), tl.fptr(qs[T:]),
+                                    tl.fptr(kc[T:]), tl.fptr(ks[T:]), tl.fptr(qc[:T]), tl.fptr(qs[:T]), S, T)
+        out[bands] = (got, ref, dbl)
+    (on, ref_on, dbl_on), (off, ref_off, dbl_off) = out[(0.0, 8.0)], out[(1.0, 1.0)]
+    eff = tl.rel_l2(on - off, ref_on - ref_off)
+    print(f"single block: bands move the output by {tl.rel_l2(ref_on - x, ref_off - x):.3e} of the block's "
+          f"update; effect rel_l2 {eff:.3e}; block rel_l2 {tl.rel_l2(on, ref_on):.3e}")
+    assert tl.rel_l2(on, ref_on) < 1e-2 and tl.rel_l2(off, ref_off) < 1e-2
+    assert eff <= 5e-2
+    assert np.array_equal(dbl_on, dbl_off)
+
 
 
 def test_sref_strength(lib, tiny):

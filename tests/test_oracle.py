@@ -234,6 +234,51 @@ def test_flux_forward_multi_refs(lib, flux):
     assert tl.rel_l2(out, G["flux_fwd_refs"]) < 1e-4
 
 
+def test_flux_sref_bands(lib, flux):
+    """SREF band control (0, 8) on the reference rows' K-side RoPE, single
+    blocks only: the forward and the bands' own effect (on - off) against
+    the reference's (golden flux_fwd_refs_sref_bands). The effect is 0.15 %
+    of the velocity; both sides compute in f32, so it is resolved to 1e-2.
+    Bands in the double blocks too, or the wrong rows scaled, miss it."""
+    lat, txt = tl.synth_f32((128, 8, 8), 21), tl.synth_f32((32, 256), 22)
+    r1, r2 = tl.synth_f32((128, 8, 8), 23), tl.synth_f32((128, 4, 6), 24)
+    refs = (Ref * 2)(Ref(tl.fptr(r1), 8, 8, 1), Ref(tl.fptr(r2), 4, 6, 2))
+    lib.orc_flux_set_sref_bands.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_float]
+
+    def fwd():
+        return tl.take_f32(lib, lib.orc_flux_forward_refs(flux, tl.fptr(lat), 8, 8, refs, 2, tl.fptr(txt), 32,
+                                                          F(0.6)), 8192)
+    off = fwd()
+    lib.orc_flux_set_sref_bands(flux, 0.0, 8.0)
+    on = fwd()
+    lib.orc_flux_set_sref_bands(flux, 1.0, 1.0)
+    assert np.array_equal(fwd(), off)
+    ref_on, ref_off = G["flux_fwd_refs_sref_bands"], G["flux_fwd_refs"]
+    assert tl.rel_l2(on, ref_on) < 1e-4
+    assert tl.rel_l2(on - off, ref_on - ref_off) < 1e-2
+
+
+def test_sref_band_scale_table(lib):
+    """orc_sref_band_scale: pairs d of the H and W axes scaled by
+    shf + (slf - shf) (d / 15)^2 from ref_start on; T and L axes and earlier
+    rows untouched (closed form in float64, 1 ulp)."""
+    rows, ref_start = 7, 3
+    c = tl.synth_f32((rows, 128), 51)
+    s = tl.synth_f32((rows, 128), 52)
+    c0, s0 = c.copy(), s.copy()
+    lib.orc_sref_band_scale.argtypes = [tl.FP, tl.FP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                        ctypes.c_float]
+    lib.orc_sref_band_scale(tl.fptr(c), tl.fptr(s), ref_start, rows, 32, 0.25, 4.0)
+    f = np.ones(128)
+    for d in range(16):
+        v = 0.25 + 3.75 * (d / 15) ** 2
+        f[32 + 2 * d:32 + 2 * d + 2] = v
+        f[64 + 2 * d:64 + 2 * d + 2] = v
+    for got, x0 in ((c, c0), (s, s0)):
+        np.testing.assert_array_equal(got[:ref_start], x0[:ref_start])
+        np.testing.assert_allclose(got[ref_start:], x0[ref_start:] * f, rtol=3e-7, atol=0)
+
+
 def test_flux_two_step_sample(lib, flux):
     """Euler loop (iris_sample.c:313-405) on the reference's noise and schedule."""
     sched = G["flux_sample2_sched"]
