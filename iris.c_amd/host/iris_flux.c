@@ -92,7 +92,9 @@ typedef struct {
     float *krope_cos, *krope_sin; /* [S][128] K side: the reference rows' H/W bands scaled (SREF) */
     float kshf, kslf;             /* band scales the K tables hold */
     float kgamma;                 /* SREF strength the captured graph applies */
-    int csd_on;                   /* the captured graph adds the CSD style delta to temb */
+    int csd_on;                   /* the captured graph adds d_csd (the CSD style delta, or
+                                   * zeros while it is skipped) to temb */
+    unsigned lora_gen;            /* tf->lora_gen the graph was captured at */
     float *tsin;             /* [256] */
     float *tmp, *temb;       /* [h] */
     float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
@@ -108,6 +110,9 @@ struct iris_transformer {
     dev_double_t *dbl;
     dev_single_t *sgl;
     work_t w;
+    work_t w_alt;                     /* the previous geometry's workspace and graph, kept so
+                                       * forwards alternating between two geometries (CFG with
+                                       * two text lengths) reuse both */
     /* adapters set through the reference's setters (owned, not applied) */
     void *lora, *ip, *ip_embeds;
     void *lora_built;                 /* the LoRA state the device adapters hold, or NULL */
@@ -118,9 +123,11 @@ struct iris_transformer {
     uint16_t *lu;                     /* [rows][lrp_max] bf16: u = x dn^T of the current linear */
     float *lws;                       /* split-K partials of the u products */
     size_t lu_rows, lws_floats;
-    int lora_stale;                   /* the step graph may hold LoRA buffers since changed or freed */
+    unsigned lora_gen;                /* bumped whenever ldev / lu / lws change: a graph captured
+                                       * at another value may hold freed LoRA buffers */
     float *d_csd;                     /* device copy of the CSD style delta [hidden] */
     float *csd_delta;
+    float *csd_zero;                  /* host zeros uploaded into d_csd while the delta is skipped */
     int csd_skip;
     float sref_shf, sref_slf, sref_strength;
 };
@@ -346,7 +353,9 @@ static void lora_seg(const iris_transformer_t *tf, iris_gemm_problem_t *p, const
 void iris_transformer_free(iris_transformer_t *tf) {
     if (!tf) return;
     work_free(&tf->w);
+    work_free(&tf->w_alt);
     lora_dev_free(tf);
+    free(tf->csd_zero);
     iris_hip_free(tf->d_csd);
     iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
     iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
@@ -496,8 +505,8 @@ static int capture(iris_transformer_t *tf) {
     work_t *w = &tf->w;
     if (w->graph) { iris_hip_graph_destroy(w->graph); w->graph = NULL; }
     w->kgamma = tf->sref_strength;
-    w->csd_on = tf->csd_delta && !tf->csd_skip;
-    tf->lora_stale = 0;
+    w->csd_on = tf->csd_delta != NULL;
+    w->lora_gen = tf->lora_gen;
     if (w->csd_on && !tf->d_csd && !(tf->d_csd = (float *)iris_hip_malloc((size_t)tf->hidden * 4))) return -1;
     if (iris_hip_graph_begin()) return -1;
     if (enqueue_forward(tf)) {
@@ -515,7 +524,16 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
     if (B < 1 || B > 2) { fprintf(stderr, "iris_hip: batch %d (1 or 2)\n", B); return -1; }
     if (ih <= 0 || iw <= 0 || T <= 0) { fprintf(stderr, "iris_hip: empty geometry\n"); return -1; }
     if (same_geometry(w, ih, iw, refs, n_refs, T, B)) return 0;
-    work_free(w);
+    if (same_geometry(&tf->w_alt, ih, iw, refs, n_refs, T, B)) {
+        const work_t t = tf->w;
+        tf->w = tf->w_alt;
+        tf->w_alt = t;
+        return 0;
+    }
+    /* the current workspace becomes the alternate one */
+    work_free(&tf->w_alt);
+    tf->w_alt = tf->w;
+    memset(w, 0, sizeof(*w));
     int h = tf->hidden, mlp = tf->mlp, C = tf->latent_ch, td = tf->text_dim, H = tf->heads;
     w->ih = ih; w->iw = iw; w->n_refs = n_refs; w->T = T; w->B = B;
     w->I0 = ih * iw;
@@ -843,7 +861,7 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
     work_t *w = &tf->w;
     if (!w->valid) return -1;
     if (adapter_active(tf)) return -1;
-    if (lora_sync(tf)) return -1;
+    if (lora_sync(tf) || lora_work(tf) < 0) return -1;
     /* SREF settings changed since the graph was captured */
     if (w->kshf != tf->sref_shf || w->kslf != tf->sref_slf) {
         const size_t n = (size_t)w->S * 128;
@@ -854,11 +872,23 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
         free(s);
         if (rc) return -1;
     }
-    const int csd_on = tf->csd_delta && !tf->csd_skip;
-    /* adapters rebuilt (the graph holds the old GEMM problems), SREF strength or CSD switched */
-    if ((tf->lora_stale || w->kgamma != tf->sref_strength || w->csd_on != csd_on) && capture(tf)) return -1;
-    if (csd_on && (iris_hip_memcpy_h2d(tf->d_csd, tf->csd_delta, (size_t)tf->hidden * 4) || iris_hip_sync()))
+    /* adapters rebuilt (the graph holds the old GEMM problems), SREF strength
+     * changed, or a CSD delta attached / removed. Skipping the CSD delta
+     * (csd_skip, flipped before every forward by the style-CFG sampler)
+     * uploads zeros instead: acc + 0 is the plain forward bit for bit, and
+     * the graph is kept. */
+    const int csd_on = tf->csd_delta != NULL;
+    if ((w->lora_gen != tf->lora_gen || w->kgamma != tf->sref_strength || w->csd_on != csd_on) && capture(tf))
         return -1;
+    if (csd_on) {
+        const size_t nb = (size_t)tf->hidden * 4;
+        if (tf->csd_skip) {
+            if (!tf->csd_zero && !(tf->csd_zero = (float *)calloc(tf->hidden, sizeof(float)))) return -1;
+            if (iris_hip_memcpy_h2d(tf->d_csd, tf->csd_zero, nb) || iris_hip_sync()) return -1;
+        } else if (iris_hip_memcpy_h2d(tf->d_csd, tf->csd_delta, nb) || iris_hip_sync()) {
+            return -1;
+        }
+    }
     /* get_timestep_embedding(t * 1000), :3967 */
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
@@ -931,7 +961,7 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
  * u is formed by a split-K GEMM per adapted linear and call. */
 static void lora_dev_free(iris_transformer_t *tf) {
     const int n = 4 * tf->n_double + 2 * tf->n_single;
-    if (tf->ldev || tf->lu || tf->lws) tf->lora_stale = 1;
+    if (tf->ldev || tf->lu || tf->lws) tf->lora_gen++;
     for (int i = 0; tf->ldev && i < n; i++) {
         iris_hip_free(tf->ldev[i].dn);
         iris_hip_free(tf->ldev[i].up);
@@ -1030,7 +1060,7 @@ static int lora_splits(int M, int K) {
 }
 
 /* u and split-K buffers for the prepared geometry; 1 if reallocated (a
- * captured graph holds the old addresses: lora_stale is set), 0 if
+ * captured graph holds the old addresses: lora_gen moves on), 0 if
  * unchanged, -1 on error */
 static int lora_work(iris_transformer_t *tf) {
     if (!tf->ldev || !tf->lrp_max || !tf->w.valid) return 0;
@@ -1038,7 +1068,7 @@ static int lora_work(iris_transformer_t *tf) {
     /* chunks * M <= 256 x 256 whenever the product is split (lora_splits) */
     const size_t wsf = (size_t)65536 * tf->lrp_max;
     if (rows <= tf->lu_rows && wsf <= tf->lws_floats) return 0;
-    tf->lora_stale = 1;
+    tf->lora_gen++;
     iris_hip_free(tf->lu);
     iris_hip_free(tf->lws);
     tf->lu = (uint16_t *)iris_hip_malloc(rows * tf->lrp_max * 2);
@@ -1058,8 +1088,9 @@ static int lora_work(iris_transformer_t *tf) {
 
 /* Device adapters for tf->lora; 0 when they match it, -1 on error (none are
  * applied then and the next forward tries again). Any change of the device
- * state sets lora_stale: the step graph must be captured again before its
- * next launch, also after a failed build freed the previous adapters. */
+ * state moves lora_gen on: a step graph captured before must be captured
+ * again before its next launch, also after a failed build freed the
+ * previous adapters. */
 static int lora_sync(iris_transformer_t *tf) {
     if (!tf->lora_dirty && tf->lora == tf->lora_built) return 0;
     tf->lora_dirty = 0;
@@ -1105,7 +1136,7 @@ static int lora_sync(iris_transformer_t *tf) {
     }
     if (lora_work(tf) < 0) goto fail;
     tf->lora_built = tf->lora;
-    tf->lora_stale = 1;
+    tf->lora_gen++;
     return 0;
 fail:
     lora_dev_free(tf);

@@ -591,6 +591,49 @@ def test_csd_delta_vs_reference(lib, tiny):
     assert np.array_equal(skipped, base) and np.array_equal(again, base)
 
 
+def test_style_cfg_alternating_geometries(lib, tiny):
+    """The style-CFG sampler with a CSD delta and two text lengths (32 cond,
+    20 uncond tokens; iris_sample.c:750-771): two forwards per step that
+    alternate geometry and the CSD skip flag. Both workspaces and the graph
+    stay cached; the sampled latent equals the same loop run forward by
+    forward, and repeating a forward after the loop gives the same bits."""
+    lib.iris_transformer_set_csd_delta.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    lib.iris_transformer_set_csd_skip.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    lib.iris_sample_euler_cfg.restype = ctypes.c_void_p
+    lib.iris_sample_euler_cfg.argtypes = [ctypes.c_void_p, ctypes.c_void_p, tl.FP] + [ctypes.c_int] * 4 + \
+        [tl.FP, ctypes.c_int, tl.FP, ctypes.c_int, F, tl.FP, ctypes.c_int, ctypes.c_void_p]
+    z0 = tl.synth_f32((128, 8, 8), 91)
+    tc, tu = tl.synth_f32((32, 256), 92), tl.synth_f32((20, 256), 93)
+    sched = np.array([1.0, 0.7, 0.35, 0.0], np.float32)
+    g = 3.5
+
+    def fwd(z, txt, T, t):
+        return take(lib, lib.iris_transformer_forward(tiny, tl.fptr(z), 8, 8, tl.fptr(txt), T, F(t)), 8192)
+
+    lib.iris_transformer_set_csd_delta(tiny, tl.c_floats(tl.synth_f32((256,), 94, 0.0, 0.5)))
+    zin = z0.copy()
+    got = take(lib, lib.iris_sample_euler_cfg(tiny, None, tl.fptr(zin), 1, 128, 8, 8, tl.fptr(tc), 32, tl.fptr(tu),
+                                              20, F(g), tl.fptr(sched), 3, None), 8192)
+    z = z0.reshape(-1).copy()
+    vus, vcs = [], []
+    for i in range(3):
+        lib.iris_transformer_set_csd_skip(tiny, 1)
+        vu = fwd(z, tu, 20, sched[i])
+        lib.iris_transformer_set_csd_skip(tiny, 0)
+        vc = fwd(z, tc, 32, sched[i])
+        vus.append(vu)
+        vcs.append(vc)
+        z = z + np.float32(sched[i + 1] - sched[i]) * (vu + np.float32(g) * (vc - vu))
+    print(f"style CFG: rel_l2 vs the forward-by-forward loop {tl.rel_l2(got, z):.3e}")
+    assert tl.rel_l2(got, z) < 1e-6
+    # fresh geometry each time: the same bits as through the cached workspaces
+    lib.iris_transformer_set_csd_skip(tiny, 1)
+    assert np.array_equal(fwd(z0, tu, 20, sched[0]), vus[0])
+    lib.iris_transformer_set_csd_skip(tiny, 0)
+    assert np.array_equal(fwd(z0, tc, 32, sched[0]), vcs[0])
+    lib.iris_transformer_set_csd_delta(tiny, None)
+
+
 def test_ip_adapter_fails_loudly(lib, tiny):
     """The IP-Adapter is the one adapter the HIP forward does not apply: while
     one is attached the forward fails with a message instead of ignoring it."""
