@@ -12,9 +12,12 @@ c4 (9B-shaped, CFG as batch 2), c5 (Z-Image-Turbo-6B-shaped, 8 NFE), qwen3
 
 Prints one JSON line. `value` is images/s; ms_per_step is per denoise step.
 `roofline` is the kernel class with the largest share of the step (the fused
-projection GEMM or the flash attention), timed per launch with HIP events on
-the library stream over back-to-back launches on the step's own resident
-buffers. `cpu_baseline` times the oracle (C restatement of the reference's
+projection GEMM or the flash attention). Its launch_ms is its average
+duration inside a step: after the timed steps one more step runs launch by
+launch with two HIP events on the library stream around every launch
+(iris_hip_profile_enable; the per-kernel table is `profiled_step`);
+back_to_back_launch_ms times the same kernel alone over 30 launches on the
+step's resident buffers. `cpu_baseline` times the oracle (C restatement of the reference's
 f32 `make blas` path on OpenBLAS) on one block of each kind at the same shape,
 extrapolated to a step.
 """
@@ -119,11 +122,46 @@ def time_launches(lib, fn, n=30, warm=3):
     return lib.iris_hip_event_elapsed_ms(2, 3) / n
 
 
-def kernel_entry(name, ms, flops, per_step, key=None):
-    return {"kernel": name, "key": key, "launch_ms": round(ms, 4), "flop_per_launch": flops,
-            "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-            "frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4), "launches_per_step": per_step,
-            "ms_per_step": round(ms * per_step, 3)}
+def kernel_entry(name, ms, flops, per_step, key=None, b2b_ms=None):
+    """One kernel class: launch_ms is its average duration inside the step
+    (profiled step), b2b_ms over back-to-back launches of it alone."""
+    e = {"kernel": name, "key": key, "launch_ms": round(ms, 4), "flop_per_launch": flops,
+         "achieved_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+         "frac": round(flops / (ms * 1e-3) / PEAK_BF16, 4), "launches_per_step": per_step,
+         "ms_per_step": round(ms * per_step, 3)}
+    if b2b_ms is not None:
+        e["back_to_back_launch_ms"] = round(b2b_ms, 4)
+    return e
+
+
+def profile_step(lib, step, i):
+    """One more step launched kernel by kernel, each launch between two HIP
+    events on the library stream (iris_hip_profile_enable): calls and
+    durations per (kernel, grid) inside a step."""
+    assert lib.iris_hip_profile_enable(1) == 0
+    step(i)
+    recs = (tl.KernelTime * 256)()
+    n = lib.iris_hip_profile_read(recs, 256)
+    assert n > 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_profile_enable(0) == 0
+    rows = [{"kernel": r.kernel.decode(), "grid": r.grid, "calls": r.calls, "avg_ms": round(r.total_ms / r.calls, 4),
+             "total_ms": round(r.total_ms, 3)} for r in recs[:n]]
+    return sorted(rows, key=lambda r: -r["total_ms"])
+
+
+def in_step(prof, kernel, grid):
+    """Average in-step duration and calls of one (kernel, grid) entry."""
+    for r in prof:
+        if r["kernel"] == kernel and r["grid"] == grid:
+            return r["total_ms"] / r["calls"], r["calls"]
+    raise AssertionError(f"{kernel} with grid {grid} not in the profiled step")
+
+
+def gemm_grid(shapes):
+    """Workgroups of one iris_hip_gemm launch over (M, N) problems: 256x256
+    tiles, rounded up to whole groups of 8 (one per XCD)."""
+    t = sum(-(-m // 256) * -(-n // 256) for m, n in shapes)
+    return 8 * -(-t // 8)
 
 
 def run_flux(lib, c, args):
@@ -153,6 +191,7 @@ def run_flux(lib, c, args):
         assert lib.iris_flux_step(tf, float(sched[j]), float(sched[j + 1]), g) == 0, lib.iris_hip_last_error()
 
     ms_step, wall = timed_steps(lib, step, args)
+    prof = profile_step(lib, step, args.warmup + args.steps)
 
     # kernel classes on the step's own resident buffers
     h, mlp, H, B = c["h"], 3 * c["h"], c["H"], c["B"]
@@ -176,15 +215,18 @@ def run_flux(lib, c, args):
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
     wdev.close()
     wq.close()
-    kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_ms,
-                            2.0 * BS * h * (3 * h + 2 * mlp), c["ns"], f"gemm_fused_{args.config}"),
-               kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_ms, 4.0 * B * S * S * h,
-                            c["nd"] + c["ns"], f"attn_{args.config}")]
+    g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(BS, 3 * h), (BS, 2 * mlp)]))
+    a_in, a_n = in_step(prof, "flash_attn_kernel<1>", 8 * -(-(-(-S // 256) * H * B) // 8))
+    assert g_n == c["ns"] and a_n == c["nd"] + c["ns"], (g_n, a_n)
+    kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_in,
+                            2.0 * BS * h * (3 * h + 2 * mlp), g_n, f"gemm_fused_{args.config}", g_ms),
+               kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_in, 4.0 * B * S * S * h, a_n,
+                            f"attn_{args.config}", a_ms)]
     lib.iris_transformer_free(tf)
     cfg = {"workload": c["workload"], "hidden": h, "heads": H, "double_blocks": c["nd"], "single_blocks": c["ns"],
            "image_tokens": I0, "reference_tokens": S - I0 - c["T"], "text_tokens": c["T"], "seq": S, "batch": B,
            "steps_per_image": c["steps"]}
-    return ms_step, wall, flux_flops(c), kernels, cfg, t_load
+    return ms_step, wall, flux_flops(c), kernels, cfg, t_load, prof
 
 
 def run_zimage(lib, c, args):
@@ -211,6 +253,7 @@ def run_zimage(lib, c, args):
         assert lib.zi_step(tf, float(sched[j]), float(sched[j + 1])) == 0, lib.iris_hip_last_error()
 
     ms_step, wall = timed_steps(lib, step, args)
+    prof = profile_step(lib, step, args.warmup + args.steps)
 
     d, f, H = c["d"], c["ffn"], c["H"]
     S = I + c["cap"]
@@ -230,14 +273,17 @@ def run_zimage(lib, c, args):
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
     for b in (q, k, vt, o):
         b.close()
-    kernels = [kernel_entry("gemm_bf16_kernel: FFN w1/w3 (SwiGLU epilogue)", g_ms, 2.0 * S * d * 2 * f,
-                            c["layers"]),
-               kernel_entry("flash_attn_kernel: unified attention, head_dim 128", a_ms, 4.0 * S * S * d,
-                            c["layers"])]
+    g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(S, 2 * f)]))
+    a_in, a_n = in_step(prof, "flash_attn_kernel<1>", 8 * -(-(-(-S // 256) * H) // 8))
+    assert g_n == c["layers"] and a_n == c["layers"], (g_n, a_n)
+    kernels = [kernel_entry("gemm_bf16_kernel: FFN w1/w3 (SwiGLU epilogue)", g_in, 2.0 * S * d * 2 * f, g_n,
+                            f"gemm_ffn_{args.config}", g_ms),
+               kernel_entry("flash_attn_kernel: unified attention, head_dim 128", a_in, 4.0 * S * S * d, a_n,
+                            f"attn_{args.config}", a_ms)]
     lib.zi_transformer_free(tf)
     cfg = {"workload": c["workload"], "dim": d, "heads": H, "layers": c["layers"], "refiners": c["refiners"],
            "image_tokens": I, "caption_tokens": c["cap"], "seq": S, "batch": 1, "steps_per_image": c["steps"]}
-    return ms_step, wall, zimage_flops(c), kernels, cfg, t_load
+    return ms_step, wall, zimage_flops(c), kernels, cfg, t_load, prof
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_rocprof_pmc.md")
@@ -364,7 +410,7 @@ def run_qwen3(lib, c, args):
                             "gemm_qwen3_gateup")]
     cfg = {"workload": c["workload"], "hidden": h, "intermediate": I, "heads": c["H"], "kv_heads": c["KV"],
            "layers": c["layers"], "layers_run": 27, "tokens": S, "real_tokens": c["n_real"], "vocab": c["vocab"]}
-    return ms_step, wall, qwen3_flops(c), kernels, cfg, t_load
+    return ms_step, wall, qwen3_flops(c), kernels, cfg, t_load, None
 
 
 def cpu_baseline_qwen3(c):
@@ -441,7 +487,7 @@ def run_vae(lib, c, args):
                             2.0 * H * W * cin * cout * 9, 5, "conv_256_512")]
     cfg = {"workload": c["workload"], "latent": [4 * c["z"], lh, lw], "image": [16 * lh, 16 * lw],
            "z_channels": c["z"], "bottleneck_tokens": 4 * lh * lw}
-    return ms_step, wall, vae_flops(c), kernels, cfg, t_load
+    return ms_step, wall, vae_flops(c), kernels, cfg, t_load, None
 
 
 def cpu_baseline_vae(c):
@@ -488,7 +534,7 @@ def main():
     c = CONFIGS[args.config]
     lib = tl.hip()
     run = {"flux": run_flux, "zimage": run_zimage, "qwen3": run_qwen3, "vae": run_vae}[c["kind"]]
-    ms_step, wall_ms, flops, kernels, cfg, t_load = run(lib, c, args)
+    ms_step, wall_ms, flops, kernels, cfg, t_load, prof = run(lib, c, args)
     images_per_s = 1000.0 / (ms_step * c["steps"])   # one image per pass (CFG: both branches in one)
     dom = max(kernels, key=lambda k: k["ms_per_step"])
     result = {
@@ -519,6 +565,10 @@ def main():
         "kernels": kernels,
         "device": lib.iris_hip_device_name().decode(),
     }
+    if prof:
+        # the profiled step: every launch between two events, the launches issued one by one
+        result["profiled_step"] = {"kernel_ms": round(sum(r["total_ms"] for r in prof), 3),
+                                   "top": prof[:10]}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = {"qwen3": cpu_baseline_qwen3, "vae": cpu_baseline_vae}.get(c["kind"], cpu_baseline)(c)
     print(json.dumps(result))

@@ -44,6 +44,25 @@ size_t iris_hip_mem_in_use(void);
 int iris_hip_event_record(int slot);                 /* slot 0..63 */
 float iris_hip_event_elapsed_ms(int slot_start, int slot_end);
 
+/* ---- per-kernel profile of eager launches ----
+ * No counterpart in the reference's interface; it backs the reference's
+ * profile counters (iris_print_blas_profile / iris_reset_blas_profile,
+ * iris_transformer_flux.c:55-80). While enabled, every kernel the library
+ * launches outside graph capture is bracketed by two events on the library
+ * stream, and the denoiser runs its forward launch by launch instead of
+ * replaying its captured graph, so the records cover a whole step.
+ * enable() syncs and clears the records; read() syncs and aggregates them by
+ * (kernel, grid size) into out (at most max entries; returns the count). */
+typedef struct {
+    const char *kernel;   /* the kernel as launched, e.g. "gemm_bf16_kernel<0>" */
+    long long grid;       /* workgroups per launch */
+    int calls;
+    double total_ms, min_ms, max_ms;
+} iris_kernel_time_t;
+int iris_hip_profile_enable(int on);
+int iris_hip_profile_enabled(void);
+int iris_hip_profile_read(iris_kernel_time_t *out, int max);
+
 /* ---- graph capture of the library stream (cf. iris_gpu_batch_begin/end) ---- */
 int iris_hip_graph_begin(void);
 void *iris_hip_graph_end(void);                      /* instantiated graph, NULL on error */

@@ -408,8 +408,13 @@ int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, in
             return -1;
         attr_set = true;
     }
-    hipLaunchKernelGGL(flash_attn_kernel<FEAT>, dim3(8 * per_xcd), dim3(NT), smem, iris_stream(), *a,
-                       scale_log2, nqb, per_xcd, total);
+    static const char *const name[8] = {"flash_attn_kernel<0>", "flash_attn_kernel<1>", "flash_attn_kernel<2>",
+                                        "flash_attn_kernel<3>", "flash_attn_kernel<4>", "flash_attn_kernel<5>",
+                                        "flash_attn_kernel<6>", "flash_attn_kernel<7>"};
+    const int prof = iris_prof_begin(name[FEAT & 7], 8LL * per_xcd);
+    hipLaunchKernelGGL(flash_attn_kernel<FEAT>, dim3(8 * per_xcd), dim3(NT), smem, iris_stream(), *a, scale_log2, nqb,
+                       per_xcd, total);
+    iris_prof_end(prof);
     return iris_launch_check("flash_attn_kernel");
 }
 

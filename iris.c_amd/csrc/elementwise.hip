@@ -391,11 +391,11 @@ int iris_hip_rownorm(const iris_norm_args_t *a) {
 #define ROWNORM_CASE(VV)                                                                                          \
     case VV:                                                                                                      \
         if (a->mode == IRIS_NORM_LN_MOD)                                                                          \
-            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_LN_MOD>), grid, dim3(NT), 0, iris_stream(), b);      \
+            IRIS_LAUNCH((rownorm_kernel<VV, IRIS_NORM_LN_MOD>), grid, dim3(NT), 0, iris_stream(), b);      \
         else if (a->mode == IRIS_NORM_LN_SCALE)                                                                   \
-            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_LN_SCALE>), grid, dim3(NT), 0, iris_stream(), b);    \
+            IRIS_LAUNCH((rownorm_kernel<VV, IRIS_NORM_LN_SCALE>), grid, dim3(NT), 0, iris_stream(), b);    \
         else                                                                                                      \
-            hipLaunchKernelGGL((rownorm_kernel<VV, IRIS_NORM_RMS>), grid, dim3(NT), 0, iris_stream(), b);         \
+            IRIS_LAUNCH((rownorm_kernel<VV, IRIS_NORM_RMS>), grid, dim3(NT), 0, iris_stream(), b);         \
         break;
     switch (v) {
         ROWNORM_CASE(1) ROWNORM_CASE(2) ROWNORM_CASE(3) ROWNORM_CASE(4)
@@ -412,11 +412,11 @@ int iris_hip_rms_gated_add(float *x, const float *y, const float *w, const float
     if (cols % 4 || cols <= 0 || need > 16) return iris_set_error("rms_gated_add: cols=%d", cols);
     const dim3 grid(rows);
     switch (need) {
-    case 1: hipLaunchKernelGGL(rms_gated_add_kernel<1>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
-    case 2: hipLaunchKernelGGL(rms_gated_add_kernel<2>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
-    case 3: hipLaunchKernelGGL(rms_gated_add_kernel<3>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
-    case 4: hipLaunchKernelGGL(rms_gated_add_kernel<4>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
-    default: hipLaunchKernelGGL(rms_gated_add_kernel<16>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 1: IRIS_LAUNCH(rms_gated_add_kernel<1>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 2: IRIS_LAUNCH(rms_gated_add_kernel<2>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 3: IRIS_LAUNCH(rms_gated_add_kernel<3>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    case 4: IRIS_LAUNCH(rms_gated_add_kernel<4>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
+    default: IRIS_LAUNCH(rms_gated_add_kernel<16>, grid, dim3(NT), 0, iris_stream(), x, y, w, gate, rows, cols, eps, gate_tanh); break;
     }
     return iris_launch_check("rms_gated_add_kernel");
 }
@@ -429,11 +429,11 @@ int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
         return iris_set_error("qk_prepare: heads=%d kv_heads=%d", a->heads, a->kv_heads);
     if (((uintptr_t)a->qkv | (uintptr_t)a->q_out | (uintptr_t)a->k_out | (uintptr_t)a->vt_out) & 15)
         return iris_set_error("qk_prepare: buffers must be 16-byte aligned");
-    hipLaunchKernelGGL(qk_norm_rope_kernel<false>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+    IRIS_LAUNCH(qk_norm_rope_kernel<false>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
                        iris_stream(), *a);
     if (iris_launch_check("qk_norm_rope_kernel")) return -1;
     const int kvh = a->kv_heads ? a->kv_heads : a->heads;
-    hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
+    IRIS_LAUNCH(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
     return iris_launch_check("v_transpose_kernel");
 }
 
@@ -448,63 +448,63 @@ int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
          (uintptr_t)a->cos_t | (uintptr_t)a->sin_t | (uintptr_t)a->kcos_t | (uintptr_t)a->ksin_t) & 15)
         return iris_set_error("kv_prepare: buffers must be 16-byte aligned");
     const int kvh = a->kv_heads ? a->kv_heads : a->heads;
-    hipLaunchKernelGGL(qk_norm_rope_kernel<true>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+    IRIS_LAUNCH(qk_norm_rope_kernel<true>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
                        iris_stream(), *a);
     if (iris_launch_check("qk_norm_rope_kernel<K>")) return -1;
-    hipLaunchKernelGGL(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
+    IRIS_LAUNCH(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
     return iris_launch_check("v_transpose_kernel");
 }
 
 int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias, int N, int K, int act_in) {
     if (N <= 0) return 0;
     if (K % 8) return iris_set_error("gemv: K=%d must be a multiple of 8", K);
-    hipLaunchKernelGGL(gemv_kernel, dim3((N + 3) / 4), dim3(NT), 0, iris_stream(), y, W, x, bias, N, K, act_in);
+    IRIS_LAUNCH(gemv_kernel, dim3((N + 3) / 4), dim3(NT), 0, iris_stream(), y, W, x, bias, N, K, act_in);
     return iris_launch_check("gemv_kernel");
 }
 
 int iris_hip_nchw_to_tokens(uint16_t *out, const float *lat, int C, int hw) {
     if (hw <= 0) return 0;
-    hipLaunchKernelGGL(nchw_to_tokens_kernel, dim3((hw + 63) / 64, (C + 63) / 64), dim3(NT), 0, iris_stream(), out,
+    IRIS_LAUNCH(nchw_to_tokens_kernel, dim3((hw + 63) / 64, (C + 63) / 64), dim3(NT), 0, iris_stream(), out,
                        lat, C, hw);
     return iris_launch_check("nchw_to_tokens_kernel");
 }
 
 int iris_hip_f32_to_bf16(uint16_t *o, const float *x, size_t n) {
     if (!n) return 0;
-    hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, x, n);
+    IRIS_LAUNCH(f32_to_bf16_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, x, n);
     return iris_launch_check("f32_to_bf16_kernel");
 }
 
 int iris_hip_bf16_to_f32(float *o, const uint16_t *x, size_t n) {
     if (!n) return 0;
-    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, x, n);
+    IRIS_LAUNCH(bf16_to_f32_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, x, n);
     return iris_launch_check("bf16_to_f32_kernel");
 }
 
 int iris_hip_euler(float *z, const float *v, const float *v2, float g, float dt, float sign, size_t n) {
     if (!n) return 0;
-    hipLaunchKernelGGL(euler_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), z, v, v2, g, dt, sign, n);
+    IRIS_LAUNCH(euler_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), z, v, v2, g, dt, sign, n);
     return iris_launch_check("euler_kernel");
 }
 
 int iris_hip_patchify(uint16_t *o, const float *lat, int C, int H, int W, int ps) {
     size_t n = (size_t)(H / ps) * (W / ps) * ps * ps * C;
     if (!n) return 0;
-    hipLaunchKernelGGL(patchify_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, lat, C, H, W, ps);
+    IRIS_LAUNCH(patchify_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), o, lat, C, H, W, ps);
     return iris_launch_check("patchify_kernel");
 }
 
 int iris_hip_unpatchify(float *lat, const float *pt, int C, int H, int W, int ps) {
     size_t n = (size_t)(H / ps) * (W / ps) * ps * ps * C;
     if (!n) return 0;
-    hipLaunchKernelGGL(unpatchify_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), lat, pt, C, H, W, ps);
+    IRIS_LAUNCH(unpatchify_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), lat, pt, C, H, W, ps);
     return iris_launch_check("unpatchify_kernel");
 }
 
 int iris_hip_fill_rows(float *x, const float *row, int r0, int r1, int cols) {
     if (r1 <= r0) return 0;
     size_t n = (size_t)(r1 - r0) * cols;
-    hipLaunchKernelGGL(fill_rows_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), x, row, r0, r1, cols);
+    IRIS_LAUNCH(fill_rows_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), x, row, r0, r1, cols);
     return iris_launch_check("fill_rows_kernel");
 }
 
@@ -513,14 +513,14 @@ int iris_hip_embed_rows(float *out, const uint16_t *table, const int *ids, int r
     if (cols <= 0 || vocab <= 0) return iris_set_error("embed_rows: cols=%d vocab=%d", cols, vocab);
     if (cols % 8 || ((uintptr_t)out | (uintptr_t)table) & 15)
         return iris_set_error("embed_rows: cols %% 8 and 16-byte aligned buffers required");
-    hipLaunchKernelGGL(embed_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), out, table, ids, rows, cols, vocab);
+    IRIS_LAUNCH(embed_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), out, table, ids, rows, cols, vocab);
     return iris_launch_check("embed_rows_kernel");
 }
 
 int iris_hip_copy_rows(float *dst, int ld_dst, const float *src, int ld_src, int rows, int cols) {
     if (rows <= 0 || cols <= 0) return 0;
     if (ld_dst < cols || ld_src < cols) return iris_set_error("copy_rows: ld_dst=%d ld_src=%d < cols=%d", ld_dst, ld_src, cols);
-    hipLaunchKernelGGL(copy_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), dst, ld_dst, src, ld_src, rows, cols);
+    IRIS_LAUNCH(copy_rows_kernel, dim3(rows), dim3(NT), 0, iris_stream(), dst, ld_dst, src, ld_src, rows, cols);
     return iris_launch_check("copy_rows_kernel");
 }
 

@@ -552,9 +552,9 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     bool seg2 = false;
     for (int i = 0; i < n; i++) seg2 = seg2 || probs[i].K2 > 0;
     if (seg2)
-        hipLaunchKernelGGL(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     else
-        hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     return iris_launch_check("gemm_bf16_kernel");
 }
 
@@ -632,10 +632,10 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     P.kchunk = kchunk;
     P.ws = ws;
     P.ws_stride = stride;
-    hipLaunchKernelGGL(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    IRIS_LAUNCH(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel")) return -1;
     const size_t n_out = (size_t)p->M * (p->epi == IRIS_EPI_SWIGLU ? p->N / 2 : p->N);
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
+    IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
                        ws, stride, chunks);
     return iris_launch_check("splitk_reduce_kernel");
 }
@@ -700,13 +700,13 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
         P.ws_stride = stride;
     }
     if (c->up == 2)
-        hipLaunchKernelGGL(gemm_bf16_kernel<2>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<2>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     else
-        hipLaunchKernelGGL(gemm_bf16_kernel<1>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<1>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel<conv>")) return -1;
     if (chunks == 1) return 0;
     const size_t n_out = (size_t)p.M * p.N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), p,
+    IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), p,
                        c->ws, stride, chunks);
     return iris_launch_check("splitk_reduce_kernel");
 }

@@ -250,7 +250,7 @@ int iris_hip_split_rows(uint16_t *dst, const float *src, int rows, int cols, int
     if (rows <= 0 || K_pad <= 0) return 0;
     if (K_pad < cols || nseg < 1 || nseg > 3) return iris_set_error("split_rows: cols %d K_pad %d", cols, K_pad);
     const size_t n = (size_t)rows * K_pad;
-    hipLaunchKernelGGL(split_rows_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, src, rows, cols, ld_src,
+    IRIS_LAUNCH(split_rows_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, src, rows, cols, ld_src,
                        K_pad, nseg, lo_mask);
     return iris_launch_check("split_rows_kernel");
 }
@@ -258,7 +258,7 @@ int iris_hip_split_rows(uint16_t *dst, const float *src, int rows, int cols, int
 int iris_hip_split_transpose(uint16_t *dst, const float *src, int K, int N, int K_pad, int nseg, int lo_mask) {
     if (K <= 0 || N <= 0) return 0;
     if (K_pad < K || nseg < 1 || nseg > 3) return iris_set_error("split_transpose: K %d K_pad %d", K, K_pad);
-    hipLaunchKernelGGL(split_transpose_kernel, dim3((N + 31) / 32, (K_pad + 31) / 32), dim3(NT), 0, iris_stream(),
+    IRIS_LAUNCH(split_transpose_kernel, dim3((N + 31) / 32, (K_pad + 31) / 32), dim3(NT), 0, iris_stream(),
                        dst, src, K, N, K_pad, nseg, lo_mask);
     return iris_launch_check("split_transpose_kernel");
 }
@@ -267,7 +267,7 @@ int iris_hip_pad_bf16(uint16_t *dst, const uint16_t *src, int rows, int cols, in
     if (rows <= 0 || K_pad <= 0) return 0;
     if (K_pad < cols || nseg < 1 || nseg > 3) return iris_set_error("pad_bf16: cols %d K_pad %d", cols, K_pad);
     const size_t n = (size_t)rows * K_pad;
-    hipLaunchKernelGGL(pad_bf16_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, src, rows, cols, K_pad,
+    IRIS_LAUNCH(pad_bf16_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, src, rows, cols, K_pad,
                        nseg);
     return iris_launch_check("pad_bf16_kernel");
 }
@@ -277,34 +277,34 @@ int iris_hip_im2col_split(uint16_t *dst, const float *in, int C, int H, int W, i
     if (npix <= 0) return 0;
     if (K_pad < C * kH * kW || nseg < 1 || nseg > 3) return iris_set_error("im2col: K_pad %d", K_pad);
     const size_t n = (size_t)npix * K_pad;
-    hipLaunchKernelGGL(im2col_split_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, in, C, H, W, kH, kW,
+    IRIS_LAUNCH(im2col_split_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), dst, in, C, H, W, kH, kW,
                        stride, pad, outW, pix0, npix, C * kH * kW, K_pad, nseg, lo_mask);
     return iris_launch_check("im2col_split_kernel");
 }
 
 int iris_hip_rms_rows(float *out, const float *x, const float *w, int rows, int cols, float eps) {
     if (rows <= 0 || cols <= 0) return 0;
-    hipLaunchKernelGGL(rms_rows_kernel, dim3((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
+    IRIS_LAUNCH(rms_rows_kernel, dim3((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
                        iris_stream(), out, x, w, rows, cols, eps);
     return iris_launch_check("rms_rows_kernel");
 }
 
 int iris_hip_elementwise(int op, float *out, const float *a, const float *b, float s, size_t n) {
     if (!n) return 0;
-    hipLaunchKernelGGL(ew_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), op, out, a, b, s, n);
+    IRIS_LAUNCH(ew_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), op, out, a, b, s, n);
     return iris_launch_check("ew_kernel");
 }
 
 int iris_hip_add_row_bias(float *out, const float *bias, int rows, int cols, int ld) {
     const size_t n = (size_t)rows * cols;
     if (!n) return 0;
-    hipLaunchKernelGGL(add_row_bias_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, bias, rows, cols, ld);
+    IRIS_LAUNCH(add_row_bias_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, bias, rows, cols, ld);
     return iris_launch_check("add_row_bias_kernel");
 }
 
 int iris_hip_softmax_rows(float *x, int rows, int cols) {
     if (rows <= 0 || cols <= 0) return 0;
-    hipLaunchKernelGGL(softmax_rows_kernel, dim3((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0, iris_stream(), x,
+    IRIS_LAUNCH(softmax_rows_kernel, dim3((rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0, iris_stream(), x,
                        rows, cols);
     return iris_launch_check("softmax_rows_kernel");
 }
@@ -312,7 +312,7 @@ int iris_hip_softmax_rows(float *x, int rows, int cols) {
 int iris_hip_group_norm(float *out, const float *x, const float *gamma, const float *beta, int batch, int channels,
                         int spatial, int groups, float eps) {
     if (batch <= 0 || groups <= 0 || channels % groups) return iris_set_error("group_norm: channels %% groups");
-    hipLaunchKernelGGL(group_norm_kernel, dim3(batch * groups), dim3(NT), 0, iris_stream(), out, x, gamma, beta,
+    IRIS_LAUNCH(group_norm_kernel, dim3(batch * groups), dim3(NT), 0, iris_stream(), out, x, gamma, beta,
                        channels, spatial, groups, eps);
     return iris_launch_check("group_norm_kernel");
 }
@@ -321,7 +321,7 @@ int iris_hip_batch_norm(float *out, const float *x, const float *mean, const flo
                         const float *beta, int batch, int channels, int spatial, float eps) {
     const size_t n = (size_t)batch * channels * spatial;
     if (!n) return 0;
-    hipLaunchKernelGGL(batch_norm_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, x, mean, var, gamma,
+    IRIS_LAUNCH(batch_norm_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, x, mean, var, gamma,
                        beta, channels, spatial, n, eps);
     return iris_launch_check("batch_norm_kernel");
 }
@@ -329,7 +329,7 @@ int iris_hip_batch_norm(float *out, const float *x, const float *mean, const flo
 int iris_hip_upsample_nearest(float *out, const float *in, int planes, int H, int W, int sh, int sw) {
     const size_t n = (size_t)planes * H * sh * W * sw;
     if (!n) return 0;
-    hipLaunchKernelGGL(upsample_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, in, H, W, sh, sw, n);
+    IRIS_LAUNCH(upsample_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, in, H, W, sh, sw, n);
     return iris_launch_check("upsample_kernel");
 }
 
@@ -337,7 +337,7 @@ int iris_hip_space_to_depth(float *out, const float *in, int batch, int C, int H
     const size_t n = (size_t)batch * C * H * W;
     if (!n) return 0;
     if (p <= 0 || H % p || W % p) return iris_set_error("space_to_depth: %dx%d not divisible by %d", H, W, p);
-    hipLaunchKernelGGL(space_to_depth_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, in, C, H, W, p,
+    IRIS_LAUNCH(space_to_depth_kernel, dim3(grid_for(n)), dim3(NT), 0, iris_stream(), out, in, C, H, W, p,
                        inverse, n);
     return iris_launch_check("space_to_depth_kernel");
 }
@@ -357,7 +357,7 @@ int iris_hip_attention_f32(float *o, const float *q, const float *k, const float
             return -1;
         attr = true;
     }
-    hipLaunchKernelGGL(attention_f32_kernel, dim3(sq, heads, batch), dim3(NT), smem, iris_stream(), o, q, k, v, sk, hd,
+    IRIS_LAUNCH(attention_f32_kernel, dim3(sq, heads, batch), dim3(NT), smem, iris_stream(), o, q, k, v, sk, hd,
                        scale, q_sb, q_sh, k_sb, k_sh, ld);
     return iris_launch_check("attention_f32_kernel");
 }

@@ -224,6 +224,77 @@ float iris_hip_event_elapsed_ms(int a, int b) {
     return ms;
 }
 
+/* ---- per-kernel profile ----
+ * Each record is one launch between two events; events are created on first
+ * use and reused, at most PROF_MAX launches per profile. */
+}  /* extern "C" */
+
+namespace {
+constexpr int PROF_MAX = 16384;
+struct ProfRec {
+    const char *kernel;
+    long long grid;
+};
+hipEvent_t g_pev[2 * PROF_MAX];
+int g_pev_made;
+ProfRec g_prec[PROF_MAX];
+int g_prof_on, g_prof_n, g_prof_lost;
+}  // namespace
+
+int iris_prof_begin(const char *kernel, long long grid) {
+    if (!g_prof_on) return -1;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return -1;
+    if (g_prof_n >= PROF_MAX) {
+        g_prof_lost++;
+        return -1;
+    }
+    const int i = g_prof_n;
+    while (g_pev_made < 2 * (i + 1))
+        if (hipEventCreate(&g_pev[g_pev_made]) == hipSuccess) g_pev_made++;
+        else return -1;
+    if (hipEventRecord(g_pev[2 * i], g_stream) != hipSuccess) return -1;
+    g_prec[i] = {kernel, grid};
+    g_prof_n++;
+    return i;
+}
+
+void iris_prof_end(int i) {
+    if (i >= 0) (void)hipEventRecord(g_pev[2 * i + 1], g_stream);
+}
+
+extern "C" {
+
+int iris_hip_profile_enable(int on) {
+    if (iris_hip_sync()) return -1;
+    g_prof_on = on != 0;
+    g_prof_n = g_prof_lost = 0;
+    return 0;
+}
+
+int iris_hip_profile_enabled(void) { return g_prof_on; }
+
+int iris_hip_profile_read(iris_kernel_time_t *out, int max) {
+    if (iris_hip_sync()) return -1;
+    int n = 0;
+    for (int i = 0; i < g_prof_n; i++) {
+        float ms = 0.0f;
+        if (iris_check(hipEventElapsedTime(&ms, g_pev[2 * i], g_pev[2 * i + 1]), "profile event")) return -1;
+        int j = 0;
+        while (j < n && !(out[j].grid == g_prec[i].grid && strcmp(out[j].kernel, g_prec[i].kernel) == 0)) j++;
+        if (j == n) {
+            if (n == max) continue;
+            out[n++] = {g_prec[i].kernel, g_prec[i].grid, 0, 0.0, 1e30, 0.0};
+        }
+        out[j].calls++;
+        out[j].total_ms += ms;
+        if (ms < out[j].min_ms) out[j].min_ms = ms;
+        if (ms > out[j].max_ms) out[j].max_ms = ms;
+    }
+    if (g_prof_lost) iris_set_error("profile: %d launches past the %d recorded", g_prof_lost, PROF_MAX);
+    return n;
+}
+
 int iris_hip_graph_begin(void) {
     if (!iris_hip_available()) return -1;
     return iris_check(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "begin capture");

@@ -358,10 +358,10 @@ extern "C" int iris_hip_gn_stats(const void *x, int is_bf16, int pixels, int C, 
     const int ppb = (pixels + nblk - 1) / nblk;
     const int used = (pixels + ppb - 1) / ppb;
     if (is_bf16)
-        hipLaunchKernelGGL(gn_stats_kernel<uint16_t>, dim3(used), dim3(NT), 0, iris_stream(), (const uint16_t *)x,
+        IRIS_LAUNCH(gn_stats_kernel<uint16_t>, dim3(used), dim3(NT), 0, iris_stream(), (const uint16_t *)x,
                            pixels, C, groups, ppb, part);
     else
-        hipLaunchKernelGGL(gn_stats_kernel<float>, dim3(used), dim3(NT), 0, iris_stream(), (const float *)x, pixels,
+        IRIS_LAUNCH(gn_stats_kernel<float>, dim3(used), dim3(NT), 0, iris_stream(), (const float *)x, pixels,
                            C, groups, ppb, part);
     if (iris_launch_check("gn_stats_kernel")) return -1;
     return used;
@@ -372,7 +372,7 @@ extern "C" int iris_hip_gn_finalize(const double *part, int nblk, int pixels, in
     if (!part || !gamma || !beta || !ab || nblk <= 0 || groups <= 0 || C % groups)
         return iris_set_error("gn_finalize: bad arguments");
     const double count = (double)pixels * (C / groups);
-    hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups), dim3(NT), 0, iris_stream(), part, nblk, C, groups, gamma,
+    IRIS_LAUNCH(gn_finalize_kernel, dim3(groups), dim3(NT), 0, iris_stream(), part, nblk, C, groups, gamma,
                        beta, eps, count, ab);
     return iris_launch_check("gn_finalize_kernel");
 }
@@ -384,10 +384,10 @@ extern "C" int iris_hip_gn_apply(const void *x, int is_bf16, const float *ab, in
         return iris_set_error("gn_apply: bad arguments");
     const size_t n8 = (size_t)pixels * C / 8;
     if (is_bf16)
-        hipLaunchKernelGGL(gn_apply_kernel<uint16_t>, dim3(blocks_for(n8)), dim3(NT), 0, iris_stream(),
+        IRIS_LAUNCH(gn_apply_kernel<uint16_t>, dim3(blocks_for(n8)), dim3(NT), 0, iris_stream(),
                            (const uint16_t *)x, ab, C, n8, swish, y, raw);
     else
-        hipLaunchKernelGGL(gn_apply_kernel<float>, dim3(blocks_for(n8)), dim3(NT), 0, iris_stream(), (const float *)x,
+        IRIS_LAUNCH(gn_apply_kernel<float>, dim3(blocks_for(n8)), dim3(NT), 0, iris_stream(), (const float *)x,
                            ab, C, n8, swish, y, raw);
     return iris_launch_check("gn_apply_kernel");
 }
@@ -397,7 +397,7 @@ extern "C" int iris_hip_vae_front(uint16_t *out, const float *lat, int z, int h,
     if (!out || !lat || !sc || !sh || z <= 0 || z > 32 || h <= 0 || w <= 0 || ((uintptr_t)out & 15))
         return iris_set_error("vae_front: bad arguments (z=%d, %dx%d)", z, h, w);
     const int npix = 4 * h * w;
-    hipLaunchKernelGGL(vae_front_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 0, iris_stream(), lat, z, h, w, sc, sh,
+    IRIS_LAUNCH(vae_front_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 0, iris_stream(), lat, z, h, w, sc, sh,
                        divide, pqw, pqb, out);
     return iris_launch_check("vae_front_kernel");
 }
@@ -408,7 +408,7 @@ extern "C" int iris_hip_softmax_bf16(uint16_t *p, int ld_p, int cols_pad, const 
         ld_s < cols || ld_p < cols_pad || ((uintptr_t)s & 15) || ((uintptr_t)p & 7))
         return iris_set_error("softmax_bf16: bad shape (rows %d cols %d pad %d ld %d/%d)", rows, cols, cols_pad, ld_s,
                               ld_p);
-    hipLaunchKernelGGL(softmax_bf16_kernel, dim3(rows), dim3(NT), 0, iris_stream(), s, ld_s, cols, p, ld_p, cols_pad);
+    IRIS_LAUNCH(softmax_bf16_kernel, dim3(rows), dim3(NT), 0, iris_stream(), s, ld_s, cols, p, ld_p, cols_pad);
     return iris_launch_check("softmax_bf16_kernel");
 }
 
@@ -417,7 +417,7 @@ extern "C" int iris_hip_transpose_bf16(uint16_t *dst, int ld_dst, int rows_pad, 
     if (!dst || !src || rows <= 0 || cols <= 0 || rows_pad < rows || rows_pad % 64 || ld_dst < rows_pad ||
         ld_src < cols)
         return iris_set_error("transpose_bf16: bad shape");
-    hipLaunchKernelGGL(transpose_bf16_kernel, dim3(rows_pad / 64, (cols + 63) / 64), dim3(NT), 0, iris_stream(), src,
+    IRIS_LAUNCH(transpose_bf16_kernel, dim3(rows_pad / 64, (cols + 63) / 64), dim3(NT), 0, iris_stream(), src,
                        ld_src, rows, cols, dst, ld_dst);
     return iris_launch_check("transpose_bf16_kernel");
 }
@@ -428,7 +428,7 @@ extern "C" int iris_hip_vae_conv_out(uint8_t *rgb, float *f32, const uint16_t *g
         ((uintptr_t)wt & 15))
         return iris_set_error("vae_conv_out: bad arguments");
     const int npix = H * W;
-    hipLaunchKernelGGL(conv_out_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 9 * cin * sizeof(float4), iris_stream(),
+    IRIS_LAUNCH(conv_out_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 9 * cin * sizeof(float4), iris_stream(),
                        g, H, W, cin, wt, bias, rgb, f32);
     return iris_launch_check("conv_out_kernel");
 }
@@ -436,14 +436,14 @@ extern "C" int iris_hip_vae_conv_out(uint8_t *rgb, float *f32, const uint16_t *g
 extern "C" int iris_hip_vae_img_in(uint16_t *out, const float *img, int H, int W) {
     if (!out || !img || H <= 0 || W <= 0 || ((uintptr_t)out & 15)) return iris_set_error("vae_img_in: bad arguments");
     const int npix = H * W;
-    hipLaunchKernelGGL(vae_img_in_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 0, iris_stream(), img, npix, out);
+    IRIS_LAUNCH(vae_img_in_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 0, iris_stream(), img, npix, out);
     return iris_launch_check("vae_img_in_kernel");
 }
 
 extern "C" int iris_hip_vae_enc_out(float *lat, const float *mom, int z, int h, int w, const float *qw,
                                     const float *qb, const float *sc, const float *sh) {
     if (!lat || !mom || !sc || !sh || z <= 0 || h < 2 || w < 2) return iris_set_error("vae_enc_out: bad arguments");
-    hipLaunchKernelGGL(vae_enc_out_kernel, dim3((h * w + NT - 1) / NT), dim3(NT), 0, iris_stream(), mom, z, h, w, qw,
+    IRIS_LAUNCH(vae_enc_out_kernel, dim3((h * w + NT - 1) / NT), dim3(NT), 0, iris_stream(), mom, z, h, w, qw,
                        qb, sc, sh, lat);
     return iris_launch_check("vae_enc_out_kernel");
 }

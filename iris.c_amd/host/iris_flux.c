@@ -892,7 +892,8 @@ int iris_flux_velocity(iris_transformer_t *tf, float t) {
     /* get_timestep_embedding(t * 1000), :3967 */
     iris_timestep_sincos(w->tsin_host, t * 1000.0f, 256, 10000.0f);
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
-    if (iris_hip_graph_launch(w->graph)) return -1;
+    /* profiled: the same launches one by one, each timed */
+    if (iris_hip_profile_enabled() ? enqueue_forward(tf) : iris_hip_graph_launch(w->graph)) return -1;
     /* per-block progress (iris_transformer_flux.c:4085-4086, :4185-4186,
      * :4315-4316); the blocks run inside one graph, so these fire once the
      * step has been enqueued */
@@ -1254,10 +1255,25 @@ iris_transformer_t *iris_transformer_load(FILE *f) {
     return NULL;
 }
 
-/* BLAS profile counters of the reference CPU path (:55-80); the HIP path is
- * profiled with rocprofv3 instead. */
-void iris_print_blas_profile(void) {}
-void iris_reset_blas_profile(void) {}
+/* The reference's profile counters (:55-80): its cumulative single-block
+ * breakdown becomes the per-kernel table of the library's profile (eager
+ * steps with an event pair around every launch). reset starts a profile,
+ * print writes the table to stderr and leaves the profile running. */
+void iris_reset_blas_profile(void) { iris_hip_profile_enable(1); }
+
+void iris_print_blas_profile(void) {
+    if (!iris_hip_profile_enabled()) return;
+    iris_kernel_time_t k[128];
+    const int n = iris_hip_profile_read(k, 128);
+    double total = 0.0;
+    for (int i = 0; i < n; i++) total += k[i].total_ms;
+    if (n <= 0 || total <= 0.0) return;
+    fprintf(stderr, "\nKernel breakdown (cumulative, %d kernel shapes):\n", n);
+    for (int i = 0; i < n; i++)
+        fprintf(stderr, "  %-44s grid %8lld  %5d x %8.3f ms = %8.1f ms (%4.1f%%)\n", k[i].kernel, k[i].grid, k[i].calls,
+                k[i].total_ms / k[i].calls, k[i].total_ms, 100.0 * k[i].total_ms / total);
+    fprintf(stderr, "  Total:  %8.1f ms\n", total);
+}
 
 /* ------------------------------------------------------ reference entries */
 

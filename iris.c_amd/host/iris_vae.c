@@ -533,7 +533,10 @@ static int conv(iris_vae_gpu_t *v, const uint16_t *in, const uint16_t *w, const 
 
 static int gemm(const uint16_t *A, int lda, const uint16_t *W, int ldw, void *out, int ldo, const float *bias, int M,
                 int N, int K, int epi) {
-    iris_gemm_problem_t p = {A, W, out, bias, M, N, K, lda, ldw, ldo, epi};
+    iris_gemm_problem_t p;
+    memset(&p, 0, sizeof(p));
+    p.A = A; p.W = W; p.out = out; p.vec = bias;
+    p.M = M; p.N = N; p.K = K; p.lda = lda; p.ldw = ldw; p.ldo = ldo; p.epi = epi;
     return iris_hip_gemm(&p, 1);
 }
 

@@ -582,6 +582,8 @@ int zi_velocity(zi_transformer_t *tf, float timestep) {
     if (!w->valid) return -1;
     iris_timestep_sincos(w->tsin_host, timestep * 1000.0f, 256, 10000.0f);   /* :550-556 */
     if (iris_hip_memcpy_h2d(w->tsin, w->tsin_host, 256 * 4)) return -1;
+    /* profiled: the same launches one by one, each timed */
+    if (iris_hip_profile_enabled()) return zi_enqueue(tf);
     return iris_hip_graph_launch(w->graph);
 }
 

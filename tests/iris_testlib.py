@@ -78,6 +78,12 @@ class GemmProblem(ctypes.Structure):
                 ("ldw2", ctypes.c_int)]
 
 
+class KernelTime(ctypes.Structure):
+    """iris_kernel_time_t (include/iris_hip.h)"""
+    _fields_ = [("kernel", ctypes.c_char_p), ("grid", ctypes.c_longlong), ("calls", ctypes.c_int),
+                ("total_ms", ctypes.c_double), ("min_ms", ctypes.c_double), ("max_ms", ctypes.c_double)]
+
+
 class NormArgs(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("ldx", ctypes.c_int), ("out", ctypes.c_void_p), ("ldo", ctypes.c_int),
                 ("out_bf16", ctypes.c_int), ("rows", ctypes.c_int), ("cols", ctypes.c_int), ("mode", ctypes.c_int),

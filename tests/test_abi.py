@@ -79,7 +79,8 @@ MIRRORS = [("iris_gemm_problem_t", "iris_hip.h", tl.GemmProblem),
            ("iris_norm_args_t", "iris_hip.h", tl.NormArgs),
            ("iris_qkprep_args_t", "iris_hip.h", tl.QkPrepArgs),
            ("iris_attn_args_t", "iris_hip.h", tl.AttnArgs),
-           ("iris_ref_t", "iris_transformer.h", tl.IrisRef)]
+           ("iris_ref_t", "iris_transformer.h", tl.IrisRef),
+           ("iris_kernel_time_t", "iris_hip.h", tl.KernelTime)]
 
 
 C_NAME = {"inp": "in"}      # Python keywords renamed in the mirrors
