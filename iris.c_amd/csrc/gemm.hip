@@ -42,8 +42,8 @@
 namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64, NT = 512;
-constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M, TW_N = BN / WAVES_N;
-constexpr int FM = TW_M / 16, FN = TW_N / 16;
+constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M;
+constexpr int FM = TW_M / 16;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
 constexpr int DMA_ROWS = 8;                         /* rows of one 64-lane x 16-byte LDS-DMA load */
 constexpr int DMA_PER_WAVE = BM / DMA_ROWS / 4;     /* loads per wave for one operand tile = 8 */
@@ -83,9 +83,14 @@ typedef __attribute__((address_space(3))) void lds_void;
  * 3: GEMM with a second K segment (A2, W2) after the first. The modes are
  * separate kernels: the load-issue phase has no cycles to spare for the
  * address arithmetic of the modes it does not run. */
-template <int MODE>
+template <int MODE, int BNT = BN>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3;
+    /* BNT: block tile width, 256 or (MODE 0, no SwiGLU) 224 = 2 waves x 7
+     * MFMA tiles, for launches whose 256-wide tiles leave the last wave of
+     * blocks part-empty */
+    static_assert(BNT == BN || (BNT == 224 && MODE == 0), "narrow tiles are for plain GEMMs");
+    constexpr int TWN = BNT / WAVES_N, FNT = TWN / 16, W_DMA = BNT / DMA_ROWS / 4;
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
      * the other */
@@ -121,7 +126,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int gsz = min(tmc - first_m, GROUP_M);
     const int tm = first_m + (t % (GROUP_M * tnc)) % gsz;
     const int tn = (t % (GROUP_M * tnc)) / gsz;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int m0 = tm * BM, n0 = tn * BNT;
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -136,10 +141,12 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * 8j + l/8, stored chunk l%8; the lane fetches global chunk
      * (l%8) ^ ((row >> 1) & 7), which depends on j only through its parity.
      * Group 0 loads the A tiles and group 1 the W tiles; wave gw of a group
-     * issues loads j = 8gw..8gw+7. */
+     * issues A loads j = 8gw..8gw+7 and W loads j = W_DMA gw .. + W_DMA-1
+     * (W_DMA = 7 for 224-wide tiles, where the parity of j is that of
+     * gw + i). */
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
-    const int a_rows = min(BM, pr.M - m0), w_rows = min(BN, pr.N - n0);
+    const int a_rows = min(BM, pr.M - m0), w_rows = min(BNT, pr.N - n0);
     const __amdgpu_buffer_rsrc_t a_rsrc =
         CONV ? __builtin_amdgcn_make_buffer_rsrc((void *)pr.A, (short)0, (int)P.conv_in_bytes, 0x00020000)
              : __builtin_amdgcn_make_buffer_rsrc((void *)a_base, (short)0, a_rows * pr.lda * 2, 0x00020000);
@@ -152,7 +159,9 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         const int c = dch ^ ((4 * par + (drow >> 1)) & 7);
         const int row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
         a_voff[par] = (row * pr.lda + c * 8) * 2;
-        w_voff[par] = (row * pr.ldw + c * 8) * 2;
+        /* W: load i of wave gw is tile load j = W_DMA gw + i */
+        const int cw = dch ^ ((4 * ((par + (W_DMA & 1) * gw) & 1) + (drow >> 1)) & 7);
+        w_voff[par] = ((gw * W_DMA * DMA_ROWS + drow) * pr.ldw + cw * 8) * 2;
         a_chunk[par] = c * 16;
     }
     const int a_step = DMA_ROWS * pr.lda * 2, w_step = DMA_ROWS * pr.ldw * 2;
@@ -232,24 +241,24 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                                                          16, w_voff[i & 1] + extra + i * step, ks, 0, 0);
         } else {
 #pragma unroll
-            for (int i = 0; i < DMA_PER_WAVE; i++)
+            for (int i = 0; i < W_DMA; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc,
-                                                         (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512),
+                                                         (lds_void *)(stage + TILE_ELEMS + (gw * W_DMA + i) * 512),
                                                          16, w_voff[i & 1] + i * w_step, kt * BK * 2, 0, 0);
         }
     };
 
-    f32x4 acc[FM][FN];
+    f32x4 acc[FM][FNT];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++)
+        for (int j = 0; j < FNT; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
     const int nk = (pr.K + (SEG2 ? pr.K2 : 0)) / BK;
     /* fragments of one K-step: two 32-wide slices */
-    bf16x8 a[2][FM], w[2][FN];
+    bf16x8 a[2][FM], w[2][FNT];
     auto frags = [&](const uint16_t *stage) {
         const uint16_t *As = stage;
         const uint16_t *Ws = stage + TILE_ELEMS;
@@ -259,14 +268,14 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
             for (int mi = 0; mi < FM; mi++) a[kk][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 16 + lr, ch));
 #pragma unroll
-            for (int ni = 0; ni < FN; ni++) w[kk][ni] = *(const bf16x8 *)(Ws + swz(wn * TW_N + ni * 16 + lr, ch));
+            for (int ni = 0; ni < FNT; ni++) w[kk][ni] = *(const bf16x8 *)(Ws + swz(wn * TWN + ni * 16 + lr, ch));
         }
     };
     auto mfmas = [&](int kk) {
 #pragma unroll
             for (int mi = 0; mi < FM; mi++)
 #pragma unroll
-                for (int ni = 0; ni < FN; ni++)
+                for (int ni = 0; ni < FNT; ni++)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[kk][ni], a[kk][mi], acc[mi][ni], 0, 0, 0);
     };
 /* explicit waits and barriers stay where they are written */
@@ -360,11 +369,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
     const int rowb = m0 + wm * TW_M + lr;
-    const int colb = n0 + wn * TW_N + lg * 4;
+    const int colb = n0 + wn * TWN + lg * 4;
     /* whole tile in range and 4-wide accesses aligned: one 8- or 16-byte
      * access per lane and 16x16 tile */
     const bool aligned = (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 && ((uintptr_t)vec & 15) == 0;
-    const bool full = m0 + BM <= M && n0 + BN <= N && aligned;
+    const bool full = m0 + BM <= M && n0 + BNT <= N && aligned;
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
@@ -372,7 +381,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     case IRIS_EPI_ADD: {
         const float vdef = pr.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f;
 #pragma unroll
-        for (int ni = 0; ni < FN; ni++) {
+        for (int ni = 0; ni < FNT; ni++) {
             const int col = colb + ni * 16;
             /* a lane's 4 columns are all in range or (N % 4 == 0 aside) all out */
             const bool cols4 = full || (aligned && col + 3 < N);
@@ -422,38 +431,39 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         }
         break;
     }
-    case IRIS_EPI_SWIGLU: {
-        /* each 64 columns of the wave are one interleaved group: tiles 4g,
-         * 4g+1 = 32 gate rows, tiles 4g+2, 4g+3 = the matching 32 up rows;
-         * output columns = group * 32 + h * 16 + lg * 4 + (0..3) */
+    case IRIS_EPI_SWIGLU:
+        if constexpr (BNT == BN) {
+            /* each 64 columns of the wave are one interleaved group: tiles 4g,
+             * 4g+1 = 32 gate rows, tiles 4g+2, 4g+3 = the matching 32 up rows;
+             * output columns = group * 32 + h * 16 + lg * 4 + (0..3) */
 #pragma unroll
-        for (int g = 0; g < FN / 4; g++)
+            for (int g = 0; g < FNT / 4; g++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int col = ((n0 + wn * TW_N + g * 64) >> 1) + h * 16 + lg * 4;
+                for (int h = 0; h < 2; h++) {
+                    const int col = ((n0 + wn * TWN + g * 64) >> 1) + h * 16 + lg * 4;
 #pragma unroll
-                for (int mi = 0; mi < FM; mi++) {
-                    const int row = rowb + mi * 16;
-                    const f32x4 gt = acc[mi][4 * g + h], up = acc[mi][4 * g + 2 + h];
-                    uint16_t y[4];
+                    for (int mi = 0; mi < FM; mi++) {
+                        const int row = rowb + mi * 16;
+                        const f32x4 gt = acc[mi][4 * g + h], up = acc[mi][4 * g + 2 + h];
+                        uint16_t y[4];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) y[r] = f2bf_hw(silu_fast(gt[r]) * up[r]);
-                    uint16_t *dst = (uint16_t *)pr.out + (size_t)row * ldo + col;
-                    if (full) {
-                        *(uint2 *)dst = make_uint2((uint32_t)y[0] | ((uint32_t)y[1] << 16),
-                                                   (uint32_t)y[2] | ((uint32_t)y[3] << 16));
-                    } else if (row < M) {
+                        for (int r = 0; r < 4; r++) y[r] = f2bf_hw(silu_fast(gt[r]) * up[r]);
+                        uint16_t *dst = (uint16_t *)pr.out + (size_t)row * ldo + col;
+                        if (full) {
+                            *(uint2 *)dst = make_uint2((uint32_t)y[0] | ((uint32_t)y[1] << 16),
+                                                       (uint32_t)y[2] | ((uint32_t)y[3] << 16));
+                        } else if (row < M) {
 #pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            if (col + r < (N >> 1)) dst[r] = y[r];
+                            for (int r = 0; r < 4; r++)
+                                if (col + r < (N >> 1)) dst[r] = y[r];
+                        }
                     }
                 }
-            }
+        }
         break;
-    }
     case IRIS_EPI_F32_T: {
 #pragma unroll
-        for (int ni = 0; ni < FN; ni++)
+        for (int ni = 0; ni < FNT; ni++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int col = colb + ni * 16 + r;
@@ -549,8 +559,34 @@ extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
     if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    bool seg2 = false;
-    for (int i = 0; i < n; i++) seg2 = seg2 || probs[i].K2 > 0;
+    bool seg2 = false, swiglu = false;
+    for (int i = 0; i < n; i++) {
+        seg2 = seg2 || probs[i].K2 > 0;
+        swiglu = swiglu || probs[i].epi == IRIS_EPI_SWIGLU;
+    }
+    /* 224-wide tiles when they need fewer rounds of tile-widths: with one
+     * block per CU a launch takes ceil(tiles / CUs) rounds, each as long as
+     * one tile's width */
+    const int cus = iris_cu_count();
+    if (!seg2 && !swiglu && cus > 0) {
+        int t224 = 0;
+        for (int i = 0; i < n; i++)
+            if (P.tiles_m[i]) t224 += P.tiles_m[i] * ((probs[i].N + 223) / 224);
+        const long long w256 = (long long)((total + cus - 1) / cus) * BN;
+        const long long w224 = (long long)((t224 + cus - 1) / cus) * 224;
+        if (w224 * 100 < w256 * 97) {
+            for (int i = 0, acc = 0; i < n; i++) {
+                P.tile_start[i] = acc;
+                if (P.tiles_m[i]) P.tiles_n[i] = (probs[i].N + 223) / 224;
+                acc += P.tiles_m[i] * P.tiles_n[i];
+            }
+            for (int i = n; i <= MAXP; i++) P.tile_start[i] = t224;
+            P.total = t224;
+            P.per_xcd = (t224 + 7) / 8;
+            IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+            return iris_launch_check("gemm_bf16_kernel");
+        }
+    }
     if (seg2)
         IRIS_LAUNCH(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     else

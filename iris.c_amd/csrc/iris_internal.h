@@ -4,6 +4,7 @@
 #include "../../include/iris_hip.h"
 
 hipStream_t iris_stream(void);
+int iris_cu_count(void);   /* compute units of the bound device (0 before init) */
 int iris_set_error(const char *fmt, ...);
 int iris_check(hipError_t e, const char *what);
 int iris_launch_check(const char *what);

@@ -22,8 +22,10 @@ static std::atomic<size_t> g_in_use{0};
 static hipEvent_t g_events[64];
 static int g_events_made = 0;
 static hipGraph_t g_capture_graph = nullptr;
+static int g_cus = 0;
 
 hipStream_t iris_stream(void) { return g_stream; }
+int iris_cu_count(void) { return g_cus; }
 
 int iris_set_error(const char *fmt, ...) {
     va_list ap;
@@ -58,6 +60,7 @@ int iris_hip_init(int device) {
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return iris_set_error("kernels are built for gfx950, device is %s", p.gcnArchName);
     if (iris_check(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate")) return -1;
+    g_cus = p.multiProcessorCount;
     g_device = device;
     g_init = 1;
     return 0;

@@ -161,6 +161,43 @@ def test_gemm_splitk_epilogues(lib, M, N, K, splits):
     assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) != 0
 
 
+@pytest.mark.parametrize("shapes,K", [([(4608, 3072)], 1024), ([(512, 9216), (4096, 9216)], 192),
+                                      ([(4608, 3840)], 320), ([(700, 3000)], 128)])
+def test_gemm_narrow_tiles(lib, shapes, K):
+    """Launches that take 224-wide tiles (fewer rounds of blocks than with
+    256: 216 -> 252 tiles, 648 -> 756, 270 -> 324 over 256 CUs), N not a
+    multiple of 224 (partial last tile): every non-SwiGLU epilogue against
+    the float64 product, two problems in one launch."""
+    rng = np.random.default_rng(sum(m * 3 + n for m, n in shapes) + K)
+    P = tl.GemmProblem
+    ins = []
+    for m, n in shapes:
+        A = rng.standard_normal((m, K), np.float32)
+        W = rng.standard_normal((n, K), np.float32) * 0.05
+        vec = rng.standard_normal(n).astype(np.float32)
+        x0 = rng.standard_normal((m, n), np.float32)
+        ref = bf(A).astype(np.float64) @ bf(W).astype(np.float64).T
+        ins.append((m, n, tl.Dev.of(tl.to_bf16(A)), tl.Dev.of(tl.to_bf16(W)), tl.Dev.of(vec), vec, x0, ref))
+    for epi in (EPI_F32, EPI_BF16, EPI_GATED_ADD, EPI_F32_T):
+        outs, probs = [], []
+        for m, n, dA, dW, dV, vec, x0, ref in ins:
+            o = tl.Dev.of(x0) if epi == EPI_GATED_ADD else tl.Dev(m * n * 4)
+            probs.append(P(dA.ptr, dW.ptr, o.ptr, dV.ptr, m, n, K, K, K, m if epi == EPI_F32_T else n, epi))
+            outs.append(o)
+        run_gemm(lib, probs)
+        for o, (m, n, dA, dW, dV, vec, x0, ref) in zip(outs, ins):
+            if epi == EPI_F32:
+                assert tl.rel_l2(o.get(np.float32, (m, n)), ref + vec) < 1e-5
+            elif epi == EPI_BF16:
+                got = tl.bf16_to_f32(o.get(np.uint16, (m * n,)).reshape(m, n))
+                assert tl.rel_l2(got, ref + vec) < 4e-3
+            elif epi == EPI_GATED_ADD:
+                assert tl.rel_l2(o.get(np.float32, (m, n)), x0 + vec * ref) < 1e-5
+            else:
+                assert tl.rel_l2(o.get(np.float32, (n, m)), (ref + vec).T) < 1e-5
+            o.close()
+
+
 def test_gemm_second_segment(lib):
     """out = A W^T + A2 W2^T (the low-rank adapter's concatenated K axis):
     F32 + bias, gated residual and SwiGLU epilogues over ragged tiles, A2 row
