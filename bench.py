@@ -157,6 +157,15 @@ def in_step(prof, kernel, grid):
     raise AssertionError(f"{kernel} with grid {grid} not in the profiled step")
 
 
+def in_step_attn(prof, calls):
+    """The attention launches of the profiled step (one block per unit or
+    the balanced schedule, whichever the launch took)."""
+    for r in prof:
+        if r["kernel"].startswith("flash_attn_kernel<") and r["calls"] == calls:
+            return r["total_ms"] / r["calls"], r["calls"]
+    raise AssertionError(f"no flash_attn_kernel entry with {calls} calls in the profiled step")
+
+
 def gemm_grid(shapes):
     """Workgroups of one iris_hip_gemm launch over (M, N) problems: 256x256
     tiles, rounded up to whole groups of 8 (one per XCD)."""
@@ -209,15 +218,19 @@ def run_flux(lib, c, args):
     # the joint attention as the step runs it: Q normalised and rotated in the prologue
     wq = tl.Dev.of(np.ones(128, np.float32))
     rc, rs = (lib.iris_flux_device_buffer(tf, n) for n in (b"rope_pair_cos", b"rope_pair_sin"))
+    wsb = lib.iris_hip_attention_workspace_bytes()
+    aws = tl.Dev(wsb)
+    assert lib.iris_hip_memset(aws.ptr, 0, wsb) == 0
     at = tl.AttnArgs(dbuf["qkv"], dbuf["k"], dbuf["vt"], dbuf["cat"], 3 * h, h, S_pad, h + mlp, S, S, H, B,
                      S * 3 * h, S * h, H * 128 * S_pad, S * (h + mlp), 1.0 / np.sqrt(128.0), 0, S, 0, 0, 0, 0, 0,
-                     0.0, wq.ptr, wq.ptr, S, 1e-6, rc, rs)
+                     0.0, wq.ptr, wq.ptr, S, 1e-6, rc, rs, aws.ptr, wsb)
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
     wdev.close()
     wq.close()
+    aws.close()
     g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(BS, 3 * h), (BS, 2 * mlp)]))
-    a_in, a_n = in_step(prof, "flash_attn_kernel<1>", 8 * -(-(-(-S // 256) * H * B) // 8))
-    assert g_n == c["ns"] and a_n == c["nd"] + c["ns"], (g_n, a_n)
+    a_in, a_n = in_step_attn(prof, c["nd"] + c["ns"])
+    assert g_n == c["ns"], g_n
     kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_in,
                             2.0 * BS * h * (3 * h + 2 * mlp), g_n, f"gemm_fused_{args.config}", g_ms),
                kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_in, 4.0 * B * S * S * h, a_n,
@@ -268,14 +281,18 @@ def run_zimage(lib, c, args):
     q, k, vt, o = (tl.Dev(S * d * 2), tl.Dev(S * d * 2), tl.Dev(H * 128 * S_pad * 2), tl.Dev(S * d * 2))
     for b in (q, k, vt):
         b.put(tl.to_bf16(tl.synth_f32((b.n // 2,), 11)))
+    wsb = lib.iris_hip_attention_workspace_bytes()
+    aws = tl.Dev(wsb)
+    assert lib.iris_hip_memset(aws.ptr, 0, wsb) == 0
     at = tl.AttnArgs(q.ptr, k.ptr, vt.ptr, o.ptr, d, d, S_pad, d, S, S, H, 1, 0, 0, 0, 0, 1.0 / np.sqrt(128.0),
                      0, S, 0, 0)
+    at.ws, at.ws_bytes = aws.ptr, wsb
     a_ms = time_launches(lib, lambda: lib.iris_hip_attention(ctypes.byref(at)))
-    for b in (q, k, vt, o):
+    for b in (q, k, vt, o, aws):
         b.close()
     g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(S, 2 * f)]))
-    a_in, a_n = in_step(prof, "flash_attn_kernel<1>", 8 * -(-(-(-S // 256) * H) // 8))
-    assert g_n == c["layers"] and a_n == c["layers"], (g_n, a_n)
+    a_in, a_n = in_step_attn(prof, c["layers"])
+    assert g_n == c["layers"], g_n
     kernels = [kernel_entry("gemm_bf16_kernel: FFN w1/w3 (SwiGLU epilogue)", g_in, 2.0 * S * d * 2 * f, g_n,
                             f"gemm_ffn_{args.config}", g_ms),
                kernel_entry("flash_attn_kernel: unified attention, head_dim 128", a_in, 4.0 * S * S * d, a_n,
@@ -305,7 +322,8 @@ def measured_traffic(key):
 def probe(kind, n):
     """Launch one kernel class n times on synthetic NS-shaped buffers (the
     program that the counter runs profile): `gemm` = the single-block fused
-    projection GEMM, `attn` = the joint attention, `copy` = a 1 GiB
+    projection GEMM, `attn` = the joint attention, `rownorm` = the AdaLN
+    row pass, `kvprep` = K RMSNorm + RoPE and the V transpose, `copy` = a 1 GiB
     device-to-device copy (the calibration kernel of known size)."""
     lib = tl.hip()
     c = CONFIGS["ns"]
@@ -336,10 +354,36 @@ def probe(kind, n):
         ang = np.random.default_rng(5).uniform(-3, 3, (S, 64))
         rc, rs = (tl.Dev.of(f(ang).astype(np.float32)) for f in (np.cos, np.sin))
         bufs.extend([wq, rc, rs])
+        wsb = lib.iris_hip_attention_workspace_bytes()
+        aws = dev(wsb)
+        assert lib.iris_hip_memset(aws, 0, wsb) == 0
         at = tl.AttnArgs(q, k, vt, o, 3 * h, h, S_pad, h + mlp, S, S, H, 1, 0, 0, 0, 0, 1.0 / np.sqrt(128.0), 0, S,
-                         0, 0, 0, 0, 0, 0.0, wq.ptr, wq.ptr, S, 1e-6, rc.ptr, rs.ptr)
+                         0, 0, 0, 0, 0, 0.0, wq.ptr, wq.ptr, S, 1e-6, rc.ptr, rs.ptr, aws, wsb)
         fn = lambda: lib.iris_hip_attention(ctypes.byref(at))  # noqa: E731
         alg = 2 * 4 * S * h + 2 * 64 * 4 * S
+    elif kind == "rownorm":
+        # the double block's AdaLN: LayerNorm + (1 + scale) x + shift of the f32 residual rows, bf16 out,
+        # txt rows with one modulation set, img rows with the other
+        x, a = dev(S * h * 4), dev(S * h * 2)
+        mods = [tl.Dev.of(tl.synth_f32((h,), 20 + i, 0, 0.1)) for i in range(4)]
+        bufs.extend(mods)
+        na = tl.NormArgs(x, h, a, h, 1, S, h, 0, 1e-6, c["T"], S, mods[0].ptr, mods[1].ptr, None, mods[2].ptr,
+                         mods[3].ptr, None)
+        fn = lambda: lib.iris_hip_rownorm(ctypes.byref(na))  # noqa: E731
+        alg = S * h * 4 + S * h * 2 + 4 * h * 4
+    elif kind == "kvprep":
+        # K RMSNorm + RoPE (K-side tables) and the V transpose from the fused QKV rows
+        qkv, k = dev(S * 3 * h * 2, 11), dev(S * h * 2)
+        vt = dev(H * 128 * S_pad * 2)
+        wk = tl.Dev.of(np.ones(128, np.float32))
+        ang = np.random.default_rng(5).uniform(-3, 3, (S, 128))
+        rc, rs = (tl.Dev.of(f(ang).astype(np.float32)) for f in (np.cos, np.sin))
+        bufs.extend([wk, rc, rs])
+        qa = tl.QkPrepArgs(qkv, 3 * h, h, 2 * h, None, k, vt, S_pad, S, H, None, wk.ptr, None, wk.ptr, S, rc.ptr,
+                           rs.ptr, 0, 1e-6, 0, rc.ptr, rs.ptr)
+        fn = lambda: lib.iris_hip_kv_prepare(ctypes.byref(qa))  # noqa: E731
+        # K and V columns read, K and V^T written, the K-side tables read
+        alg = 2 * S * h * 2 + 2 * S * h * 2 + 2 * S * 128 * 4
     else:
         nb = 1 << 30
         src, dst = dev(nb), dev(nb)
@@ -520,7 +564,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="ns", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--probe", choices=["gemm", "attn", "copy"],
+    ap.add_argument("--probe", choices=["gemm", "attn", "copy", "rownorm", "kvprep"],
                     help="only launch one kernel class a few times (for counter runs)")
     ap.add_argument("--probe-launches", type=int, default=3)
     args = ap.parse_args()

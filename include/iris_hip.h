@@ -267,7 +267,19 @@ typedef struct {
     int qn_split;
     float qn_eps;
     const float *rope_cos, *rope_sin;
+    /* Optional workspace (NULL: one block per 256 queries of a head). When
+     * those blocks would fill the rounds of blocks (one per compute unit)
+     * less than 80 % on average and causal is 0, the key tiles of all
+     * (query block, head) units are dealt out in equal ranges, one per
+     * compute unit, and the partial softmax states of a unit done by several
+     * blocks are merged by the last of them (deterministic order). At least
+     * iris_hip_attention_workspace_bytes(), 256-byte aligned, zeroed once
+     * before first use (calls leave it zeroed); calls sharing one workspace
+     * must not overlap. */
+    void *ws;
+    size_t ws_bytes;
 } iris_attn_args_t;
+size_t iris_hip_attention_workspace_bytes(void);
 int iris_hip_attention(const iris_attn_args_t *a);
 
 /* ---- layout and conversion ---- */

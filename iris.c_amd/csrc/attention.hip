@@ -67,6 +67,8 @@
  */
 #include "iris_internal.h"
 
+#include <string.h>
+
 namespace {
 
 constexpr int QB = 256, KB = 64, HD = 128, NT = 512, NW = NT / 64, QW = QB / NW;
@@ -79,21 +81,51 @@ constexpr int QS_OFF = 2 * KS_ELEMS + 2 * VS_ELEMS;
 constexpr size_t SMEM_FUSEQ_BYTES = SMEM_BYTES + (size_t)NW * 32 * KSTR * 2;
 static_assert(QW == 32, "one 32-query MFMA column block per wave");
 
-enum { F_FUSEQ = 1, F_CAUSAL = 2, F_BIAS = 4 };
+enum { F_FUSEQ = 1, F_CAUSAL = 2, F_BIAS = 4, F_SPLIT = 8 };
+
+/* Balanced schedule (F_SPLIT): the nkt key tiles of all units (query block,
+ * head, batch) form one range of units * nkt steps, dealt out to the blocks
+ * (one per CU) in contiguous pieces: block slot s takes per + (s < rem)
+ * steps. Slots are numbered XCD-major (slot s runs on XCD s / bpx), so one
+ * XCD's blocks work on neighbouring units, mostly of one head, and share its
+ * K and V in L2. A unit done by several blocks is finished by the last of
+ * them to arrive (cnt[unit] counts arrivals and is left at zero), which
+ * merges the partial softmax states in slot order: o and (m, l) of each
+ * block's first segment in slot 2s, of its last in slot 2s + 1. */
+struct AttnSplit {
+    int nkt, per, rem, bpx;
+    int *cnt;
+    float *ws;   /* o partials, then (m, l) pairs */
+    int slots;
+};
+constexpr int SPLIT_MAX_UNITS = 1 << 16;
+constexpr size_t SPLIT_CNT_BYTES = SPLIT_MAX_UNITS * sizeof(int);
+constexpr size_t SPLIT_SLOT_BYTES = (size_t)NT * 64 * 4 + (size_t)NT * 8;   /* o, then (m, l) per lane */
+
+__device__ __forceinline__ int split_start(const AttnSplit &sp, int s) { return s * sp.per + min(s, sp.rem); }
+__device__ __forceinline__ int split_slot_of(const AttnSplit &sp, int i) {
+    const int big = sp.rem * (sp.per + 1);
+    return i < big ? i / (sp.per + 1) : sp.rem + (i - big) / sp.per;
+}
+
+/* one segment of a unit: key tiles [t0, t0 + tn) of unit L; part != 0: a
+ * piece of a unit split over several blocks (slot owner s, first segment of
+ * that block or not) */
+struct AttnSeg {
+    int part, s, first;
+};
 
 /* s_waitcnt immediate: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8 */
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8); }
 
 template <int FEAT>
-__global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a, float scale_log2, int nqb,
-                                                        int per_xcd, int total) {
+__device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float scale_log2, int nqb, const int L,
+                                             const int t0, int tn, const AttnSplit &sp, const AttnSeg sg) {
     constexpr bool FUSEQ = FEAT & F_FUSEQ, CAUSAL = FEAT & F_CAUSAL, BIAS = FEAT & F_BIAS;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 #define KBUF(b) (smem + (b) * KS_ELEMS)
 #define VBUF(b) (smem + 2 * KS_ELEMS + (b) * VS_ELEMS)
 
-    const int L = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-    if (L >= total) return;
     const int qblk = L % nqb, hb = L / nqb;
     const int head = hb % a.heads, bz = hb / a.heads;
     const int kv_head = a.kv_group > 1 ? head / a.kv_group : head;
@@ -105,8 +137,10 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     const uint16_t *VT = a.vt + (size_t)bz * a.vt_bstride + (size_t)kv_head * HD * a.ld_vt;
     uint16_t *O = a.o + (size_t)bz * a.o_bstride + head * HD;
     const int sq = a.sq, sk = a.sk;
-    /* causal: the block's last query needs keys up to its own index */
-    const int nkt = CAUSAL ? (min(sk, min(sq, (qblk + 1) * QB)) + KB - 1) / KB : (sk + KB - 1) / KB;
+    /* the segment's key tiles, t0 .. t0 + nkt - 1 (tn < 0: all; causal: the
+     * block's last query needs keys up to its own index) */
+    const int nkt = tn >= 0 ? tn
+                            : CAUSAL ? (min(sk, min(sq, (qblk + 1) * QB)) + KB - 1) / KB : (sk + KB - 1) / KB;
     const int wave_q0 = qblk * QB + wave * QW;
     const int q_row = wave_q0 + lr;
 
@@ -118,8 +152,10 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
     {
         const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
-        uint4 r0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, 0, 0));
-        uint4 r1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, 32 * a.ld_k * 2, 0));
+        const int k0off = t0 * KB * a.ld_k * 2;
+        uint4 r0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, k0off, 0));
+        uint4 r1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off,
+                                                                                    k0off + 32 * a.ld_k * 2, 0));
         uint16_t *kd = KBUF(0) + (tid >> 4) * KSTR + (tid & 15) * 8;
         *(uint4 *)kd = r0;
         *(uint4 *)(kd + 32 * KSTR) = r1;
@@ -135,13 +171,13 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
 #pragma unroll
         for (int i = 0; i < 2; i++)
             rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  k_rsrc, kh_off, (kt * KB + 16 * i) * a.ld_k * 2, 0));
+                                                  k_rsrc, kh_off, ((t0 + kt) * KB + 16 * i) * a.ld_k * 2, 0));
     };
     auto load_v = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
             rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  v_rsrc, vh_off, (32 * i * a.ld_vt + kt * KB) * 2, 0));
+                                                  v_rsrc, vh_off, (32 * i * a.ld_vt + (t0 + kt) * KB) * 2, 0));
     };
     auto store_k = [&](int stage) {
 #pragma unroll
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     /* V phase of tile t: masks, max, lazy rescale, P = exp2(S - m) as bf16
      * B-operand fragments, row sums */
     auto v_phase = [&](int t) {
-        const int k0 = t * KB;
+        const int k0 = (t0 + t) * KB;
         const bool full = k0 + KB <= sk && ((k0 >= a.kv_lo0 && k0 + KB <= a.kv_hi0) ||
                                             (k0 >= a.kv_lo1 && k0 + KB <= a.kv_hi1)) &&
                           !(CAUSAL && k0 + KB - 1 > wave_q0);
@@ -378,6 +414,60 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
     bar();
     if (!grp) bar();
 
+    if ((FEAT & F_SPLIT) && sg.part) {
+        /* a piece of the unit: store o, m, l at system coherence (written
+         * through the XCDs' L2 caches, no cache-wide flush), count the
+         * arrival; the last block to arrive merges the pieces in slot order */
+        __shared__ int arrived;
+        const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)sp.ws, (short)0, (int)(sp.slots * SPLIT_SLOT_BYTES), 0x00020000);
+        constexpr int COHERENT = 1 | 16;   /* sc0 | sc1 */
+        const int o_end = sp.slots * NT * 64 * 4;
+        auto o_off = [&](int slot, int i) { return ((slot * 16 + i) * NT + tid) * 16; };
+        auto ml_off = [&](int slot) { return o_end + (slot * NT + tid) * 8; };
+        const int slot = 2 * sg.s + (sg.first ? 0 : 1);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const f32x4 v = {o[i >> 2][(i & 3) * 4], o[i >> 2][(i & 3) * 4 + 1], o[i >> 2][(i & 3) * 4 + 2],
+                             o[i >> 2][(i & 3) * 4 + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), wr, o_off(slot, i), 0, COHERENT);
+        }
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), wr, ml_off(slot), 0,
+                                              COHERENT);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));   /* written through before the arrival is counted */
+        __syncthreads();
+        if (tid == 0) arrived = __hip_atomic_fetch_add(sp.cnt + L, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __syncthreads();
+        const int j0 = split_slot_of(sp, L * sp.nkt), j1 = split_slot_of(sp, (L + 1) * sp.nkt - 1);
+        if (arrived != j1 - j0) return;
+        /* merged state: m = max m_j, o = sum o_j 2^(m_j - m), l likewise */
+        float m_all = -INFINITY;
+        for (int j = j0; j <= j1; j++) {
+            const int sj = 2 * j + (split_start(sp, j) / sp.nkt == L ? 0 : 1);
+            const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off(sj), 0, COHERENT));
+            m_all = fmaxf(m_all, ml.x);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) o[i][r] = 0.0f;
+        l_run = 0.0f;
+        for (int j = j0; j <= j1; j++) {
+            const int sj = 2 * j + (split_start(sp, j) / sp.nkt == L ? 0 : 1);
+            const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(wr, ml_off(sj), 0, COHERENT));
+            const float f = __builtin_amdgcn_exp2f(ml.x - m_all);
+            l_run += ml.y * f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, o_off(sj, i), 0,
+                                                                                                 COHERENT));
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[i >> 2][(i & 3) * 4 + e] += v[e] * f;
+            }
+        }
+        if (tid == 0) __hip_atomic_store(sp.cnt + L, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+
     /* normalise and store O[q][d]: lane holds query lr, d = dsub*32 + (r>>2)*8 + lg*4 + (r&3) */
     const float l = l_run + __shfl_xor(l_run, 32, 64);
     if (q_row < sq) {
@@ -398,7 +488,25 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
 }
 
 template <int FEAT>
-int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, int total) {
+__global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a, float scale_log2, int nqb,
+                                                        int per_xcd, int total, const AttnSplit sp) {
+    if constexpr (!(FEAT & F_SPLIT)) {
+        const int L = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+        if (L >= total) return;
+        attn_segment<FEAT>(a, scale_log2, nqb, L, 0, -1, sp, AttnSeg{0, 0, 0});
+    } else {
+        const int s = (blockIdx.x & 7) * sp.bpx + (blockIdx.x >> 3), end = split_start(sp, s + 1);
+        for (int it = split_start(sp, s), first = 1; it < end; first = 0) {
+            const int unit = it / sp.nkt, t0 = it - unit * sp.nkt, tn = min(sp.nkt - t0, end - it);
+            if (!first) __syncthreads();   /* the previous segment's LDS reads are done */
+            attn_segment<FEAT>(a, scale_log2, nqb, unit, t0, tn, sp, AttnSeg{tn != sp.nkt, s, first});
+            it += tn;
+        }
+    }
+}
+
+template <int FEAT>
+int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, int total, const AttnSplit &sp) {
     constexpr size_t smem = (FEAT & F_FUSEQ) ? SMEM_FUSEQ_BYTES : SMEM_BYTES;
     static bool attr_set = false;
     if (!attr_set) {
@@ -408,12 +516,15 @@ int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, in
             return -1;
         attr_set = true;
     }
-    static const char *const name[8] = {"flash_attn_kernel<0>", "flash_attn_kernel<1>", "flash_attn_kernel<2>",
-                                        "flash_attn_kernel<3>", "flash_attn_kernel<4>", "flash_attn_kernel<5>",
-                                        "flash_attn_kernel<6>", "flash_attn_kernel<7>"};
-    const int prof = iris_prof_begin(name[FEAT & 7], 8LL * per_xcd);
-    hipLaunchKernelGGL(flash_attn_kernel<FEAT>, dim3(8 * per_xcd), dim3(NT), smem, iris_stream(), *a, scale_log2, nqb,
-                       per_xcd, total);
+    static const char *const name[16] = {
+        "flash_attn_kernel<0>",  "flash_attn_kernel<1>",  "flash_attn_kernel<2>",  "flash_attn_kernel<3>",
+        "flash_attn_kernel<4>",  "flash_attn_kernel<5>",  "flash_attn_kernel<6>",  "flash_attn_kernel<7>",
+        "flash_attn_kernel<8>",  "flash_attn_kernel<9>",  "flash_attn_kernel<10>", "flash_attn_kernel<11>",
+        "flash_attn_kernel<12>", "flash_attn_kernel<13>", "flash_attn_kernel<14>", "flash_attn_kernel<15>"};
+    const unsigned grid = (FEAT & F_SPLIT) ? 8u * sp.bpx : 8u * per_xcd;
+    const int prof = iris_prof_begin(name[FEAT & 15], grid);
+    hipLaunchKernelGGL(flash_attn_kernel<FEAT>, dim3(grid), dim3(NT), smem, iris_stream(), *a, scale_log2, nqb, per_xcd,
+                       total, sp);
     iris_prof_end(prof);
     return iris_launch_check("flash_attn_kernel");
 }
@@ -439,14 +550,48 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
     if (total > (1LL << 28)) return iris_set_error("attention: grid too large");
     const int per_xcd = (int)((total + 7) / 8);
     const float scale_log2 = a->scale * 1.4426950408889634f;
-    const int feat = (fuseq ? F_FUSEQ : 0) | (a->causal ? F_CAUSAL : 0) | (a->key_bias != 0.0f ? F_BIAS : 0);
+    int feat = (fuseq ? F_FUSEQ : 0) | (a->causal ? F_CAUSAL : 0) | (a->key_bias != 0.0f ? F_BIAS : 0);
+    /* balanced schedule when one block per unit leaves the rounds of blocks
+     * (one per CU) less than 80 % full on average and a workspace is given.
+     * Above that the part-empty last round costs little: the chip is at its
+     * power limit and fewer busy CUs run at a higher clock (432 units on 256
+     * CUs time the same either way; 540 units run 17 % faster balanced). */
+    AttnSplit sp;
+    memset(&sp, 0, sizeof(sp));
+    const int cus = iris_cu_count(), nkt = (a->sk + KB - 1) / KB;
+    if (!a->causal && a->ws && cus > 0 && cus % 8 == 0 && total <= SPLIT_MAX_UNITS &&
+        a->ws_bytes >= iris_hip_attention_workspace_bytes()) {
+        const long long rounds = (total + cus - 1) / cus;
+        const long long steps = total * (long long)nkt;
+        if ((double)total < 0.8 * (double)(rounds * cus) && steps / cus >= 8 && steps < (1LL << 31)) {
+            if (((uintptr_t)a->ws & 255)) return iris_set_error("attention: workspace must be 256-byte aligned");
+            sp.nkt = nkt;
+            sp.per = (int)(steps / cus);
+            sp.rem = (int)(steps % cus);
+            sp.bpx = cus / 8;
+            sp.cnt = (int *)a->ws;
+            sp.ws = (float *)((char *)a->ws + SPLIT_CNT_BYTES);
+            sp.slots = 2 * cus;
+            feat |= F_SPLIT;
+        }
+    }
     switch (feat) {
-    case 0: return launch<0>(a, scale_log2, nqb, per_xcd, (int)total);
-    case F_FUSEQ: return launch<F_FUSEQ>(a, scale_log2, nqb, per_xcd, (int)total);
-    case F_CAUSAL: return launch<F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total);
-    case F_FUSEQ | F_CAUSAL: return launch<F_FUSEQ | F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total);
-    case F_BIAS: return launch<F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total);
-    case F_FUSEQ | F_BIAS: return launch<F_FUSEQ | F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total);
+    case 0: return launch<0>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_FUSEQ: return launch<F_FUSEQ>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_CAUSAL: return launch<F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_FUSEQ | F_CAUSAL: return launch<F_FUSEQ | F_CAUSAL>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_BIAS: return launch<F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_FUSEQ | F_BIAS: return launch<F_FUSEQ | F_BIAS>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_SPLIT: return launch<F_SPLIT>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_FUSEQ | F_SPLIT: return launch<F_FUSEQ | F_SPLIT>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_BIAS | F_SPLIT: return launch<F_BIAS | F_SPLIT>(a, scale_log2, nqb, per_xcd, (int)total, sp);
+    case F_FUSEQ | F_BIAS | F_SPLIT:
+        return launch<F_FUSEQ | F_BIAS | F_SPLIT>(a, scale_log2, nqb, per_xcd, (int)total, sp);
     default: return iris_set_error("attention: causal masking with a key bias is not supported");
     }
+}
+
+extern "C" size_t iris_hip_attention_workspace_bytes(void) {
+    if (!iris_hip_available()) return 0;
+    return SPLIT_CNT_BYTES + 2 * (size_t)iris_cu_count() * SPLIT_SLOT_BYTES;
 }

@@ -100,6 +100,8 @@ typedef struct {
     float *mod;              /* dimg 6h | dtxt 6h | single 3h | final 2h */
     float *tsin_host;        /* host copy of the timestep sinusoid (small uploads are staged out of
                               * it into pinned slots before iris_hip_memcpy_h2d returns) */
+    void *attn_ws;           /* the attention's balanced-schedule workspace (zeroed) */
+    size_t attn_ws_bytes;
     void *graph;
 } work_t;
 
@@ -446,7 +448,7 @@ static void work_free(work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
                     w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp,
-                    w->temb, w->mod};
+                    w->temb, w->mod, w->attn_ws};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -568,6 +570,9 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
     DA(w->tmp, (size_t)h * 4);
     DA(w->temb, (size_t)h * 4);
     DA(w->mod, (size_t)17 * h * 4);
+    w->attn_ws_bytes = iris_hip_attention_workspace_bytes();
+    DA(w->attn_ws, w->attn_ws_bytes);
+    if (iris_hip_memset(w->attn_ws, 0, w->attn_ws_bytes) || iris_hip_sync()) goto fail;
 #undef DA
     w->tsin_host = (float *)malloc(256 * sizeof(float));
     if (!w->tsin_host) goto fail;
@@ -659,6 +664,7 @@ static int attention(iris_transformer_t *tf, const float *wqA, const float *wqB,
     a.kv_lo0 = 0; a.kv_hi0 = w->S;
     a.qn_wA = wqA; a.qn_wB = wqB; a.qn_split = split; a.qn_eps = 1e-6f;
     a.rope_cos = w->rp_cos; a.rope_sin = w->rp_sin;
+    a.ws = w->attn_ws; a.ws_bytes = w->attn_ws_bytes;
     /* SREF strength (sref_set_strength_bias, iris_transformer_flux.c:1328-1338):
      * log gamma on the logits of the reference keys, the trailing I - I0 tokens */
     if (w->n_refs > 0 && tf->sref_strength != 1.0f) {

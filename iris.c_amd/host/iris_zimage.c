@@ -45,6 +45,8 @@ typedef struct {
     float *rp_cos, *rp_sin;       /* [U][64]: one value per rotation pair (the attention's Q prologue) */
     uint16_t *a, *qkv, *q, *k, *vt, *attn, *ffn, *patches;
     float *tsin_host;
+    void *attn_ws;                /* the attention's balanced-schedule workspace (zeroed) */
+    size_t attn_ws_bytes;
     void *graph;
 } zi_work_t;
 
@@ -340,7 +342,7 @@ zi_transformer_t *zi_transformer_create_synthetic(int dim, int n_heads, int n_la
 static void zwork_free(zi_work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *p[] = {w->x, w->y, w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->tsin, w->tmp, w->temb, w->mods, w->fscale, w->lat, w->vel,
-                 w->capf, w->fout, w->a, w->qkv, w->q, w->k, w->vt, w->attn, w->ffn, w->patches};
+                 w->capf, w->fout, w->a, w->qkv, w->q, w->k, w->vt, w->attn, w->ffn, w->patches, w->attn_ws};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -390,6 +392,9 @@ int zi_prepare(zi_transformer_t *tf, int lh, int lw, int cap_len) {
     DA(w->attn, U * d * 2);
     DA(w->ffn, U * tf->ffn * 2);
     DA(w->patches, (size_t)w->I * pf * 2);
+    w->attn_ws_bytes = iris_hip_attention_workspace_bytes();
+    DA(w->attn_ws, w->attn_ws_bytes);
+    if (iris_hip_memset(w->attn_ws, 0, w->attn_ws_bytes) || iris_hip_sync()) goto fail;
 #undef DA
     w->tsin_host = (float *)malloc(256 * sizeof(float));
     if (!w->tsin_host) goto fail;
@@ -481,6 +486,7 @@ static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const
     at.kv_lo0 = klo0; at.kv_hi0 = khi0; at.kv_lo1 = klo1; at.kv_hi1 = khi1;
     at.qn_wA = b->nq; at.qn_wB = b->nq; at.qn_split = n; at.qn_eps = ZI_EPS;
     at.rope_cos = w->rp_cos + (size_t)r0 * 64; at.rope_sin = w->rp_sin + (size_t)r0 * 64;
+    at.ws = w->attn_ws; at.ws_bytes = w->attn_ws_bytes;
     CK(iris_hip_attention(&at));
     p = zprob(w->attn, d, b->o, w->y, d, NULL, n, d, d, IRIS_EPI_F32);
     CK(iris_hip_gemm(&p, 1));

@@ -112,7 +112,8 @@ class AttnArgs(ctypes.Structure):
                 ("kv_lo1", ctypes.c_int), ("kv_hi1", ctypes.c_int), ("causal", ctypes.c_int),
                 ("kv_group", ctypes.c_int), ("bias_from", ctypes.c_int), ("key_bias", ctypes.c_float),
                 ("qn_wA", ctypes.c_void_p), ("qn_wB", ctypes.c_void_p), ("qn_split", ctypes.c_int),
-                ("qn_eps", ctypes.c_float), ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p)]
+                ("qn_eps", ctypes.c_float), ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
+                ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
 
 
 class Conv3x3(ctypes.Structure):
@@ -150,6 +151,7 @@ def hip():
         lib.iris_hip_last_error.restype = ctypes.c_char_p
         lib.iris_hip_device_name.restype = ctypes.c_char_p
         lib.iris_hip_event_elapsed_ms.restype = ctypes.c_float
+        lib.iris_hip_attention_workspace_bytes.restype = ctypes.c_size_t
         lib.iris_hip_gemv.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_hip_euler.argtypes = [vp, vp, vp, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_size_t]
         lib.iris_hip_nchw_to_tokens.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int]

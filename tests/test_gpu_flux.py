@@ -286,7 +286,12 @@ def test_9b_cfg_step_reduced_depth(lib, orc):
     passes (unequal lengths), against v_u + g (v_c - v_u) from the HIP
     build's own single passes (< 1e-5), and the stepped latent against the
     oracle's (cosine > 0.999). The guided difference amplifies the bf16 error
-    of v_c - v_u by g, so the step itself is not held to the per-velocity bar."""
+    of v_c - v_u by g, so the step itself is not held to the per-velocity bar.
+    The batch-2 pass has twice the attention units of a single pass, so it
+    may take the other attention schedule (balanced key ranges, pieces merged
+    in another order): it matches the single passes to bf16 rounding (< 1e-2)
+    rather than bit for bit; the sequential passes keep the single passes'
+    schedule and match them to < 1e-5."""
     seed = 109
     tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(4096, 32, 1, 1, 12288, 128, 3.0, 2000.0, seed))
     m = ctypes.c_void_p(orc.orc_flux_create_synth(4096, 32, 1, 1, 12288, 128, 3.0, 2000.0, seed))
@@ -308,7 +313,7 @@ def test_9b_cfg_step_reduced_depth(lib, orc):
                                                   T, g, tl.fptr(sched), 1, None), n)
         own = lat.ravel() + (t1 - t0) * (v[u][0] + g * (v["c"][0] - v[u][0]))
         oracle = lat.ravel() + (t1 - t0) * (v[u][1] + g * (v["c"][1] - v[u][1]))
-        assert tl.rel_l2(got, own) < 1e-5, u
+        assert tl.rel_l2(got, own) < (1e-2 if u == "u" else 1e-5), u
         assert tl.cosine(got, oracle) > 0.999, u
     lib.iris_transformer_free(tf)
     orc.orc_flux_free(m)
@@ -331,7 +336,11 @@ def test_4b_large_geometry_properties(lib):
     512 text, S = 16896): sizes where the oracle would take minutes, checked
     through properties that hold at any size: finite, deterministic (two
     forwards bit-identical), and the batch-2 CFG pass with equal texts equal
-    to z + dt * v of the single pass (rows of the two batch slots never mix)."""
+    to z + dt * v of the single pass (rows of the two batch slots never mix).
+    The batch-2 attention has twice the (query block, head) units, so it may
+    take the other schedule (key ranges balanced over the CUs, pieces merged
+    in another order): equal to bf16 rounding (< 2e-3; rows of the other slot
+    mixed in would move it by O(1))."""
     tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 1, 7680, 128, 3.0, 2000.0, 123))
     assert tf.value, lib.iris_hip_last_error()
     lat, txt = tl.synth_f32((128, 128, 128), 92), tl.synth_f32((512, 7680), 93)
@@ -347,7 +356,7 @@ def test_4b_large_geometry_properties(lib):
                                             512, 2.5, tl.fptr(sched), 1, None), n)
     lib.iris_transformer_free(tf)
     want = lat.ravel() + np.float32(0.35 - 0.6) * a
-    assert tl.rel_l2(z, want) < 1e-6
+    assert tl.rel_l2(z, want) < 2e-3
 
 
 def sref_ktables_numpy(c, s, ref_start, shf, slf):

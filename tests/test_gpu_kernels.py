@@ -338,6 +338,69 @@ def test_flash_attention(lib, S, H, batch, mask, qscale, kramp):
             assert tl.rel_l2(got[b, :, sl], ref) < 1e-2, (b, h)
 
 
+@pytest.mark.parametrize("S,H,fused,bias", [(4608, 30, True, False), (4608, 31, False, False), (2000, 24, True, True),
+                                            (2304, 60, False, False)])
+def test_flash_attention_balanced_split(lib, S, H, fused, bias):
+    """The balanced schedule (key tiles of all units dealt out in equal
+    ranges, one per CU; pieces of a unit merged by the last block to arrive)
+    at unit counts that leave the rounds part-full (540 = Z-Image's joint
+    attention, 558, 192 with a key bias, 540 with 60 heads): against the float64 reference
+    (1.5e-2, as the one-block-per-unit kernel) and against that kernel's
+    output (the same bf16 rounding up to the merge), bit-identical over
+    repeated launches, and the workspace left zeroed."""
+    rng = np.random.default_rng(S + H)
+    h = H * 128
+    S_pad = (S + 63) // 64 * 64
+    q = rng.standard_normal((S, h)).astype(np.float32)
+    k = rng.standard_normal((S, h)).astype(np.float32)
+    v = rng.standard_normal((S, h)).astype(np.float32)
+    vt = np.zeros((H, 128, S_pad), np.float32)
+    for hh in range(H):
+        vt[hh, :, :S] = v[:, hh * 128:(hh + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(q)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    wsb = lib.iris_hip_attention_workspace_bytes()
+    ws = tl.Dev(wsb)
+    assert lib.iris_hip_memset(ws.ptr, 0, wsb) == 0
+    scale = 1.0 / np.sqrt(128.0)
+    wq = tl.Dev.of(np.ones(128, np.float32)) if fused else None
+    bias_from, key_bias = (S - 300, 0.7) if bias else (0, 0.0)
+
+    def run(use_ws):
+        o = tl.Dev(S * h * 2)
+        a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, o.ptr, h, h, S_pad, h, S, S, H, 1, 0, 0, 0, 0, scale, 0, S, 0, 0, 0,
+                        0, bias_from, key_bias, wq.ptr if fused else None, wq.ptr if fused else None, S, 1e-6,
+                        None, None, ws.ptr if use_ws else None, wsb if use_ws else 0)
+        assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+        got = o.get(np.uint16, (S, h))
+        o.close()
+        return got
+
+    plain = tl.bf16_to_f32(run(False))
+    first = run(True)
+    for _ in range(2):
+        assert np.array_equal(run(True), first)
+    got = tl.bf16_to_f32(first)
+    assert not np.any(ws.get(np.int32, (65536,))), "arrival counters not reset"
+    qq = bf(q)
+    if fused:   # RMS norm with unit weights, no rotation
+        qq = bf((qq.reshape(S, H, 128) / np.sqrt((qq.reshape(S, H, 128) ** 2).mean(-1, keepdims=True) + 1e-6))
+                .reshape(S, h))
+    heads = [0, H // 2, H - 1]
+    for hh in heads:
+        sl = slice(hh * 128, (hh + 1) * 128)
+        sc = qq[:, sl].astype(np.float64) @ bf(k)[:, sl].astype(np.float64).T * scale
+        if bias:
+            sc[:, bias_from:] += key_bias
+        sc -= sc.max(1, keepdims=True)
+        p = np.exp(sc)
+        p /= p.sum(1, keepdims=True)
+        ref = p @ bf(v)[:, sl].astype(np.float64)
+        assert tl.rel_l2(got[:, sl], ref) < 1.5e-2, hh
+    assert tl.rel_l2(got, plain) < 1e-2
+    print(f"split vs one block per unit: rel_l2 {tl.rel_l2(got, plain):.3e}")
+
+
 @pytest.mark.parametrize("S,H,group,n_real", [(300, 4, 2, 250), (512, 8, 4, 512), (70, 2, 1, 70), (1, 4, 4, 1)])
 def test_flash_attention_causal_gqa(lib, S, H, group, n_real):
     """Causal mask (key j hidden from query i < j) with a padding key range
