@@ -149,17 +149,6 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
     const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)VT, (short)0, (int)((size_t)HD * a.ld_vt * 2), 0x00020000);
 
-    /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
-    {
-        const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
-        const int k0off = t0 * KB * a.ld_k * 2;
-        uint4 r0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, k0off, 0));
-        uint4 r1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off,
-                                                                                    k0off + 32 * a.ld_k * 2, 0));
-        uint16_t *kd = KBUF(0) + (tid >> 4) * KSTR + (tid & 15) * 8;
-        *(uint4 *)kd = r0;
-        *(uint4 *)(kd + 32 * KSTR) = r1;
-    }
     /* this group's half of a tile: K rows 32 grp + gt/16 (+ 16), chunk gt % 16;
      * V^T d rows 64 grp + gt/8 (+ 32), chunk gt % 8 */
     const int kh_off = ((32 * grp + (gt >> 4)) * a.ld_k + (gt & 15) * 8) * 2;
@@ -191,20 +180,35 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
             *(uint2 *)(d + 4) = make_uint2(rv[i].z, rv[i].w);
         }
     };
-    if (nkt > 1) load_k(1);
-    load_v(0);
-
-    /* Q fragments (B operand): lane holds query lr of the wave's 32, d = ds*16 + lg*8 .. +7 */
+    /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
+    uint4 k0r[2];
+    {
+        const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
+        const int k0off = t0 * KB * a.ld_k * 2;
+        k0r[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, k0off, 0));
+        k0r[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off,
+                                                                                  k0off + 32 * a.ld_k * 2, 0));
+    }
+    /* Q loads next, so that their latency and K(0)'s overlap: the fragments
+     * (B operand: lane holds query lr of the wave's 32, d = ds*16 + lg*8 ..
+     * +7), or for the prologue the wave's 32 raw rows row by row, 16 lanes
+     * per row and 8 dims per lane, and their pair tables (coalesced) */
     bf16x8 qf[8];
-    /* Q prologue: the wave's 32 rows row by row, 16 lanes per row and 8 dims
-     * per lane (coalesced reads of the projection and of the pair tables; the
-     * arithmetic of the K pass), staged in LDS as [32][KSTR] and read back in
-     * the B-operand layout. All loads are issued before any arithmetic. */
-    auto q_prologue = [&]() {
-        uint16_t *qs = smem + QS_OFF + wave * 32 * KSTR;
-        const int rl = lane >> 4, hl = lane & 15, d0 = hl * 8;
-        u16x8 raw[8];
-        float4 c4[8], s4[8];
+    u16x8 raw[8];
+    float4 c4[8], s4[8], wa0, wa1, wb0, wb1;
+    const int rl = lane >> 4, hl = lane & 15, d0 = hl * 8;
+    if (!FUSEQ) {
+#pragma unroll
+        for (int ds = 0; ds < 8; ds++) {
+            u16x8 r = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (q_row < sq) r = *(const u16x8 *)(Q + (size_t)q_row * a.ld_q + ds * 16 + lg * 8);
+            qf[ds] = __builtin_bit_cast(bf16x8, r);
+        }
+    } else {
+        wa0 = *(const float4 *)(a.qn_wA + d0);
+        wa1 = *(const float4 *)(a.qn_wA + d0 + 4);
+        wb0 = *(const float4 *)(a.qn_wB + d0);
+        wb1 = *(const float4 *)(a.qn_wB + d0 + 4);
 #pragma unroll
         for (int pass = 0; pass < 8; pass++) {
             const int row = wave_q0 + pass * 4 + rl;
@@ -218,16 +222,29 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
                 s4[pass] = *(const float4 *)(a.rope_sin + tr);
             }
         }
-        const float4 wa0 = *(const float4 *)(a.qn_wA + d0), wa1 = *(const float4 *)(a.qn_wA + d0 + 4);
-        const float4 wb0 = *(const float4 *)(a.qn_wB + d0), wb1 = *(const float4 *)(a.qn_wB + d0 + 4);
+    }
+    /* K(1) and V(0) in flight during the Q arithmetic (unconditional, the
+     * index clamped: no branch for the wait counters to merge) */
+    load_k(min(1, nkt - 1));
+    load_v(0);
+    {
+        uint16_t *kd = KBUF(0) + (tid >> 4) * KSTR + (tid & 15) * 8;
+        *(uint4 *)kd = k0r[0];
+        *(uint4 *)(kd + 32 * KSTR) = k0r[1];
+    }
+
+    /* Q prologue: the raw rows loaded above, with the arithmetic of the K
+     * pass (16-lane row sums by DPP), staged in LDS as [32][KSTR] and read
+     * back in the B-operand layout */
+    auto q_prologue = [&]() {
+        uint16_t *qs = smem + QS_OFF + wave * 32 * KSTR;
 #pragma unroll
         for (int pass = 0; pass < 8; pass++) {
             const int rw = pass * 4 + rl, row = wave_q0 + rw;
             float x[8], ss = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[pass][j]); ss += x[j] * x[j]; }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+            ss = row16_sum(ss);
             const float inv = 1.0f / sqrtf(ss / 128.0f + a.qn_eps);
             const bool sa = row < a.qn_split;
             const float ww[8] = {sa ? wa0.x : wb0.x, sa ? wa0.y : wb0.y, sa ? wa0.z : wb0.z, sa ? wa0.w : wb0.w,
@@ -247,16 +264,7 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
 #pragma unroll
         for (int ds = 0; ds < 8; ds++) qf[ds] = *(const bf16x8 *)(qs + lr * KSTR + (ds * 2 + lg) * 8);
     };
-    if (!FUSEQ) {
-#pragma unroll
-        for (int ds = 0; ds < 8; ds++) {
-            u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (q_row < sq) raw = *(const u16x8 *)(Q + (size_t)q_row * a.ld_q + ds * 16 + lg * 8);
-            qf[ds] = __builtin_bit_cast(bf16x8, raw);
-        }
-    } else {
-        q_prologue();
-    }
+    if (FUSEQ) q_prologue();
 
     f32x16 o[4];
 #pragma unroll
@@ -392,7 +400,7 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
     if (grp) bar();
     if (nkt > 1) store_k(1);
     store_v(0);
-    if (nkt > 2) load_k(2);
+    load_k(min(2, nkt - 1));
     if (nkt > 1) load_v(1);
     qk(0);
     bar();

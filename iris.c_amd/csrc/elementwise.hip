@@ -200,8 +200,7 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
             float ss = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) { x[j] = bf2f(raw[j]); ss += x[j] * x[j]; }
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);
+            ss = row16_sum(ss);
             const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
             u16x8 out;
 #pragma unroll

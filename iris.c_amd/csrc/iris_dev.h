@@ -36,6 +36,19 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+/* Sum over each 16-lane row of the wave; every lane gets its row's total.
+ * DPP moves (no LDS round trip) whose pairings give the same sums, bit for
+ * bit, as the xor butterfly 1, 2, 4, 8: after the two quad steps a quad holds
+ * one value, so mirroring within 8 and then within 16 lanes adds the same
+ * partner values as xor 4 and xor 8. */
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));  /* quad_perm 1,0,3,2 */
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));  /* quad_perm 2,3,0,1 */
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)); /* row_half_mirror */
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); /* row_mirror */
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
