@@ -57,9 +57,12 @@
  * LDS rows are padded instead of swizzled, so every fragment address is one
  * base register plus an immediate offset: K rows hold 128 + 8 elements (272 B:
  * 16 consecutive rows start 4 banks apart, conflict-free 16-byte reads), V^T
- * rows 64 + 4 (136 B: 32 consecutive rows start 2 banks apart, conflict-free
- * 8-byte reads). Global loads go through buffer descriptors; K's range ends at
- * its last valid row so rows past the end read as zero.
+ * rows 64 + 8 (144 B: 16 consecutive rows start at 16 distinct 4-bank
+ * groups). Within each 16 keys a V^T row is stored in the order the P
+ * fragments take them (keys 0-3, 8-11, 4-7, 12-15), so a lane's 8 keys of one
+ * PV product are one 16-byte read. Global loads go through buffer
+ * descriptors; K's range ends at its last valid row so rows past the end read
+ * as zero.
  *
  * Blocks are ordered head-major and mapped XCD-major (block b runs on XCD
  * b % 8 and takes a contiguous range of the work list), so the query blocks
@@ -73,7 +76,7 @@ namespace {
 
 constexpr int QB = 256, KB = 64, HD = 128, NT = 512, NW = NT / 64, QW = QB / NW;
 constexpr float RESCALE_LOG2 = 8.0f;
-constexpr int KSTR = HD + 8, VSTR = KB + 4;
+constexpr int KSTR = HD + 8, VSTR = KB + 8;
 constexpr int KS_ELEMS = KB * KSTR, VS_ELEMS = HD * VSTR;
 constexpr size_t SMEM_BYTES = (size_t)(2 * KS_ELEMS + 2 * VS_ELEMS) * 2;
 /* with the Q prologue: each wave's 32 normalised, rotated rows after the stages */
@@ -144,6 +147,8 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
     const int wave_q0 = qblk * QB + wave * QW;
     const int q_row = wave_q0 + lr;
 
+    /* Every tile offset goes into the VGPR offset, which the buffer range check
+     * covers (the SGPR offset is not checked): K rows past sk - 1 read as zero. */
     const __amdgpu_buffer_rsrc_t k_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)K, (short)0, (int)(((size_t)(sk - 1) * a.ld_k + HD) * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t v_rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -154,19 +159,23 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
     const int kh_off = ((32 * grp + (gt >> 4)) * a.ld_k + (gt & 15) * 8) * 2;
     const int vh_off = ((64 * grp + (gt >> 3)) * a.ld_vt + (gt & 7) * 8) * 2;
     uint16_t *const kh_dst = smem + (32 * grp + (gt >> 4)) * KSTR + (gt & 15) * 8;
-    uint16_t *const vh_dst = smem + 2 * KS_ELEMS + (64 * grp + (gt >> 3)) * VSTR + (gt & 7) * 8;
+    /* V^T chunk c = gt % 8 holds keys 8c .. 8c + 7 of the tile: key block c / 2,
+     * half c % 2; its first 4 keys go to 4 (c % 2), its last 4 to 8 + 4 (c % 2)
+     * of the block */
+    uint16_t *const vh_dst =
+        smem + 2 * KS_ELEMS + (64 * grp + (gt >> 3)) * VSTR + 16 * ((gt & 7) >> 1) + 4 * (gt & 1);
     uint4 rk[2], rv[2];
     auto load_k = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
             rk[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  k_rsrc, kh_off, ((t0 + kt) * KB + 16 * i) * a.ld_k * 2, 0));
+                                                  k_rsrc, kh_off + ((t0 + kt) * KB + 16 * i) * a.ld_k * 2, 0, 0));
     };
     auto load_v = [&](int kt) {
 #pragma unroll
         for (int i = 0; i < 2; i++)
             rv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  v_rsrc, vh_off, (32 * i * a.ld_vt + (t0 + kt) * KB) * 2, 0));
+                                                  v_rsrc, vh_off + (32 * i * a.ld_vt + (t0 + kt) * KB) * 2, 0, 0));
     };
     auto store_k = [&](int stage) {
 #pragma unroll
@@ -177,17 +186,16 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
         for (int i = 0; i < 2; i++) {
             uint16_t *d = vh_dst + stage * VS_ELEMS + 32 * i * VSTR;
             *(uint2 *)d = make_uint2(rv[i].x, rv[i].y);
-            *(uint2 *)(d + 4) = make_uint2(rv[i].z, rv[i].w);
+            *(uint2 *)(d + 8) = make_uint2(rv[i].z, rv[i].w);
         }
     };
     /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
     uint4 k0r[2];
     {
-        const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2;
-        const int k0off = t0 * KB * a.ld_k * 2;
-        k0r[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, k0off, 0));
-        k0r[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off,
-                                                                                  k0off + 32 * a.ld_k * 2, 0));
+        const int k_off = ((tid >> 4) * a.ld_k + (tid & 15) * 8) * 2 + t0 * KB * a.ld_k * 2;
+        k0r[0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off, 0, 0));
+        k0r[1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(k_rsrc, k_off + 32 * a.ld_k * 2,
+                                                                                  0, 0));
     }
     /* Q loads next, so that their latency and K(0)'s overlap: the fragments
      * (B operand: lane holds query lr of the wave's 32, d = ds*16 + lg*8 ..
@@ -292,9 +300,8 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
 #pragma unroll
             for (int dsub = 0; dsub < 4; dsub++) {
                 const int d = dsub * 32 + lr;
-                const uint2 lo = *(const uint2 *)(&vb[d * VSTR + (4 * j + lg) * 4]);
-                const uint2 hi = *(const uint2 *)(&vb[d * VSTR + (4 * j + 2 + lg) * 4]);
-                const bf16x8 vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                /* keys 16j + 4lg .. +3 and 16j + 8 + 4lg .. +3: the k order of pf[j] */
+                const bf16x8 vf = *(const bf16x8 *)(&vb[d * VSTR + 16 * j + 8 * lg]);
                 o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[dsub], 0, 0, 0);
             }
         }
