@@ -48,6 +48,26 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
                              int w, const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
                              int text_seq_uncond, float guidance_scale, const float *schedule, int num_steps,
                              void (*progress_callback)(int step, int total));
+/* one reference image at RoPE T coordinate t_offset (iris_sample.c:543-625) */
+float *iris_sample_euler_with_refs(void *transformer, void *text_encoder, float *z, int batch, int channels, int h,
+                                   int w, const float *ref_latent, int ref_h, int ref_w, int t_offset,
+                                   const float *text_emb, int text_seq, const float *schedule, int num_steps,
+                                   void (*progress_callback)(int step, int total));
+/* CFG with reference images (iris_sample.c:807-989): the reference tokens join
+ * both branches; one batch-2 pass when the text lengths match, else two
+ * sequential passes; a CSD style delta acts on both branches, as in the
+ * reference */
+float *iris_sample_euler_cfg_with_refs(void *transformer, void *text_encoder, float *z, int batch, int channels, int h,
+                                       int w, const float *ref_latent, int ref_h, int ref_w, int t_offset,
+                                       const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
+                                       int text_seq_uncond, float guidance_scale, const float *schedule,
+                                       int num_steps, void (*progress_callback)(int step, int total));
+float *iris_sample_euler_cfg_with_multi_refs(void *transformer, void *text_encoder, float *z, int batch, int channels,
+                                             int h, int w, const iris_ref_t *refs, int num_refs,
+                                             const float *text_emb_cond, int text_seq_cond,
+                                             const float *text_emb_uncond, int text_seq_uncond, float guidance_scale,
+                                             const float *schedule, int num_steps,
+                                             void (*progress_callback)(int step, int total));
 float *iris_sample_euler_zimage(void *transformer, float *z, int batch, int channels, int h, int w, int patch_size,
                                 const float *cap_feats, int cap_seq, const float *schedule, int num_steps,
                                 void (*progress_callback)(int step, int total));

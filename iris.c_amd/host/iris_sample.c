@@ -4,7 +4,7 @@
  * Noise follows iris_sample.c:1146-1188 and the xoshiro256** RNG of
  * iris_kernels.c:50-107 (same seeds give the same noise); the schedules are
  * in iris_schedule.c.
- * The Euler loops (iris_sample.c:313-405, :412-536, :630-702, :717-802) keep
+ * The Euler loops (iris_sample.c:313-405, :412-536, :543-702, :717-989) keep
  * the latent resident on the device: one upload, one graph replay and one
  * update kernel per step, one download at the end.
  */
@@ -110,28 +110,17 @@ float *iris_sample_euler_with_multi_refs(void *transformer, void *text_encoder, 
                      schedule, num_steps, progress_callback);
 }
 
-float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, int batch, int channels, int h, int w,
-                             const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
-                             int text_seq_uncond, float guidance_scale, const float *schedule, int num_steps,
-                             void (*progress_callback)(int, int)) {
-    (void)text_encoder; (void)batch;
-    iris_transformer_t *tf = (iris_transformer_t *)transformer;
-    if (text_seq_cond == text_seq_uncond && !iris_transformer_csd_active(tf)) {
-        /* one batch-2 pass per step: slot 0 = uncond, slot 1 = cond */
-        size_t tsz = (size_t)text_seq_cond * iris_transformer_text_dim(tf);
-        float *both = (float *)malloc(2 * tsz * sizeof(float));
-        if (!both) return NULL;
-        memcpy(both, text_emb_uncond, tsz * sizeof(float));
-        memcpy(both + tsz, text_emb_cond, tsz * sizeof(float));
-        float *r = flux_loop(tf, z, channels, h, w, NULL, 0, both, text_seq_cond, 2, guidance_scale, schedule,
-                             num_steps, progress_callback);
-        free(both);
-        return r;
+/* Two sequential forwards per step (v_u, then v_c) with the guided Euler
+ * update on the device; style_cfg: the CSD style delta is suppressed on the
+ * unconditional forward (the plain CFG sampler, iris_sample.c:750-760; the
+ * reference-image CFG samplers :807-989 keep it on both). */
+static float *cfg_two_pass(iris_transformer_t *tf, const float *z, int channels, int h, int w, const iris_ref_t *refs,
+                           int nrefs, const float *tc, int Tc, const float *tu, int Tu, float g, const float *sched,
+                           int num_steps, void (*cb)(int, int), int style_cfg) {
+    if (num_steps > IRIS_MAX_STEPS) {
+        fprintf(stderr, "iris_sample: num_steps %d exceeds IRIS_MAX_STEPS %d\n", num_steps, IRIS_MAX_STEPS);
+        return NULL;
     }
-    /* different text lengths, or a CSD style delta (applied to the
-     * conditional forward only, iris_sample.c:750-760): two sequential
-     * forwards per step, as the reference; the guided Euler update runs on
-     * the device */
     size_t n = (size_t)channels * h * w;
     float *zc = (float *)malloc(n * sizeof(float));
     float *dz = (float *)iris_hip_malloc(3 * n * sizeof(float));
@@ -145,17 +134,16 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
     for (int i = 0; ok && i < num_steps; i++) {
         if (iris_step_callback) iris_step_callback(i + 1, num_steps);
         if (iris_cancel_requested || iris_hip_memcpy_d2h(zc, dz, n * sizeof(float))) { ok = 0; break; }
-        iris_transformer_set_csd_skip(tf, 1);
-        float *vu = iris_transformer_forward(tf, zc, h, w, text_emb_uncond, text_seq_uncond, schedule[i]);
-        iris_transformer_set_csd_skip(tf, 0);
-        float *vc = vu ? iris_transformer_forward(tf, zc, h, w, text_emb_cond, text_seq_cond, schedule[i]) : NULL;
+        if (style_cfg) iris_transformer_set_csd_skip(tf, 1);
+        float *vu = iris_transformer_forward_with_multi_refs(tf, zc, h, w, refs, nrefs, tu, Tu, sched[i]);
+        if (style_cfg) iris_transformer_set_csd_skip(tf, 0);
+        float *vc = vu ? iris_transformer_forward_with_multi_refs(tf, zc, h, w, refs, nrefs, tc, Tc, sched[i]) : NULL;
         ok = vu && vc && !iris_hip_memcpy_h2d(dvu, vu, n * sizeof(float)) &&
              !iris_hip_memcpy_h2d(dvc, vc, n * sizeof(float)) &&
-             !iris_hip_euler(dz, dvu, dvc, guidance_scale, schedule[i + 1] - schedule[i], 1.0f, n) &&
-             !iris_hip_sync();
+             !iris_hip_euler(dz, dvu, dvc, g, sched[i + 1] - sched[i], 1.0f, n) && !iris_hip_sync();
         free(vu);
         free(vc);
-        if (ok && progress_callback) progress_callback(i + 1, num_steps);
+        if (ok && cb) cb(i + 1, num_steps);
     }
     if (ok && iris_hip_memcpy_d2h(zc, dz, n * sizeof(float))) ok = 0;
     iris_hip_free(dz);
@@ -164,6 +152,79 @@ float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, in
         return NULL;
     }
     return zc;
+}
+
+/* both CFG branches as one batch-2 pass: slot 0 = uncond, slot 1 = cond */
+static float *cfg_batch2(iris_transformer_t *tf, const float *z, int channels, int h, int w, const iris_ref_t *refs,
+                         int nrefs, const float *tc, const float *tu, int T, float g, const float *sched,
+                         int num_steps, void (*cb)(int, int)) {
+    size_t tsz = (size_t)T * iris_transformer_text_dim(tf);
+    float *both = (float *)malloc(2 * tsz * sizeof(float));
+    if (!both) return NULL;
+    memcpy(both, tu, tsz * sizeof(float));
+    memcpy(both + tsz, tc, tsz * sizeof(float));
+    float *r = flux_loop(tf, z, channels, h, w, refs, nrefs, both, T, 2, g, sched, num_steps, cb);
+    free(both);
+    return r;
+}
+
+float *iris_sample_euler_cfg(void *transformer, void *text_encoder, float *z, int batch, int channels, int h, int w,
+                             const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
+                             int text_seq_uncond, float guidance_scale, const float *schedule, int num_steps,
+                             void (*progress_callback)(int, int)) {
+    (void)text_encoder; (void)batch;
+    iris_transformer_t *tf = (iris_transformer_t *)transformer;
+    if (text_seq_cond == text_seq_uncond && !iris_transformer_csd_active(tf))
+        return cfg_batch2(tf, z, channels, h, w, NULL, 0, text_emb_cond, text_emb_uncond, text_seq_cond,
+                          guidance_scale, schedule, num_steps, progress_callback);
+    /* different text lengths, or a CSD style delta (applied to the
+     * conditional forward only): two sequential forwards per step */
+    return cfg_two_pass(tf, z, channels, h, w, NULL, 0, text_emb_cond, text_seq_cond, text_emb_uncond,
+                        text_seq_uncond, guidance_scale, schedule, num_steps, progress_callback, 1);
+}
+
+/* iris_sample_euler_with_refs (iris_sample.c:543-625): one reference image
+ * at RoPE T coordinate t_offset */
+float *iris_sample_euler_with_refs(void *transformer, void *text_encoder, float *z, int batch, int channels, int h,
+                                   int w, const float *ref_latent, int ref_h, int ref_w, int t_offset,
+                                   const float *text_emb, int text_seq, const float *schedule, int num_steps,
+                                   void (*progress_callback)(int, int)) {
+    const iris_ref_t r = {ref_latent, ref_h, ref_w, t_offset};
+    return iris_sample_euler_with_multi_refs(transformer, text_encoder, z, batch, channels, h, w, &r,
+                                             ref_latent ? 1 : 0, text_emb, text_seq, schedule, num_steps,
+                                             progress_callback);
+}
+
+/* iris_sample_euler_cfg_with_multi_refs (iris_sample.c:898-989): the
+ * reference tokens join both branches; a CSD delta stays on both (the
+ * reference toggles it only in the plain CFG sampler) */
+float *iris_sample_euler_cfg_with_multi_refs(void *transformer, void *text_encoder, float *z, int batch, int channels,
+                                             int h, int w, const iris_ref_t *refs, int num_refs,
+                                             const float *text_emb_cond, int text_seq_cond,
+                                             const float *text_emb_uncond, int text_seq_uncond, float guidance_scale,
+                                             const float *schedule, int num_steps,
+                                             void (*progress_callback)(int, int)) {
+    (void)text_encoder; (void)batch;
+    iris_transformer_t *tf = (iris_transformer_t *)transformer;
+    if (!refs) num_refs = 0;
+    if (text_seq_cond == text_seq_uncond)
+        return cfg_batch2(tf, z, channels, h, w, refs, num_refs, text_emb_cond, text_emb_uncond, text_seq_cond,
+                          guidance_scale, schedule, num_steps, progress_callback);
+    return cfg_two_pass(tf, z, channels, h, w, refs, num_refs, text_emb_cond, text_seq_cond, text_emb_uncond,
+                        text_seq_uncond, guidance_scale, schedule, num_steps, progress_callback, 0);
+}
+
+/* iris_sample_euler_cfg_with_refs (iris_sample.c:807-893) */
+float *iris_sample_euler_cfg_with_refs(void *transformer, void *text_encoder, float *z, int batch, int channels, int h,
+                                       int w, const float *ref_latent, int ref_h, int ref_w, int t_offset,
+                                       const float *text_emb_cond, int text_seq_cond, const float *text_emb_uncond,
+                                       int text_seq_uncond, float guidance_scale, const float *schedule,
+                                       int num_steps, void (*progress_callback)(int, int)) {
+    const iris_ref_t r = {ref_latent, ref_h, ref_w, t_offset};
+    return iris_sample_euler_cfg_with_multi_refs(transformer, text_encoder, z, batch, channels, h, w, &r,
+                                                 ref_latent ? 1 : 0, text_emb_cond, text_seq_cond, text_emb_uncond,
+                                                 text_seq_uncond, guidance_scale, schedule, num_steps,
+                                                 progress_callback);
 }
 
 /* iris_sample_euler_zimage (iris_sample.c:412-536): velocity at timestep

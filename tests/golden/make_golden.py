@@ -132,6 +132,35 @@ def flux_goldens(r, d, res):
     res["flux_sample2"] = tl.take_f32(r, p, 128 * 64)
     res["flux_sample2_sched"] = sched_arr
     res["flux_noise42"] = noise_arr
+    # the reference-image samplers: one reference (T offset 1), two references,
+    # CFG over both references with equal text lengths, CFG over one
+    # reference with an uncond text of 20 tokens
+    V, I_ = ctypes.c_void_p, ctypes.c_int
+    r.iris_sample_euler_with_refs.argtypes = [V, V, tl.FP, I_, I_, I_, I_, tl.FP, I_, I_, I_, tl.FP, I_, tl.FP, I_, V]
+    r.iris_sample_euler_with_multi_refs.argtypes = [V, V, tl.FP, I_, I_, I_, I_, V, I_, tl.FP, I_, tl.FP, I_, V]
+    r.iris_sample_euler_cfg_with_multi_refs.argtypes = [V, V, tl.FP, I_, I_, I_, I_, V, I_, tl.FP, I_, tl.FP, I_,
+                                                        ctypes.c_float, tl.FP, I_, V]
+    r.iris_sample_euler_cfg_with_refs.argtypes = [V, V, tl.FP, I_, I_, I_, I_, tl.FP, I_, I_, I_, tl.FP, I_, tl.FP,
+                                                  I_, ctypes.c_float, tl.FP, I_, V]
+    for fn in ("iris_sample_euler_with_refs", "iris_sample_euler_with_multi_refs",
+               "iris_sample_euler_cfg_with_multi_refs", "iris_sample_euler_cfg_with_refs"):
+        getattr(r, fn).restype = V
+    txt_u = tl.synth_f32((T, 256), 25)
+    txt_u20 = tl.synth_f32((20, 256), 26)
+    p = r.iris_sample_euler_with_refs(tf, None, tl.fptr(noise_arr), 1, 128, 8, 8, tl.fptr(r1), 8, 8, 1,
+                                      tl.fptr(temb_txt), T, tl.fptr(sched_arr), 2, None)
+    res["flux_sample2_ref1"] = tl.take_f32(r, p, 128 * 64)
+    p = r.iris_sample_euler_with_multi_refs(tf, None, tl.fptr(noise_arr), 1, 128, 8, 8, refs, 2, tl.fptr(temb_txt), T,
+                                            tl.fptr(sched_arr), 2, None)
+    res["flux_sample2_refs"] = tl.take_f32(r, p, 128 * 64)
+    p = r.iris_sample_euler_cfg_with_multi_refs(tf, None, tl.fptr(noise_arr), 1, 128, 8, 8, refs, 2,
+                                                tl.fptr(temb_txt), T, tl.fptr(txt_u), T, 4.0, tl.fptr(sched_arr), 2,
+                                                None)
+    res["flux_sample2_cfg_refs"] = tl.take_f32(r, p, 128 * 64)
+    p = r.iris_sample_euler_cfg_with_refs(tf, None, tl.fptr(noise_arr), 1, 128, 8, 8, tl.fptr(r2), 4, 6, 2,
+                                          tl.fptr(temb_txt), T, tl.fptr(txt_u20), 20, 3.0, tl.fptr(sched_arr), 2,
+                                          None)
+    res["flux_sample2_cfg_ref1_t20"] = tl.take_f32(r, p, 128 * 64)
     r.iris_transformer_free(tf)
 
 
