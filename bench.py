@@ -11,11 +11,14 @@ c4 (9B-shaped, CFG as batch 2), c5 (Z-Image-Turbo-6B-shaped, 8 NFE), qwen3
 (the Qwen3-4B-shaped text encoder at 512 tokens; a "step" is one encode).
 
 Prints one JSON line. `value` is images/s; ms_per_step is per denoise step.
-`roofline` is the kernel class with the largest share of the step (the fused
-projection GEMM or the flash attention). Its launch_ms is its average
-duration inside a step: after the timed steps one more step runs launch by
-launch with two HIP events on the library stream around every launch
-(iris_hip_profile_enable; the per-kernel table is `profiled_step`);
+`roofline` is the kernel class with the largest share of the step (the
+gate/up projection GEMM with its SwiGLU epilogue, or the flash attention).
+Its launch_ms is its average duration inside a step: after the timed steps
+one more step runs launch by launch with two HIP events on the library
+stream around every launch and the launches issued one after the other (in
+the timed steps each single block's gate/up product runs on a side stream
+beside its QKV product and attention); the per-kernel table is
+`profiled_step` (iris_hip_profile_enable);
 back_to_back_launch_ms times the same kernel alone over 30 launches on the
 step's resident buffers. `cpu_baseline` times the oracle (C restatement of the reference's
 f32 `make blas` path on OpenBLAS) on one block of each kind at the same shape,
@@ -208,13 +211,11 @@ def run_flux(lib, c, args):
     S_pad = (S + 63) // 64 * 64
     BS = B * S
     dbuf = {n: lib.iris_flux_device_buffer(tf, n.encode()) for n in ("a", "qkv", "cat", "q", "k", "vt")}
-    wdev = tl.Dev((3 * h + 2 * mlp) * h * 2)
-    wdev.put(tl.to_bf16(tl.synth_f32(((3 * h + 2 * mlp) * h,), 9, 0, 0.02)))
+    wdev = tl.Dev(2 * mlp * h * 2)
+    wdev.put(tl.to_bf16(tl.synth_f32((2 * mlp * h,), 9, 0, 0.02)))
     P = tl.GemmProblem
-    probs = (P * 2)(P(dbuf["a"], wdev.ptr, dbuf["qkv"], None, BS, 3 * h, h, h, h, 3 * h, 1),
-                    P(dbuf["a"], wdev.ptr + 3 * h * h * 2, dbuf["cat"] + h * 2, None, BS, 2 * mlp, h, h, h,
-                      h + mlp, 3))
-    g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(probs, 2))
+    probs = (P * 1)(P(dbuf["a"], wdev.ptr, dbuf["cat"] + h * 2, None, BS, 2 * mlp, h, h, h, h + mlp, 3))
+    g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(probs, 1))
     # the joint attention as the step runs it: Q normalised and rotated in the prologue
     wq = tl.Dev.of(np.ones(128, np.float32))
     rc, rs = (lib.iris_flux_device_buffer(tf, n) for n in (b"rope_pair_cos", b"rope_pair_sin"))
@@ -228,11 +229,13 @@ def run_flux(lib, c, args):
     wdev.close()
     wq.close()
     aws.close()
-    g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(BS, 3 * h), (BS, 2 * mlp)]))
+    # the gate/up launches of the single blocks and, when their text and image
+    # rows are whole 256-row tiles, of the double blocks (the same M x N x K)
+    g_in, g_n = in_step(prof, "gemm_bf16_kernel<0>", gemm_grid([(BS, 2 * mlp)]))
     a_in, a_n = in_step_attn(prof, c["nd"] + c["ns"])
-    assert g_n == c["ns"], g_n
-    kernels = [kernel_entry("gemm_bf16_kernel: single-block fused QKV (bf16 out) + gate/up (SwiGLU epilogue)", g_in,
-                            2.0 * BS * h * (3 * h + 2 * mlp), g_n, f"gemm_fused_{args.config}", g_ms),
+    assert g_n in (c["ns"], c["nd"] + c["ns"]), g_n
+    kernels = [kernel_entry("gemm_bf16_kernel: gate/up projection, SwiGLU epilogue", g_in,
+                            2.0 * BS * h * 2 * mlp, g_n, f"gemm_gateup_{args.config}", g_ms),
                kernel_entry("flash_attn_kernel: joint attention, head_dim 128", a_in, 4.0 * B * S * S * h, a_n,
                             f"attn_{args.config}", a_ms)]
     lib.iris_transformer_free(tf)
@@ -321,7 +324,7 @@ def measured_traffic(key):
 
 def probe(kind, n):
     """Launch one kernel class n times on synthetic NS-shaped buffers (the
-    program that the counter runs profile): `gemm` = the single-block fused
+    program that the counter runs profile): `gemm` = the gate/up
     projection GEMM, `attn` = the joint attention, `rownorm` = the AdaLN
     row pass, `kvprep` = K RMSNorm + RoPE and the V transpose, `copy` = a 1 GiB
     device-to-device copy (the calibration kernel of known size)."""
@@ -340,13 +343,13 @@ def probe(kind, n):
         return d.ptr
 
     if kind == "gemm":
-        a, w = dev(S * h * 2, 3), dev((3 * h + 2 * mlp) * h * 2, 9, 0.02)
-        qkv, cat = dev(S * 3 * h * 2), dev(S * (h + mlp) * 2)
+        # gate/up rows of the single block's first linear, SwiGLU epilogue into cat[:, h:]
+        a, w = dev(S * h * 2, 3), dev(2 * mlp * h * 2, 9, 0.02)
+        cat = dev(S * (h + mlp) * 2)
         P = tl.GemmProblem
-        probs = (P * 2)(P(a, w, qkv, None, S, 3 * h, h, h, h, 3 * h, 1),
-                        P(a, w + 3 * h * h * 2, cat + h * 2, None, S, 2 * mlp, h, h, h, h + mlp, 3))
-        fn = lambda: lib.iris_hip_gemm(probs, 2)  # noqa: E731
-        alg = 2 * S * h + 2 * (3 * h + 2 * mlp) * h + 2 * S * (3 * h + mlp)
+        probs = (P * 1)(P(a, w, cat + h * 2, None, S, 2 * mlp, h, h, h, h + mlp, 3))
+        fn = lambda: lib.iris_hip_gemm(probs, 1)  # noqa: E731
+        alg = 2 * S * h + 2 * 2 * mlp * h + 2 * S * mlp
     elif kind == "attn":
         q, k = dev(S * 3 * h * 2, 11), dev(S * h * 2, 12)
         vt, o = dev(H * 128 * S_pad * 2, 13), dev(S * (h + mlp) * 2)

@@ -63,6 +63,19 @@ int iris_hip_profile_enable(int on);
 int iris_hip_profile_enabled(void);
 int iris_hip_profile_read(iris_kernel_time_t *out, int max);
 
+/* ---- side stream (no counterpart in the reference) ----
+ * Work that does not feed what follows it on the library stream can run
+ * beside it: iris_hip_fork makes the side stream wait for everything enqueued
+ * on the library stream so far; launches made between iris_hip_side(1) and
+ * iris_hip_side(0) go to the side stream; iris_hip_join makes the library
+ * stream wait for everything enqueued on the side stream. Inside a graph
+ * capture of the library stream the side stream is captured with it (fork
+ * and join become dependency edges); every fork is joined before the capture
+ * ends. Synchronisation and copies stay on the library stream. */
+int iris_hip_fork(void);
+void iris_hip_side(int on);
+int iris_hip_join(void);
+
 /* ---- graph capture of the library stream (cf. iris_gpu_batch_begin/end) ---- */
 int iris_hip_graph_begin(void);
 void *iris_hip_graph_end(void);                      /* instantiated graph, NULL on error */

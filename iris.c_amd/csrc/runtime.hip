@@ -16,6 +16,11 @@
 static int g_init = 0;
 static int g_device = -1;
 static hipStream_t g_stream = nullptr;
+/* side stream: launches between iris_hip_side(1) and iris_hip_side(0) go to it;
+ * fork / join order it against the library stream with two events */
+static hipStream_t g_side = nullptr;
+static hipEvent_t g_fork_ev = nullptr, g_join_ev = nullptr;
+static int g_on_side = 0;
 static char g_err[512] = "";
 static char g_name[256] = "";
 static std::atomic<size_t> g_in_use{0};
@@ -24,7 +29,7 @@ static int g_events_made = 0;
 static hipGraph_t g_capture_graph = nullptr;
 static int g_cus = 0;
 
-hipStream_t iris_stream(void) { return g_stream; }
+hipStream_t iris_stream(void) { return g_on_side ? g_side : g_stream; }
 int iris_cu_count(void) { return g_cus; }
 
 int iris_set_error(const char *fmt, ...) {
@@ -60,6 +65,11 @@ int iris_hip_init(int device) {
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return iris_set_error("kernels are built for gfx950, device is %s", p.gcnArchName);
     if (iris_check(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreate")) return -1;
+    /* both streams at the default priority */
+    if (iris_check(hipStreamCreateWithFlags(&g_side, hipStreamNonBlocking), "hipStreamCreate (side)") ||
+        iris_check(hipEventCreateWithFlags(&g_fork_ev, hipEventDisableTiming), "hipEventCreate (fork)") ||
+        iris_check(hipEventCreateWithFlags(&g_join_ev, hipEventDisableTiming), "hipEventCreate (join)"))
+        return -1;
     g_cus = p.multiProcessorCount;
     g_device = device;
     g_init = 1;
@@ -296,6 +306,20 @@ int iris_hip_profile_read(iris_kernel_time_t *out, int max) {
     }
     if (g_prof_lost) iris_set_error("profile: %d launches past the %d recorded", g_prof_lost, PROF_MAX);
     return n;
+}
+
+int iris_hip_fork(void) {
+    if (!iris_hip_available()) return -1;
+    return iris_check(hipEventRecord(g_fork_ev, g_stream), "fork record") ||
+           iris_check(hipStreamWaitEvent(g_side, g_fork_ev, 0), "fork wait");
+}
+
+void iris_hip_side(int on) { g_on_side = on != 0; }
+
+int iris_hip_join(void) {
+    if (!iris_hip_available()) return -1;
+    return iris_check(hipEventRecord(g_join_ev, g_side), "join record") ||
+           iris_check(hipStreamWaitEvent(g_stream, g_join_ev, 0), "join wait");
 }
 
 int iris_hip_graph_begin(void) {

@@ -357,6 +357,27 @@ def test_4b_forward_reduced_depth(lib, orc):
     assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
 
 
+def test_side_stream_forward_bitwise(lib):
+    """4B widths, 1 double + 2 single blocks, 64x64 latent + 512 text tokens:
+    the captured step (each single block's gate/up product on the side
+    stream, beside its QKV product and attention) equals the profiled step
+    (the same launches one after the other) bit for bit, over repeated
+    replays."""
+    tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(3072, 24, 1, 2, 7680, 128, 3.0, 2000.0, 123))
+    lat, txt = tl.synth_f32((128, 64, 64), 81), tl.synth_f32((512, 7680), 82)
+    n = 128 * 4096
+    fwd = lambda: take(lib, lib.iris_transformer_forward(tf, tl.fptr(lat), 64, 64, tl.fptr(txt), 512,  # noqa: E731
+                                                         F(0.7)), n)
+    graph = fwd()
+    assert lib.iris_hip_profile_enable(1) == 0
+    seq = fwd()
+    assert lib.iris_hip_profile_enable(0) == 0
+    np.testing.assert_array_equal(seq, graph)
+    for _ in range(3):
+        np.testing.assert_array_equal(fwd(), graph)
+    lib.iris_transformer_free(tf)
+
+
 def test_9b_cfg_step_reduced_depth(lib, orc):
     """9B widths (h 4096, 32 heads, text 12288) with 1 double + 1 single block.
     Each velocity against the oracle (rel-L2 < 1e-2, cosine > 0.999); one CFG
