@@ -566,11 +566,14 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
     const int per_xcd = (int)((total + 7) / 8);
     const float scale_log2 = a->scale * 1.4426950408889634f;
     int feat = (fuseq ? F_FUSEQ : 0) | (a->causal ? F_CAUSAL : 0) | (a->key_bias != 0.0f ? F_BIAS : 0);
-    /* balanced schedule when one block per unit leaves the rounds of blocks
-     * (one per CU) less than 80 % full on average and a workspace is given.
-     * Above that the part-empty last round costs little: the chip is at its
-     * power limit and fewer busy CUs run at a higher clock (432 units on 256
-     * CUs time the same either way; 540 units run 17 % faster balanced). */
+    /* balanced schedule when one block per unit needs two or more rounds of
+     * blocks (one per CU) that are on average less than 60 % full, and a
+     * workspace is given. Merging the pieces' partial states goes through
+     * memory at system coherence (128 KiB of o per piece) and every piece
+     * repeats the Q prologue, so elsewhere one block per unit is faster (same
+     * box, 128-dim heads: 270 units on 256 CUs 136.5 -> 129.7 us balanced;
+     * 540 units 390.6 -> 430.7 us and 144 units 48.6 -> 72.3 us, where the
+     * part-empty round lets the busy CUs run at a higher clock). */
     AttnSplit sp;
     memset(&sp, 0, sizeof(sp));
     const int cus = iris_cu_count(), nkt = (a->sk + KB - 1) / KB;
@@ -578,7 +581,7 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
         a->ws_bytes >= iris_hip_attention_workspace_bytes()) {
         const long long rounds = (total + cus - 1) / cus;
         const long long steps = total * (long long)nkt;
-        if ((double)total < 0.8 * (double)(rounds * cus) && steps / cus >= 8 && steps < (1LL << 31)) {
+        if (rounds >= 2 && (double)total < 0.6 * (double)(rounds * cus) && steps / cus >= 8 && steps < (1LL << 31)) {
             if (((uintptr_t)a->ws & 255)) return iris_set_error("attention: workspace must be 256-byte aligned");
             sp.nkt = nkt;
             sp.per = (int)(steps / cus);
