@@ -56,11 +56,15 @@
  *
  * LDS rows are padded instead of swizzled, so every fragment address is one
  * base register plus an immediate offset: K rows hold 128 + 8 elements (272 B:
- * 16 consecutive rows start 4 banks apart, conflict-free 16-byte reads), V^T
- * rows 64 + 8 (144 B: 16 consecutive rows start at 16 distinct 4-bank
- * groups). Within each 16 keys a V^T row is stored in the order the P
- * fragments take them (keys 0-3, 8-11, 4-7, 12-15), so a lane's 8 keys of one
- * PV product are one 16-byte read. Global loads go through buffer
+ * 16 consecutive rows start 4 banks apart, conflict-free 16-byte reads). V^T
+ * rows take one of two layouts. One block per unit: rows of 64 + 8 (144 B: 16
+ * consecutive rows start at 16 distinct 4-bank groups), each 16 keys stored
+ * in the order the P fragments take them (keys 0-3, 8-11, 4-7, 12-15), so a
+ * lane's 8 keys of one PV product are one 16-byte read. Balanced schedule:
+ * rows of 64 + 4 (136 B) in key order, read as two 8-byte halves, which
+ * measured faster there (540 units of 4096 keys, same box: 345.7 us against
+ * 407.5 us with the 16-byte layout, while one block per unit gains with it:
+ * 432 units of 4608 keys 258.1 -> 253.3 us). Global loads go through buffer
  * descriptors; K's range ends at its last valid row so rows past the end read
  * as zero.
  *
@@ -76,15 +80,19 @@ namespace {
 
 constexpr int QB = 256, KB = 64, HD = 128, NT = 512, NW = NT / 64, QW = QB / NW;
 constexpr float RESCALE_LOG2 = 8.0f;
-constexpr int KSTR = HD + 8, VSTR = KB + 8;
-constexpr int KS_ELEMS = KB * KSTR, VS_ELEMS = HD * VSTR;
-constexpr size_t SMEM_BYTES = (size_t)(2 * KS_ELEMS + 2 * VS_ELEMS) * 2;
-/* with the Q prologue: each wave's 32 normalised, rotated rows after the stages */
-constexpr int QS_OFF = 2 * KS_ELEMS + 2 * VS_ELEMS;
-constexpr size_t SMEM_FUSEQ_BYTES = SMEM_BYTES + (size_t)NW * 32 * KSTR * 2;
+constexpr int KSTR = HD + 8, KS_ELEMS = KB * KSTR;
 static_assert(QW == 32, "one 32-query MFMA column block per wave");
 
 enum { F_FUSEQ = 1, F_CAUSAL = 2, F_BIAS = 4, F_SPLIT = 8 };
+
+/* LDS of one block: two K stages, two V^T stages and, with the Q prologue,
+ * each wave's 32 normalised, rotated rows after them */
+template <int FEAT> struct AttnLds {
+    static constexpr bool V16 = !(FEAT & F_SPLIT); /* V^T read as 16-byte chunks */
+    static constexpr int VSTR = V16 ? KB + 8 : KB + 4, VS_ELEMS = HD * VSTR;
+    static constexpr int QS_OFF = 2 * KS_ELEMS + 2 * VS_ELEMS;
+    static constexpr size_t BYTES = (size_t)QS_OFF * 2 + ((FEAT & F_FUSEQ) ? (size_t)NW * 32 * KSTR * 2 : 0);
+};
 
 /* Balanced schedule (F_SPLIT): the nkt key tiles of all units (query block,
  * head, batch) form one range of units * nkt steps, dealt out to the blocks
@@ -125,6 +133,8 @@ template <int FEAT>
 __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float scale_log2, int nqb, const int L,
                                              const int t0, int tn, const AttnSplit &sp, const AttnSeg sg) {
     constexpr bool FUSEQ = FEAT & F_FUSEQ, CAUSAL = FEAT & F_CAUSAL, BIAS = FEAT & F_BIAS;
+    constexpr bool V16 = AttnLds<FEAT>::V16;
+    constexpr int VSTR = AttnLds<FEAT>::VSTR, VS_ELEMS = AttnLds<FEAT>::VS_ELEMS, QS_OFF = AttnLds<FEAT>::QS_OFF;
     extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 #define KBUF(b) (smem + (b) * KS_ELEMS)
 #define VBUF(b) (smem + 2 * KS_ELEMS + (b) * VS_ELEMS)
@@ -159,11 +169,11 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
     const int kh_off = ((32 * grp + (gt >> 4)) * a.ld_k + (gt & 15) * 8) * 2;
     const int vh_off = ((64 * grp + (gt >> 3)) * a.ld_vt + (gt & 7) * 8) * 2;
     uint16_t *const kh_dst = smem + (32 * grp + (gt >> 4)) * KSTR + (gt & 15) * 8;
-    /* V^T chunk c = gt % 8 holds keys 8c .. 8c + 7 of the tile: key block c / 2,
-     * half c % 2; its first 4 keys go to 4 (c % 2), its last 4 to 8 + 4 (c % 2)
-     * of the block */
-    uint16_t *const vh_dst =
-        smem + 2 * KS_ELEMS + (64 * grp + (gt >> 3)) * VSTR + 16 * ((gt & 7) >> 1) + 4 * (gt & 1);
+    /* V^T chunk c = gt % 8 holds keys 8c .. 8c + 7 of the tile; in the 16-byte
+     * layout that is key block c / 2, half c % 2: its first 4 keys go to
+     * 4 (c % 2), its last 4 to 8 + 4 (c % 2) of the block */
+    uint16_t *const vh_dst = smem + 2 * KS_ELEMS + (64 * grp + (gt >> 3)) * VSTR +
+                             (V16 ? 16 * ((gt & 7) >> 1) + 4 * (gt & 1) : 8 * (gt & 7));
     uint4 rk[2], rv[2];
     auto load_k = [&](int kt) {
 #pragma unroll
@@ -186,7 +196,7 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
         for (int i = 0; i < 2; i++) {
             uint16_t *d = vh_dst + stage * VS_ELEMS + 32 * i * VSTR;
             *(uint2 *)d = make_uint2(rv[i].x, rv[i].y);
-            *(uint2 *)(d + 8) = make_uint2(rv[i].z, rv[i].w);
+            *(uint2 *)(d + (V16 ? 8 : 4)) = make_uint2(rv[i].z, rv[i].w);
         }
     };
     /* the whole K(0) tile: rows tid/16 and + 32, chunk tid % 16 */
@@ -301,7 +311,14 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
             for (int dsub = 0; dsub < 4; dsub++) {
                 const int d = dsub * 32 + lr;
                 /* keys 16j + 4lg .. +3 and 16j + 8 + 4lg .. +3: the k order of pf[j] */
-                const bf16x8 vf = *(const bf16x8 *)(&vb[d * VSTR + 16 * j + 8 * lg]);
+                bf16x8 vf;
+                if constexpr (V16) {
+                    vf = *(const bf16x8 *)(&vb[d * VSTR + 16 * j + 8 * lg]);
+                } else {
+                    const uint2 lo = *(const uint2 *)(&vb[d * VSTR + 16 * j + 4 * lg]);
+                    const uint2 hi = *(const uint2 *)(&vb[d * VSTR + 16 * j + 8 + 4 * lg]);
+                    vf = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                }
                 o[dsub] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[dsub], 0, 0, 0);
             }
         }
@@ -522,7 +539,7 @@ __global__ __launch_bounds__(NT) void flash_attn_kernel(const iris_attn_args_t a
 
 template <int FEAT>
 int launch(const iris_attn_args_t *a, float scale_log2, int nqb, int per_xcd, int total, const AttnSplit &sp) {
-    constexpr size_t smem = (FEAT & F_FUSEQ) ? SMEM_FUSEQ_BYTES : SMEM_BYTES;
+    constexpr size_t smem = AttnLds<FEAT>::BYTES;
     static bool attr_set = false;
     if (!attr_set) {
         if (iris_check(hipFuncSetAttribute((const void *)flash_attn_kernel<FEAT>,
@@ -567,13 +584,14 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
     const float scale_log2 = a->scale * 1.4426950408889634f;
     int feat = (fuseq ? F_FUSEQ : 0) | (a->causal ? F_CAUSAL : 0) | (a->key_bias != 0.0f ? F_BIAS : 0);
     /* balanced schedule when one block per unit needs two or more rounds of
-     * blocks (one per CU) that are on average less than 60 % full, and a
+     * blocks (one per CU) that are on average less than 80 % full, and a
      * workspace is given. Merging the pieces' partial states goes through
      * memory at system coherence (128 KiB of o per piece) and every piece
-     * repeats the Q prologue, so elsewhere one block per unit is faster (same
-     * box, 128-dim heads: 270 units on 256 CUs 136.5 -> 129.7 us balanced;
-     * 540 units 390.6 -> 430.7 us and 144 units 48.6 -> 72.3 us, where the
-     * part-empty round lets the busy CUs run at a higher clock). */
+     * repeats the Q prologue, so a single part-empty round stays one block per
+     * unit (same box, 128-dim heads: 144 units of 1536 keys 47.3 us, 63.3 us
+     * balanced, the idle CUs letting the busy ones clock higher), while 540
+     * units of 4096 keys take 390.3 -> 356.6 us and 270 units 136.5 ->
+     * 129.7 us balanced. */
     AttnSplit sp;
     memset(&sp, 0, sizeof(sp));
     const int cus = iris_cu_count(), nkt = (a->sk + KB - 1) / KB;
@@ -581,7 +599,7 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
         a->ws_bytes >= iris_hip_attention_workspace_bytes()) {
         const long long rounds = (total + cus - 1) / cus;
         const long long steps = total * (long long)nkt;
-        if (rounds >= 2 && (double)total < 0.6 * (double)(rounds * cus) && steps / cus >= 8 && steps < (1LL << 31)) {
+        if (rounds >= 2 && (double)total < 0.8 * (double)(rounds * cus) && steps / cus >= 8 && steps < (1LL << 31)) {
             if (((uintptr_t)a->ws & 255)) return iris_set_error("attention: workspace must be 256-byte aligned");
             sp.nkt = nkt;
             sp.per = (int)(steps / cus);
