@@ -78,6 +78,73 @@ constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 1
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+/* element offset of (row, col) in a staged output half of OC columns: rows
+ * padded by 16 bytes, or for 256 columns (a full 64 KiB stage) with the
+ * 16-byte chunk index XORed with row % 16 */
+template <int OC> __device__ __forceinline__ int opos(int row, int col) {
+    if constexpr (OC == 256) return row * 256 + ((((col >> 3) ^ (row & 15)) << 3) | (col & 7));
+    else return row * (OC + 8) + col;
+}
+
+/* bf16 epilogue of a whole tile through LDS (the caller has checked that the
+ * tile is in range and the output rows 16-byte aligned). Group g (rows
+ * 128 g .. 128 g + 127) stages its rows in stage g. SWIGLU: accumulator
+ * columns are 32-row gate / up groups, OC = half the tile width. */
+template <int OC, bool SWIGLU, int FM_, int FNT_>
+__device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_t *lds0, uint16_t *lds1,
+                                          const iris_gemm_problem_t &pr, const float *vec, int m0, int oc0, int wm,
+                                          int wn, int twn) {
+    static_assert(128 * (OC == 256 ? 256 : OC + 8) * 2 <= 2 * TILE_ELEMS * 2, "a staged half fits one stage");
+    constexpr int CPR = OC / 8; /* 16-byte chunks per row */
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int grp = (tid >> 6) >> 2;
+    uint16_t *const st = grp ? lds1 : lds0;
+    const int hrow = (wm & 1) * 64 + lr;
+    __syncthreads(); /* every wave is done with the K loop's stages */
+    if constexpr (SWIGLU) {
+#pragma unroll
+        for (int g = 0; g < FNT_ / 4; g++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int col = ((wn * twn + g * 64) >> 1) + h * 16 + lg * 4;
+#pragma unroll
+                for (int mi = 0; mi < FM_; mi++) {
+                    const f32x4 gt = acc[mi][4 * g + h], up = acc[mi][4 * g + 2 + h];
+                    uint16_t y[4];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) y[r] = f2bf_hw(silu_fast(gt[r]) * up[r]);
+                    *(uint2 *)(st + opos<OC>(hrow + mi * 16, col)) =
+                        make_uint2((uint32_t)y[0] | ((uint32_t)y[1] << 16), (uint32_t)y[2] | ((uint32_t)y[3] << 16));
+                }
+            }
+    } else {
+#pragma unroll
+        for (int ni = 0; ni < FNT_; ni++) {
+            const int col = wn * twn + ni * 16 + lg * 4;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (vec) {
+                const float4 t = *(const float4 *)(vec + oc0 + col);
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            }
+#pragma unroll
+            for (int mi = 0; mi < FM_; mi++) {
+                const f32x4 x = acc[mi][ni];
+                *(uint2 *)(st + opos<OC>(hrow + mi * 16, col)) =
+                    make_uint2((uint32_t)f2bf_hw(x[0] + v[0]) | ((uint32_t)f2bf_hw(x[1] + v[1]) << 16),
+                               (uint32_t)f2bf_hw(x[2] + v[2]) | ((uint32_t)f2bf_hw(x[3] + v[3]) << 16));
+            }
+        }
+    }
+    __syncthreads();
+    uint16_t *const out = (uint16_t *)pr.out + (size_t)(m0 + 128 * grp) * pr.ldo + oc0;
+    const int gt = tid & 255;
+#pragma unroll
+    for (int i = 0; i < 128 * CPR / 256; i++) {
+        const int c = gt + 256 * i, row = c / CPR, ch = c - row * CPR;
+        *(uint4 *)(out + (size_t)row * pr.ldo + ch * 8) = *(const uint4 *)(st + opos<OC>(row, ch * 8));
+    }
+}
+
 /* MODE 0: GEMM; 1: 3x3 convolution, stride 1, input optionally read through
  * a nearest 2x upsample; 2: 3x3 convolution, stride 2, right/bottom padding;
  * 3: GEMM with a second K segment (A2, W2) after the first. The modes are
@@ -374,6 +441,16 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * access per lane and 16x16 tile */
     const bool aligned = (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 && ((uintptr_t)vec & 15) == 0;
     const bool full = m0 + BM <= M && n0 + BNT <= N && aligned;
+    /* Whole tiles of bf16 output (plain or SwiGLU) go out through LDS: each
+     * group writes its 128 rows into one of the stages, now free, and then
+     * stores them as 16-byte chunks of whole rows, so one store instruction
+     * covers full 128-byte lines instead of 32-byte pieces of 16 rows (the
+     * direct stores left the waves stalled on issue). */
+    if (full && (ldo & 7) == 0 && (pr.epi == IRIS_EPI_BF16 || (BNT == BN && pr.epi == IRIS_EPI_SWIGLU))) {
+        if (pr.epi == IRIS_EPI_SWIGLU) stage_out<BNT / 2, true, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0 >> 1, wm, wn, TWN);
+        else stage_out<BNT, false, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0, wm, wn, TWN);
+        return;
+    }
     switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
