@@ -502,7 +502,33 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
 
     /* normalise and store O[q][d]: lane holds query lr, d = dsub*32 + (r>>2)*8 + lg*4 + (r&3) */
     const float l = l_run + __shfl_xor(l_run, 32, 64);
-    if (q_row < sq) {
+    if ((a.ld_o & 7) == 0 && ((uintptr_t)a.o & 15) == 0) {
+        /* through LDS (every stage is free after the last barrier): the block's
+         * 256 rows of 128 + 8 elements, then 16-byte chunks of whole rows, so a
+         * store instruction writes 4 full rows instead of 16-byte pieces of 32 */
+        constexpr int OSTR = HD + 8;
+        static_assert(QB * OSTR <= QS_OFF, "the O tile fits the K and V stages");
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        uint16_t *const orow = smem + (wave * QW + lr) * OSTR;
+#pragma unroll
+        for (int dsub = 0; dsub < 4; dsub++)
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                u16x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = f2bf(o[dsub][rb * 4 + e] * inv);
+                *(u16x4 *)(orow + dsub * 32 + rb * 8 + lg * 4) = v;
+            }
+        __syncthreads();
+        uint16_t *const Ob = O + (size_t)(qblk * QB) * a.ld_o;
+        const int nrow = min(QB, sq - qblk * QB);
+#pragma unroll
+        for (int i = 0; i < QB * (HD / 8) / NT; i++) {
+            const int c = tid + NT * i, row = c >> 4, ch = c & 15;
+            if (row < nrow) *(uint4 *)(Ob + (size_t)row * a.ld_o + ch * 8) = *(const uint4 *)(smem + row * OSTR + ch * 8);
+        }
+        if constexpr ((FEAT & F_SPLIT) != 0) __syncthreads(); /* the block's next segment stages K(0) here */
+    } else if (q_row < sq) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
         for (int dsub = 0; dsub < 4; dsub++)
