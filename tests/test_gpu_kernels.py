@@ -115,6 +115,44 @@ def test_gemm_repeat_bitwise_mixed_k(lib):
             assert np.array_equal(first, got), f"launch {rep} differs from the first"
 
 
+@pytest.mark.parametrize("M,N,K,epi,bias", [(4096, 4096, 64, EPI_BF16, False), (1000, 1344, 128, EPI_BF16, True),
+                                            (600, 1024, 192, EPI_SWIGLU, False)])
+def test_gemm_staged_stores_match_direct(lib, M, N, K, epi, bias):
+    """bf16 and SwiGLU outputs of whole tiles leave through LDS as 16-byte
+    chunks of full rows when the output rows are 16-byte aligned (ldo % 8 ==
+    0), and by direct 8-byte stores otherwise (ldo % 8 == 4, and the partial
+    tiles of either): the same bits both ways, nothing written past the
+    output columns, and float64 agreement. 4096 x 4096 takes 256-wide tiles
+    (staged rows XOR-swizzled) on a 256-CU device, 1000 x 1344 224-wide tiles
+    with a bias and a partial last row of tiles, the SwiGLU case 128-column
+    output halves of 32-row interleaved gate / up groups."""
+    rng = np.random.default_rng(M + N + K)
+    a = bf(rng.standard_normal((M, K), np.float32))
+    w = bf(rng.standard_normal((N, K), np.float32) * 0.05)
+    A, W = tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w))
+    b = rng.standard_normal(N).astype(np.float32)
+    vec = tl.Dev.of(b) if bias else None
+    ncol = N // 2 if epi == EPI_SWIGLU else N
+    outs = []
+    for ldo in (ncol, ncol + 4):
+        o = tl.Dev(M * ldo * 2)
+        assert lib.iris_hip_memset(o.ptr, 0xff, M * ldo * 2) == 0
+        run_gemm(lib, [tl.GemmProblem(A.ptr, W.ptr, o.ptr, vec.ptr if bias else None, M, N, K, K, K, ldo, epi)])
+        got = o.get(np.uint16, (M, ldo))
+        assert np.all(got[:, ncol:] == 0xffff), "stores past the output columns"
+        outs.append(got[:, :ncol])
+        o.close()
+    assert np.array_equal(outs[0], outs[1]), "staged and direct stores differ"
+    y = a.astype(np.float64) @ w.astype(np.float64).T
+    if epi == EPI_SWIGLU:
+        c = np.arange(ncol)
+        g, u = y[:, (c // 32) * 64 + c % 32], y[:, (c // 32) * 64 + 32 + c % 32]
+        ref = g / (1 + np.exp(-g)) * u
+    else:
+        ref = y + (b if bias else 0.0)
+    assert tl.rel_l2(tl.bf16_to_f32(outs[0]), ref) < 4e-3
+
+
 @pytest.mark.parametrize("M,N,K,splits", [(512, 2560, 4096, 8), (77, 640, 960, 7), (300, 384, 192, 3)])
 def test_gemm_splitk_epilogues(lib, M, N, K, splits):
     """Split-K against the float64 product for every epilogue, and bitwise
@@ -387,7 +425,7 @@ def test_flash_attention_repeat_bitwise_joint_shape(lib):
 def test_flash_attention_balanced_split(lib, S, H, fused, bias):
     """The balanced schedule (key tiles of all units dealt out in equal
     ranges, one per CU; pieces of a unit merged by the last block to arrive)
-    at unit counts that need two rounds of blocks under 60 % full (270, 279,
+    at unit counts that need two rounds of blocks under 80 % full (270, 279,
     288 with a key bias, 261 with a ragged end): against the float64 reference
     (1.5e-2, as the one-block-per-unit kernel) and against that kernel's
     output (the same bf16 rounding up to the merge), bit-identical over
@@ -444,6 +482,51 @@ def test_flash_attention_balanced_split(lib, S, H, fused, bias):
     assert tl.rel_l2(got, plain) < 1e-2
     assert not np.array_equal(got, plain), "the balanced schedule was not taken"
     print(f"split vs one block per unit: rel_l2 {tl.rel_l2(got, plain):.3e}")
+
+
+@pytest.mark.parametrize("S,H,batch,split", [(1000, 3, 2, False), (2304, 30, 1, True)])
+def test_flash_attention_staged_o_matches_direct(lib, S, H, batch, split):
+    """O leaves through LDS as 16-byte chunks of whole rows when its rows are
+    16-byte aligned (ld_o % 8 == 0) and by direct 8-byte stores otherwise
+    (ld_o % 8 == 4): the same bits both ways and nothing written past a row's
+    128 head columns, on a ragged last query block (1000 queries, batch 2)
+    and on the balanced schedule (270 units over 256 CUs: a block runs several
+    segments and stages the next K tile over the rows it stored O from)."""
+    rng = np.random.default_rng(S * H)
+    h = H * 128
+    S_pad = (S + 63) // 64 * 64
+    q = rng.standard_normal((batch, S, h)).astype(np.float32)
+    k = rng.standard_normal((batch, S, h)).astype(np.float32)
+    v = rng.standard_normal((batch, S, h)).astype(np.float32)
+    vt = np.zeros((batch, H, 128, S_pad), np.float32)
+    for bb in range(batch):
+        for hh in range(H):
+            vt[bb, hh, :, :S] = v[bb, :, hh * 128:(hh + 1) * 128].T
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(q)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    wsb = lib.iris_hip_attention_workspace_bytes() if split else 0
+    ws = tl.Dev(wsb) if split else None
+    if split:
+        assert lib.iris_hip_memset(ws.ptr, 0, wsb) == 0
+    outs = []
+    for ld_o in (h, h + 4):
+        o = tl.Dev(batch * S * ld_o * 2)
+        assert lib.iris_hip_memset(o.ptr, 0xff, batch * S * ld_o * 2) == 0
+        a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, o.ptr, h, h, S_pad, ld_o, S, S, H, batch, S * h, S * h,
+                        H * 128 * S_pad, S * ld_o, 1 / math.sqrt(128), 0, S, 0, 0, 0, 0, 0, 0.0, None, None, 0, 0.0,
+                        None, None, ws.ptr if split else None, wsb)
+        assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+        got = o.get(np.uint16, (batch, S, ld_o))
+        assert np.all(got[:, :, h:] == 0xffff), "stores past the head columns"
+        outs.append(got[:, :, :h])
+        o.close()
+    assert np.array_equal(outs[0], outs[1]), "staged and direct O stores differ"
+    got = tl.bf16_to_f32(outs[0])
+    for bb in range(batch):
+        hh = H - 1
+        sl = slice(hh * 128, (hh + 1) * 128)
+        ref = attention_ref(bf(q[bb, :, sl]), bf(k[bb, :, sl]), bf(v[bb, :, sl]), 1 / math.sqrt(128))
+        assert tl.rel_l2(got[bb, :, sl], ref) < 1.5e-2, bb
 
 
 @pytest.mark.parametrize("S,H,group,n_real", [(300, 4, 2, 250), (512, 8, 4, 512), (70, 2, 1, 70), (1, 4, 4, 1)])
