@@ -157,8 +157,8 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
  * a 16-lane shuffle reduction. The row's table values are loaded once for all
  * its heads. KONLY: K alone (Q is normalised in the attention prologue). */
 template <bool KONLY>
-__global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args_t a) {
-    const int row = blockIdx.x * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+__device__ __forceinline__ void qk_norm_rope_rows(const iris_qkprep_args_t &a, int blk) {
+    const int row = blk * (NT / IRIS_WAVE) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= a.rows) return;
     const int prow = a.period ? row % a.period : row;
     const bool use_b = prow >= a.split;
@@ -218,9 +218,8 @@ __global__ __launch_bounds__(NT) void qk_norm_rope_kernel(const iris_qkprep_args
  * block. LDS holds the tile as [d][row] in rows of 72 elements (16-byte
  * aligned); 8-row chunks are XOR-swizzled by (d / 8) mod 8 to spread the
  * two-row writes over the banks. Rows past the end are written as zeros. */
-__global__ __launch_bounds__(NT) void v_transpose_kernel(const iris_qkprep_args_t a) {
-    __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
-    const int r0 = blockIdx.x * 64, head = blockIdx.y, tid = threadIdx.x;
+__device__ __forceinline__ void v_transpose_tile(const iris_qkprep_args_t &a, int tile, int head, uint16_t *t) {
+    const int r0 = tile * 64, tid = threadIdx.x;
 #pragma unroll
     for (int it = 0; it < 2; it++) {                       /* 32 row pairs x 16 chunks of 8 dims */
         const int item = tid + NT * it, p = item >> 4, ch = item & 15;
@@ -244,6 +243,18 @@ __global__ __launch_bounds__(NT) void v_transpose_kernel(const iris_qkprep_args_
         const uint4 v = *(const uint4 *)(&t[d * 72 + ((c8 ^ ((d >> 3) & 7)) << 3)]);
         *(uint4 *)(dst + (size_t)d * a.ld_vt + c8 * 8) = v;
     }
+}
+
+/* The K (and Q) normalisation and the V transpose in one launch: blocks
+ * 0 .. vblocks - 1 transpose V tiles (vx tiles of 64 rows per head), the rest
+ * normalise 4 rows each. The two passes are short and HBM-bound; one launch
+ * runs them side by side instead of paying two ramps and two tails. */
+template <bool KONLY>
+__global__ __launch_bounds__(NT) void qkv_prep_kernel(const iris_qkprep_args_t a, int vblocks, int vx) {
+    __shared__ __attribute__((aligned(16))) uint16_t t[128 * 72];
+    const int b = blockIdx.x;
+    if (b < vblocks) v_transpose_tile(a, b % vx, b / vx, t);
+    else qk_norm_rope_rows<KONLY>(a, b - vblocks);
 }
 
 /* one wave per output row */
@@ -428,12 +439,11 @@ int iris_hip_qk_prepare(const iris_qkprep_args_t *a) {
         return iris_set_error("qk_prepare: heads=%d kv_heads=%d", a->heads, a->kv_heads);
     if (((uintptr_t)a->qkv | (uintptr_t)a->q_out | (uintptr_t)a->k_out | (uintptr_t)a->vt_out) & 15)
         return iris_set_error("qk_prepare: buffers must be 16-byte aligned");
-    IRIS_LAUNCH(qk_norm_rope_kernel<false>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
-                       iris_stream(), *a);
-    if (iris_launch_check("qk_norm_rope_kernel")) return -1;
-    const int kvh = a->kv_heads ? a->kv_heads : a->heads;
-    IRIS_LAUNCH(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
-    return iris_launch_check("v_transpose_kernel");
+    const int kvh = a->kv_heads ? a->kv_heads : a->heads, vx = a->ld_vt / 64;
+    const long long blocks = (long long)vx * kvh + (a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE);
+    if (blocks >= (1LL << 31)) return iris_set_error("qk_prepare: too many rows");
+    IRIS_LAUNCH(qkv_prep_kernel<false>, dim3((unsigned)blocks), dim3(NT), 0, iris_stream(), *a, vx * kvh, vx);
+    return iris_launch_check("qkv_prep_kernel");
 }
 
 int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
@@ -446,12 +456,11 @@ int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
     if (((uintptr_t)a->qkv | (uintptr_t)a->k_out | (uintptr_t)a->vt_out | (uintptr_t)a->wkA | (uintptr_t)a->wkB |
          (uintptr_t)a->cos_t | (uintptr_t)a->sin_t | (uintptr_t)a->kcos_t | (uintptr_t)a->ksin_t) & 15)
         return iris_set_error("kv_prepare: buffers must be 16-byte aligned");
-    const int kvh = a->kv_heads ? a->kv_heads : a->heads;
-    IRIS_LAUNCH(qk_norm_rope_kernel<true>, dim3((a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE)), dim3(NT), 0,
-                       iris_stream(), *a);
-    if (iris_launch_check("qk_norm_rope_kernel<K>")) return -1;
-    IRIS_LAUNCH(v_transpose_kernel, dim3(a->ld_vt / 64, kvh), dim3(NT), 0, iris_stream(), *a);
-    return iris_launch_check("v_transpose_kernel");
+    const int kvh = a->kv_heads ? a->kv_heads : a->heads, vx = a->ld_vt / 64;
+    const long long blocks = (long long)vx * kvh + (a->rows + NT / IRIS_WAVE - 1) / (NT / IRIS_WAVE);
+    if (blocks >= (1LL << 31)) return iris_set_error("kv_prepare: too many rows");
+    IRIS_LAUNCH(qkv_prep_kernel<true>, dim3((unsigned)blocks), dim3(NT), 0, iris_stream(), *a, vx * kvh, vx);
+    return iris_launch_check("qkv_prep_kernel<K>");
 }
 
 int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias, int N, int K, int act_in) {
