@@ -527,7 +527,6 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
             const int c = tid + NT * i, row = c >> 4, ch = c & 15;
             if (row < nrow) *(uint4 *)(Ob + (size_t)row * a.ld_o + ch * 8) = *(const uint4 *)(smem + row * OSTR + ch * 8);
         }
-        if constexpr ((FEAT & F_SPLIT) != 0) __syncthreads(); /* the block's next segment stages K(0) here */
     } else if (q_row < sq) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll

@@ -728,6 +728,9 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     const int nk = p->K / BK;
     const int kchunk = (nk + splits - 1) / splits * BK;
     const int chunks = (p->K + kchunk - 1) / kchunk;
+    /* K of one step leaves one chunk: that is the plain product (the kernel
+     * applies the epilogue itself and writes no partials to reduce) */
+    if (chunks <= 1) return iris_hip_gemm(p, 1);
     const long long stride = (long long)p->M * p->N;
     if (!ws || ((uintptr_t)ws & 15) || (size_t)chunks * stride * sizeof(float) > ws_bytes)
         return iris_set_error("gemm_splitk: workspace of %zu bytes for %d x %d x %d f32", ws_bytes, chunks, p->M,

@@ -153,10 +153,13 @@ def test_gemm_staged_stores_match_direct(lib, M, N, K, epi, bias):
     assert tl.rel_l2(tl.bf16_to_f32(outs[0]), ref) < 4e-3
 
 
-@pytest.mark.parametrize("M,N,K,splits", [(512, 2560, 4096, 8), (77, 640, 960, 7), (300, 384, 192, 3)])
+@pytest.mark.parametrize("M,N,K,splits", [(512, 2560, 4096, 8), (77, 640, 960, 7), (300, 384, 192, 3),
+                                          (200, 384, 64, 4)])
 def test_gemm_splitk_epilogues(lib, M, N, K, splits):
     """Split-K against the float64 product for every epilogue, and bitwise
-    repeatable (the chunks are summed in a fixed order)."""
+    repeatable (the chunks are summed in a fixed order). K of one step (64)
+    leaves a single chunk: the plain product, whose epilogue must be applied
+    once (no reduce pass over partials) and which needs no workspace."""
     rng = np.random.default_rng(M + N + K)
     A = rng.standard_normal((M, K), np.float32)
     W = rng.standard_normal((N, K), np.float32) * 0.05
@@ -196,7 +199,10 @@ def test_gemm_splitk_epilogues(lib, M, N, K, splits):
         u = np.concatenate([ref[:, c * 64 + 32:c * 64 + 64] for c in range(N // 64)], 1)
         assert tl.rel_l2(tl.bf16_to_f32(osw.get(np.uint16, (M, N // 2))), g / (1 + np.exp(-g)) * u) < 4e-3
     pr = P(dA.ptr, dW.ptr, o.ptr, None, M, N, K, K, K, N, EPI_F32)
-    assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) != 0
+    if K > 64:
+        assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) != 0
+    else:
+        assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) == 0, lib.iris_hip_last_error()
 
 
 @pytest.mark.parametrize("shapes,K", [([(4608, 3072)], 1024), ([(512, 9216), (4096, 9216)], 192),
