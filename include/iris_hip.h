@@ -119,6 +119,14 @@ int iris_hip_gemm(const iris_gemm_problem_t *problems, int n_problems);
  * kernel sums the chunks in order (deterministic) and applies the epilogue. */
 int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *d_workspace, size_t workspace_bytes);
 
+/* No counterpart in the reference. One problem, split-K when its 256x256
+ * tiles fill less than half of the device's CUs and K has at least 8 steps
+ * of 64: up to CUs / tiles chunks of at least 4 steps, as many as the
+ * workspace holds (splits * M * N floats); otherwise the plain launch. For
+ * the products on few rows (a 512-token caption or text stream, a 128-column
+ * final projection) that leave most of the chip idle. */
+int iris_hip_gemm_fill(const iris_gemm_problem_t *problem, float *d_workspace, size_t workspace_bytes);
+
 /* No counterpart in the reference. iris_hip_gemm_splitk without a
  * workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): the

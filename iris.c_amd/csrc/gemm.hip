@@ -36,6 +36,7 @@
  */
 #include "iris_internal.h"
 
+#include <algorithm>
 #include <mutex>
 #include <string.h>
 
@@ -754,6 +755,23 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
                        ws, stride, chunks);
     return iris_launch_check("splitk_reduce_kernel");
+}
+
+extern "C" int iris_hip_gemm_fill(const iris_gemm_problem_t *p, float *ws, size_t ws_bytes) {
+    if (!p) return iris_set_error("gemm_fill: null problem");
+    if (p->M <= 0 || p->N <= 0) return 0;
+    const int cus = iris_cu_count();
+    const long long tiles = (long long)((p->M + BM - 1) / BM) * ((p->N + BN - 1) / BN);
+    const int nk = p->K / BK;
+    /* tiles filling less than half of the CUs and a long K: split K into up to
+     * CUs / tiles chunks of at least 4 K steps, as many as the workspace holds */
+    if (p->K2 == 0 && cus > 0 && ws && 2 * tiles <= cus && nk >= 8) {
+        int splits = (int)std::min<long long>(cus / tiles, nk / 4);
+        const size_t per = (size_t)p->M * (size_t)p->N * sizeof(float);
+        while (splits > 1 && (size_t)splits * per > ws_bytes) splits--;
+        if (splits > 1) return iris_hip_gemm_splitk(p, splits, ws, ws_bytes);
+    }
+    return iris_hip_gemm(p, 1);
 }
 
 extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {

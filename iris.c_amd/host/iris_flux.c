@@ -69,6 +69,10 @@ typedef struct {
     float *nq, *nk;
 } dev_single_t;
 
+/* split-K partials of one product on few rows (iris_hip_gemm_fill picks the
+ * chunk count that fits) */
+#define FILL_WS_BYTES ((size_t)64 << 20)
+
 typedef struct {
     int valid;
     int ih, iw, n_refs, T, B;
@@ -102,6 +106,7 @@ typedef struct {
                               * it into pinned slots before iris_hip_memcpy_h2d returns) */
     void *attn_ws;           /* the attention's balanced-schedule workspace (zeroed) */
     size_t attn_ws_bytes;
+    float *fill_ws;          /* split-K partials of the products on few rows (iris_hip_gemm_fill) */
     void *graph;
 } work_t;
 
@@ -448,7 +453,7 @@ static void work_free(work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
                     w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp,
-                    w->temb, w->mod, w->attn_ws};
+                    w->temb, w->mod, w->attn_ws, w->fill_ws};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -572,6 +577,7 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
     DA(w->mod, (size_t)17 * h * 4);
     w->attn_ws_bytes = iris_hip_attention_workspace_bytes();
     DA(w->attn_ws, w->attn_ws_bytes);
+    DA(w->fill_ws, FILL_WS_BYTES);
     if (iris_hip_memset(w->attn_ws, 0, w->attn_ws_bytes) || iris_hip_sync()) goto fail;
 #undef DA
     w->tsin_host = (float *)malloc(256 * sizeof(float));
@@ -611,6 +617,11 @@ fail:
 #define CK(x) do { if ((x) != 0) return -1; } while (0)
 
 static int gemm(const iris_gemm_problem_t *p, int n) { return iris_hip_gemm(p, n); }
+/* one product on few rows: split-K through the forward's workspace when its
+ * tiles leave most of the chip idle */
+static int gemm_fill(iris_transformer_t *tf, const iris_gemm_problem_t *p) {
+    return iris_hip_gemm_fill(p, tf->w.fill_ws, FILL_WS_BYTES);
+}
 
 static iris_gemm_problem_t prob(const void *A, int lda, const uint16_t *W, int ldw, void *out, int ldo,
                                 const float *vec, int M, int N, int K, int epi) {
@@ -815,21 +826,24 @@ static int enqueue_forward(iris_transformer_t *tf) {
         off += rs;
     }
     CK(iris_hip_f32_to_bf16(w->txtb, w->txtf, (size_t)B * T * td));
-    /* img_in / txt_in into the residual stream rows [T, S) and [0, T) (:4022-4031) */
+    /* img_in / txt_in into the residual stream rows [T, S) and [0, T) (:4022-4031):
+     * the image rows (K = latent channels) in one launch, then each text
+     * stream (K = text_dim, few rows) split over K */
     iris_gemm_problem_t p[4];
     int n = 0;
-    for (int b = 0; b < B; b++) {
-        size_t r0 = (size_t)b * S;
-        p[n++] = prob(w->txtb + (size_t)b * T * td, td, tf->txt_in, td, w->x + r0 * h, h, NULL, T, h, td, IRIS_EPI_F32);
-        p[n++] = prob(w->tok, C, tf->img_in, C, w->x + (r0 + T) * h, h, NULL, w->I, h, C, IRIS_EPI_F32);
-    }
+    for (int b = 0; b < B; b++)
+        p[n++] = prob(w->tok, C, tf->img_in, C, w->x + ((size_t)b * S + T) * h, h, NULL, w->I, h, C, IRIS_EPI_F32);
     CK(gemm(p, n));
+    for (int b = 0; b < B; b++) {
+        p[0] = prob(w->txtb + (size_t)b * T * td, td, tf->txt_in, td, w->x + (size_t)b * S * h, h, NULL, T, h, td,
+                    IRIS_EPI_F32);
+        CK(gemm_fill(tf, p));
+    }
     for (int i = 0; i < tf->n_double; i++) CK(double_block_forward(tf, i));
     for (int i = 0; i < tf->n_single; i++) CK(single_block_forward(tf, i));
     /* final layer on the target rows: AdaLN with (scale, shift) order, proj_out,
      * written transposed to NCHW (:4254-4301) */
     const float *fm = w->mod + 15 * h;
-    n = 0;
     for (int b = 0; b < B; b++) {
         iris_norm_args_t a;
         memset(&a, 0, sizeof(a));
@@ -838,10 +852,10 @@ static int enqueue_forward(iris_transformer_t *tf) {
         a.rows = I0; a.cols = h; a.mode = IRIS_NORM_LN_MOD; a.eps = 1e-6f;
         a.split = I0; a.shiftA = fm + h; a.scaleA = fm;
         CK(iris_hip_rownorm(&a));
-        p[n++] = prob(w->a + (size_t)b * I0 * h, h, tf->proj_out, h, w->vel + (size_t)b * C * I0, I0, NULL, I0, C, h,
-                      IRIS_EPI_F32_T);
+        p[0] = prob(w->a + (size_t)b * I0 * h, h, tf->proj_out, h, w->vel + (size_t)b * C * I0, I0, NULL, I0, C, h,
+                    IRIS_EPI_F32_T);
+        CK(gemm_fill(tf, p));
     }
-    CK(gemm(p, n));
     return 0;
 }
 

@@ -38,6 +38,10 @@ typedef struct {
     float *nq, *nk, *n1, *n2, *fn1, *fn2, *ada_b;
 } zi_dev_block_t;
 
+/* split-K partials of one product on few rows (iris_hip_gemm_fill picks the
+ * chunk count that fits) */
+#define ZI_FILL_WS_BYTES ((size_t)64 << 20)
+
 typedef struct {
     int valid, lh, lw, cap_len;
     int I, Ip, Cp, U, U_pad;
@@ -47,6 +51,7 @@ typedef struct {
     float *tsin_host;
     void *attn_ws;                /* the attention's balanced-schedule workspace (zeroed) */
     size_t attn_ws_bytes;
+    float *fill_ws;               /* split-K partials of the products on few rows (iris_hip_gemm_fill) */
     void *graph;
 } zi_work_t;
 
@@ -342,7 +347,7 @@ zi_transformer_t *zi_transformer_create_synthetic(int dim, int n_heads, int n_la
 static void zwork_free(zi_work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *p[] = {w->x, w->y, w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->tsin, w->tmp, w->temb, w->mods, w->fscale, w->lat, w->vel,
-                 w->capf, w->fout, w->a, w->qkv, w->q, w->k, w->vt, w->attn, w->ffn, w->patches, w->attn_ws};
+                 w->capf, w->fout, w->a, w->qkv, w->q, w->k, w->vt, w->attn, w->ffn, w->patches, w->attn_ws, w->fill_ws};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
@@ -392,6 +397,7 @@ int zi_prepare(zi_transformer_t *tf, int lh, int lw, int cap_len) {
     DA(w->attn, U * d * 2);
     DA(w->ffn, U * tf->ffn * 2);
     DA(w->patches, (size_t)w->I * pf * 2);
+    DA(w->fill_ws, ZI_FILL_WS_BYTES);
     w->attn_ws_bytes = iris_hip_attention_workspace_bytes();
     DA(w->attn_ws, w->attn_ws_bytes);
     if (iris_hip_memset(w->attn_ws, 0, w->attn_ws_bytes) || iris_hip_sync()) goto fail;
@@ -445,6 +451,13 @@ static iris_gemm_problem_t zprob(const void *A, int lda, const uint16_t *W, void
     return p;
 }
 
+/* one product: split over K through the forward's workspace when its tiles
+ * leave most of the chip idle (the context refiner's 512 caption rows, the
+ * caption embedder, the final projection), else the plain launch */
+static int zgemm(zi_transformer_t *tf, const iris_gemm_problem_t *p) {
+    return iris_hip_gemm_fill(p, tf->w.fill_ws, ZI_FILL_WS_BYTES);
+}
+
 static int rms(zi_transformer_t *tf, const float *x, uint16_t *out, int rows, const float *w, const float *scale) {
     iris_norm_args_t a;
     memset(&a, 0, sizeof(a));
@@ -466,7 +479,7 @@ static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const
     /* attention: h = attention(norm1(x) * (1 + scale_msa)) */
     CK(rms(tf, x, w->a, n, b->n1, mod));
     iris_gemm_problem_t p = zprob(w->a, d, b->qkv, w->qkv, 3 * d, NULL, n, 3 * d, d, IRIS_EPI_BF16);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     iris_qkprep_args_t q;
     memset(&q, 0, sizeof(q));
     q.qkv = w->qkv; q.ld_qkv = 3 * d; q.col_k = d; q.col_v = 2 * d;
@@ -489,15 +502,15 @@ static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const
     at.ws = w->attn_ws; at.ws_bytes = w->attn_ws_bytes;
     CK(iris_hip_attention(&at));
     p = zprob(w->attn, d, b->o, w->y, d, NULL, n, d, d, IRIS_EPI_F32);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     /* x += tanh(gate_msa) * norm2(attn_out) */
     CK(iris_hip_rms_gated_add(x, w->y, b->n2, mod ? mod + d : NULL, n, d, ZI_EPS, 1));
     /* FFN: x += tanh(gate_mlp) * norm2(w2(silu(w1 h) * w3 h)), h = norm1(x) * (1 + scale_mlp) */
     CK(rms(tf, x, w->a, n, b->fn1, mod ? mod + 2 * d : NULL));
     p = zprob(w->a, d, b->w13, w->ffn, f, NULL, n, 2 * f, d, IRIS_EPI_SWIGLU);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     p = zprob(w->ffn, f, b->w2, w->y, d, NULL, n, d, f, IRIS_EPI_F32);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     CK(iris_hip_rms_gated_add(x, w->y, b->fn2, mod ? mod + 3 * d : NULL, n, d, ZI_EPS, 1));
     return 0;
 }
@@ -520,7 +533,7 @@ static int zi_enqueue(zi_transformer_t *tf) {
     /* patchify (ph, pw, c) and embed image rows [0, I); padding rows get x_pad_token */
     CK(iris_hip_patchify(w->patches, w->lat, tf->in_ch, w->lh, w->lw, tf->ps));
     iris_gemm_problem_t p = zprob(w->patches, pf, tf->x_w, w->x, d, tf->x_b, I, d, pf, IRIS_EPI_F32);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     CK(iris_hip_fill_rows(w->x, tf->x_pad, I, Ip, d));
     /* caption: RMSNorm * w then linear + b into rows [Ip, Ip + cap_len); padding rows get cap_pad_token */
     iris_norm_args_t a;
@@ -531,7 +544,7 @@ static int zi_enqueue(zi_transformer_t *tf) {
     CK(iris_hip_rownorm(&a));
     p = zprob(w->a, tf->cap_dim, tf->cap_w, w->x + (size_t)Ip * d, d, tf->cap_b, w->cap_len, d, tf->cap_dim,
               IRIS_EPI_F32);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     CK(iris_hip_fill_rows(w->x, tf->cap_pad, Ip + w->cap_len, U, d));
     /* refiners: noise refiner on image rows, context refiner on caption rows */
     for (int i = 0; i < tf->refiners; i++)
@@ -549,7 +562,7 @@ static int zi_enqueue(zi_transformer_t *tf) {
     a.split = I; a.scaleA = w->fscale;
     CK(iris_hip_rownorm(&a));
     p = zprob(w->a, d, tf->f_lin_w, w->fout, pf, tf->f_lin_b, I, pf, d, IRIS_EPI_F32);
-    CK(iris_hip_gemm(&p, 1));
+    CK(zgemm(tf, &p));
     CK(iris_hip_unpatchify(w->vel, w->fout, tf->in_ch, w->lh, w->lw, tf->ps));
     return 0;
 }

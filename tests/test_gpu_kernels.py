@@ -205,6 +205,48 @@ def test_gemm_splitk_epilogues(lib, M, N, K, splits):
         assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, 4) == 0, lib.iris_hip_last_error()
 
 
+@pytest.mark.parametrize("M,N,K,epi,ws_mb", [(512, 3072, 7680, EPI_F32, 64), (4096, 128, 3072, EPI_F32_T, 64),
+                                              (300, 640, 2560, EPI_GATED_ADD, 64), (4608, 3072, 512, EPI_F32, 64),
+                                              (512, 3072, 7680, EPI_F32, 1)])
+def test_gemm_fill(lib, M, N, K, epi, ws_mb):
+    """iris_hip_gemm_fill: a product on few tiles with a long K is split over K
+    (the text embedder's 512 x 3072 x 7680, the final projection's
+    4096 x 128 x 3072 transposed store, a gated residual add on ragged tiles)
+    and matches float64 and repeats bit for bit; many tiles (4608 x 3072) and
+    a workspace too small for two chunks (1 MB) take the plain launch, equal
+    to iris_hip_gemm bit for bit."""
+    rng = np.random.default_rng(M + N + K)
+    a = bf(rng.standard_normal((M, K), np.float32))
+    w = bf(rng.standard_normal((N, K), np.float32) * 0.03)
+    vec = rng.standard_normal(N).astype(np.float32)
+    x0 = rng.standard_normal((M, N), np.float32)
+    A, W, V = tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w)), tl.Dev.of(vec)
+    ws_bytes = ws_mb << 20
+    ws = tl.Dev(ws_bytes)
+    lib.iris_hip_gemm_fill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    shape = (N, M) if epi == EPI_F32_T else (M, N)
+    ldo = M if epi == EPI_F32_T else N
+    outs = []
+    for fill in (True, True, False):
+        o = tl.Dev.of(x0) if epi == EPI_GATED_ADD else tl.Dev(M * N * 4)
+        pr = tl.GemmProblem(A.ptr, W.ptr, o.ptr, V.ptr if epi == EPI_GATED_ADD else None, M, N, K, K, K, ldo, epi)
+        if fill:
+            assert lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+        else:
+            run_gemm(lib, [pr])
+        assert lib.iris_hip_sync() == 0
+        outs.append(o.get(np.float32, shape))
+        o.close()
+    assert np.array_equal(outs[0], outs[1]), "not repeatable"
+    y = a.astype(np.float64) @ w.astype(np.float64).T
+    ref = x0 + vec * y if epi == EPI_GATED_ADD else (y.T if epi == EPI_F32_T else y)
+    assert tl.rel_l2(outs[0], ref) < 1e-5
+    split = 2 * ((M + 255) // 256) * ((N + 255) // 256) <= 256 and K >= 512 and ws_bytes >= 2 * M * N * 4
+    if not split:
+        assert np.array_equal(outs[0], outs[2]), "plain launch expected"
+    print(f"fill {'split-K' if split else 'plain'}: rel_l2 {tl.rel_l2(outs[0], ref):.2e}")
+
+
 @pytest.mark.parametrize("shapes,K", [([(4608, 3072)], 1024), ([(512, 9216), (4096, 9216)], 192),
                                       ([(4608, 3840)], 320), ([(700, 3000)], 128)])
 def test_gemm_narrow_tiles(lib, shapes, K):
