@@ -257,27 +257,53 @@ __global__ __launch_bounds__(NT) void qkv_prep_kernel(const iris_qkprep_args_t a
     else qk_norm_rope_rows<KONLY>(a, b - vblocks);
 }
 
-/* one wave per output row */
+/* y[n] = W[n, :] . act(x) + bias[n]. One wave per row, or for K <= 256 half
+ * a wave per row (lanes 32..63 take the next row); each lane takes 8
+ * consecutive elements of every 512- (256-) wide chunk, and up to four
+ * chunks' loads are issued before their products. */
 __global__ __launch_bounds__(NT) void gemv_kernel(float *y, const uint16_t *W, const float *x, const float *bias,
                                                   int N, int K, int act_in) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n = blockIdx.x * (NT / IRIS_WAVE) + wave;
-    if (n >= N) return;
-    const uint16_t *w = W + (size_t)n * K;
+    const bool half = K <= 256;
+    const int gw = blockIdx.x * (NT / IRIS_WAVE) + wave;
+    const int n = half ? 2 * gw + (lane >> 5) : gw;
+    const int l = half ? lane & 31 : lane, step = half ? 256 : 512;
     float acc = 0.0f;
-    for (int k = lane * 8; k < K; k += 64 * 8) {
-        const u16x8 wv = *(const u16x8 *)(w + k);
-        const float4 xa = *(const float4 *)(x + k), xb = *(const float4 *)(x + k + 4);
-        float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    if (n < N) {
+        const uint16_t *w = W + (size_t)n * K;
+        for (int k0 = l * 8; k0 < K; k0 += 4 * step) {
+            u16x8 wv[4];
+            float4 xa[4], xb[4];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float xv = xs[e];
-            if (act_in == 1) xv = xv / (1.0f + __expf(-xv));
-            acc += bf2f(wv[e]) * xv;
+            for (int u = 0; u < 4; u++) {
+                const int k = k0 + u * step;
+                wv[u] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+                xa[u] = xb[u] = make_float4(0, 0, 0, 0);
+                if (k < K) {
+                    wv[u] = *(const u16x8 *)(w + k);
+                    xa[u] = *(const float4 *)(x + k);
+                    xb[u] = *(const float4 *)(x + k + 4);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float xs[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    float xv = xs[e];
+                    if (act_in == 1) xv = xv / (1.0f + __expf(-xv));
+                    acc += bf2f(wv[u][e]) * xv;
+                }
+            }
         }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) y[n] = acc + (bias ? bias[n] : 0.0f);
+    if (half) {
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    } else {
+        acc = wave_sum(acc);
+    }
+    if (n < N && l == 0) y[n] = acc + (bias ? bias[n] : 0.0f);
 }
 
 __global__ void nchw_to_tokens_kernel(uint16_t *out, const float *lat, int C, int hw) {
@@ -466,7 +492,9 @@ int iris_hip_kv_prepare(const iris_qkprep_args_t *a) {
 int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias, int N, int K, int act_in) {
     if (N <= 0) return 0;
     if (K % 8) return iris_set_error("gemv: K=%d must be a multiple of 8", K);
-    IRIS_LAUNCH(gemv_kernel, dim3((N + 3) / 4), dim3(NT), 0, iris_stream(), y, W, x, bias, N, K, act_in);
+    const int rows_per_block = (K <= 256 ? 2 : 1) * (NT / IRIS_WAVE);
+    IRIS_LAUNCH(gemv_kernel, dim3((N + rows_per_block - 1) / rows_per_block), dim3(NT), 0, iris_stream(), y, W, x,
+                bias, N, K, act_in);
     return iris_launch_check("gemv_kernel");
 }
 

@@ -62,6 +62,11 @@ struct zi_transformer {
     uint16_t *t0_w, *t2_w, *cap_w, *x_w, *f_ada_w, *f_lin_w;
     float *t0_b, *t2_b, *cap_norm, *cap_b, *x_b, *x_pad, *cap_pad, *f_ada_b1, *f_lin_b;
     zi_dev_block_t *nr, *cr, *ly;
+    /* the modulated blocks' adaLN weights [refiners + layers][4 dim][adaln_dim]
+     * and biases, noise refiners first: one GEMV yields every block's
+     * modulation (the blocks' ada_w / ada_b point into them) */
+    uint16_t *ada_all_w;
+    float *ada_all_b;
     zi_work_t w;
 };
 
@@ -147,7 +152,8 @@ static uint16_t *up_bf16(zsrc_t *s, const char *name, size_t rows, size_t cols) 
     return d;
 }
 
-static int load_block(zi_transformer_t *tf, zsrc_t *s, zi_dev_block_t *b, const char *pre, int mod) {
+/* slot: the block's row in ada_all_w / ada_all_b, or -1 (unmodulated) */
+static int load_block(zi_transformer_t *tf, zsrc_t *s, zi_dev_block_t *b, const char *pre, int slot) {
     size_t d = tf->dim, f = tf->ffn;
     char nm[256];
     b->qkv = (uint16_t *)iris_hip_malloc(3 * d * d * 2);
@@ -184,9 +190,10 @@ static int load_block(zi_transformer_t *tf, zsrc_t *s, zi_dev_block_t *b, const 
     NORM(b->fn1, "ffn_norm1.weight", d);
     NORM(b->fn2, "ffn_norm2.weight", d);
 #undef NORM
-    if (mod) {
+    if (slot >= 0) {
         snprintf(nm, sizeof(nm), "%s.adaLN_modulation.0.weight", pre);
-        if (!(b->ada_w = up_bf16(s, nm, 4 * d, tf->adaln_dim))) return -1;
+        b->ada_w = tf->ada_all_w + (size_t)slot * 4 * d * tf->adaln_dim;
+        if (up_rows(s, nm, b->ada_w, 4 * d, tf->adaln_dim)) return -1;
         /* bias with 1 folded into the two scale segments: the GEMV then yields
          * 1 + scale_msa and 1 + scale_mlp directly (:809-816) */
         snprintf(nm, sizeof(nm), "%s.adaLN_modulation.0.bias", pre);
@@ -195,8 +202,8 @@ static int load_block(zi_transformer_t *tf, zsrc_t *s, zi_dev_block_t *b, const 
         float *t = (float *)malloc(4 * d * 4);
         if (!t) return -1;
         for (size_t i = 0; i < 4 * d; i++) t[i] = h[i] + ((i < d || (i >= 2 * d && i < 3 * d)) ? 1.0f : 0.0f);
-        b->ada_b = (float *)iris_hip_malloc(4 * d * 4);
-        int rc = !b->ada_b || iris_hip_memcpy_h2d(b->ada_b, t, 4 * d * 4) || iris_hip_sync();
+        b->ada_b = tf->ada_all_b + (size_t)slot * 4 * d;
+        int rc = iris_hip_memcpy_h2d(b->ada_b, t, 4 * d * 4) || iris_hip_sync();
         free(t);
         if (rc) return -1;
     }
@@ -204,7 +211,7 @@ static int load_block(zi_transformer_t *tf, zsrc_t *s, zi_dev_block_t *b, const 
 }
 
 static void free_block(zi_dev_block_t *b) {
-    void *p[] = {b->qkv, b->o, b->w13, b->w2, b->ada_w, b->nq, b->nk, b->n1, b->n2, b->fn1, b->fn2, b->ada_b};
+    void *p[] = {b->qkv, b->o, b->w13, b->w2, b->nq, b->nk, b->n1, b->n2, b->fn1, b->fn2};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
 }
 
@@ -214,7 +221,7 @@ void zi_transformer_free(zi_transformer_t *tf) {
     if (!tf) return;
     zwork_free(&tf->w);
     void *p[] = {tf->t0_w, tf->t2_w, tf->cap_w, tf->x_w, tf->f_ada_w, tf->f_lin_w, tf->t0_b, tf->t2_b, tf->cap_norm,
-                 tf->cap_b, tf->x_b, tf->x_pad, tf->cap_pad, tf->f_ada_b1, tf->f_lin_b};
+                 tf->cap_b, tf->x_b, tf->x_pad, tf->cap_pad, tf->f_ada_b1, tf->f_lin_b, tf->ada_all_w, tf->ada_all_b};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
     for (int i = 0; tf->nr && i < tf->refiners; i++) free_block(&tf->nr[i]);
     for (int i = 0; tf->cr && i < tf->refiners; i++) free_block(&tf->cr[i]);
@@ -244,15 +251,19 @@ static int load_all(zi_transformer_t *tf, zsrc_t *s) {
     tf->cr = (zi_dev_block_t *)calloc((size_t)tf->refiners, sizeof(zi_dev_block_t));
     tf->ly = (zi_dev_block_t *)calloc((size_t)tf->layers, sizeof(zi_dev_block_t));
     if (!tf->nr || !tf->cr || !tf->ly) return -1;
+    const size_t nmod = (size_t)tf->refiners + tf->layers;
+    tf->ada_all_w = (uint16_t *)iris_hip_malloc(nmod * 4 * d * ad * 2);
+    tf->ada_all_b = (float *)iris_hip_malloc(nmod * 4 * d * 4);
+    if (!tf->ada_all_w || !tf->ada_all_b) return -1;
     for (int i = 0; i < tf->refiners; i++) {
         snprintf(nm, sizeof(nm), "noise_refiner.%d", i);
-        if (load_block(tf, s, &tf->nr[i], nm, 1)) return -1;
+        if (load_block(tf, s, &tf->nr[i], nm, i)) return -1;
         snprintf(nm, sizeof(nm), "context_refiner.%d", i);
-        if (load_block(tf, s, &tf->cr[i], nm, 0)) return -1;
+        if (load_block(tf, s, &tf->cr[i], nm, -1)) return -1;
     }
     for (int i = 0; i < tf->layers; i++) {
         snprintf(nm, sizeof(nm), "layers.%d", i);
-        if (load_block(tf, s, &tf->ly[i], nm, 1)) return -1;
+        if (load_block(tf, s, &tf->ly[i], nm, tf->refiners + i)) return -1;
     }
     snprintf(nm, sizeof(nm), "all_final_layer.%d-1.adaLN_modulation.1.weight", tf->ps);
     if (!(tf->f_ada_w = up_bf16(s, nm, d, ad))) return -1;
@@ -521,14 +532,11 @@ static int zi_enqueue(zi_transformer_t *tf) {
     /* timestep MLP with biases (:561-584) */
     CK(iris_hip_gemv(w->tmp, tf->t0_w, w->tsin, tf->t0_b, tf->t_mid, 256, 0));
     CK(iris_hip_gemv(w->temb, tf->t2_w, w->tmp, tf->t2_b, tf->adaln_dim, tf->t_mid, 1));
-    /* per-block modulation W t_emb + b, no SiLU (:806-807); final scale
+    /* per-block modulation W t_emb + b, no SiLU (:806-807), for every
+     * modulated block in one GEMV over their stacked weights; final scale
      * 1 + W SiLU(t_emb) + b (:1563-1574) */
-    for (int i = 0; i < tf->refiners; i++)
-        CK(iris_hip_gemv(w->mods + (size_t)i * 4 * d, tf->nr[i].ada_w, w->temb, tf->nr[i].ada_b, 4 * d,
-                         tf->adaln_dim, 0));
-    for (int i = 0; i < tf->layers; i++)
-        CK(iris_hip_gemv(w->mods + (size_t)(tf->refiners + i) * 4 * d, tf->ly[i].ada_w, w->temb, tf->ly[i].ada_b,
-                         4 * d, tf->adaln_dim, 0));
+    CK(iris_hip_gemv(w->mods, tf->ada_all_w, w->temb, tf->ada_all_b, (tf->refiners + tf->layers) * 4 * d,
+                     tf->adaln_dim, 0));
     CK(iris_hip_gemv(w->fscale, tf->f_ada_w, w->temb, tf->f_ada_b1, d, tf->adaln_dim, 1));
     /* patchify (ph, pw, c) and embed image rows [0, I); padding rows get x_pad_token */
     CK(iris_hip_patchify(w->patches, w->lat, tf->in_ch, w->lh, w->lw, tf->ps));

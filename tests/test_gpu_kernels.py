@@ -782,7 +782,8 @@ def test_flash_attention_fused_q(lib, S, H, batch, split, rope, causal, group):
             assert tl.rel_l2(got[b, :, h * 128:(h + 1) * 128], ref) < 1e-2, (b, h)
 
 
-@pytest.mark.parametrize("N,K,act", [(18432, 3072, 1), (3072, 256, 0), (100, 3840, 1)])
+@pytest.mark.parametrize("N,K,act", [(18432, 3072, 1), (3072, 256, 0), (100, 3840, 1), (1001, 128, 0), (7, 264, 1),
+                                     (33, 8, 0), (61440, 256, 0)])
 def test_gemv(lib, N, K, act):
     rng = np.random.default_rng(N)
     W = rng.standard_normal((N, K), np.float32) * 0.02
