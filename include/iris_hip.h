@@ -289,8 +289,8 @@ typedef struct {
     float qn_eps;
     const float *rope_cos, *rope_sin;
     /* Optional workspace (NULL: one block per 256 queries of a head). When
-     * those blocks would fill the rounds of blocks (one per compute unit)
-     * less than 80 % on average and causal is 0, the key tiles of all
+     * those blocks need two or more rounds of blocks (one per compute unit)
+     * that are on average less than 80 % full and causal is 0, the key tiles of all
      * (query block, head) units are dealt out in equal ranges, one per
      * compute unit, and the partial softmax states of a unit done by several
      * blocks are merged by the last of them (deterministic order). At least
@@ -299,6 +299,16 @@ typedef struct {
      * must not overlap. */
     void *ws;
     size_t ws_bytes;
+    /* Factored RoPE for the Q prologue, used instead of rope_cos / rope_sin
+     * when rope_pos is set: pair i of a head belongs to axis i / 16 (four
+     * axes of 16 pairs with one frequency table, as Flux's), query q sits at
+     * position rope_pos[4 q + i / 16] on it, and the pair's cos and sin are
+     * rope_axis[16 p + i % 16] and rope_axis[16 (rope_axis_len + p) + i % 16]
+     * for that position p (0 <= p < rope_axis_len). The same values as the
+     * per-query tables, from 8 bytes per query instead of 512. */
+    const int16_t *rope_pos;
+    const float *rope_axis;
+    int rope_axis_len;
 } iris_attn_args_t;
 size_t iris_hip_attention_workspace_bytes(void);
 int iris_hip_attention(const iris_attn_args_t *a);

@@ -234,10 +234,27 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
             if (row < sq) raw[pass] = *(const u16x8 *)(Q + (size_t)row * a.ld_q + d0);
             c4[pass] = make_float4(1, 1, 1, 1);
             s4[pass] = make_float4(0, 0, 0, 0);
-            if (a.rope_cos) {
+            if (!a.rope_pos && a.rope_cos) {
                 const size_t tr = (size_t)(row < sq ? row : 0) * (HD / 2) + hl * 4;
                 c4[pass] = *(const float4 *)(a.rope_cos + tr);
                 s4[pass] = *(const float4 *)(a.rope_sin + tr);
+            }
+        }
+        if (a.rope_pos) {
+            /* factored tables: the lane's 4 pairs hl*4 .. +3 lie on axis hl / 4
+             * at entries (hl % 4) * 4 .. +3 of the shared frequency table */
+            int pos[8];
+#pragma unroll
+            for (int pass = 0; pass < 8; pass++) {
+                const int row = wave_q0 + pass * 4 + rl;
+                pos[pass] = a.rope_pos[(size_t)(row < sq ? row : 0) * 4 + (hl >> 2)];
+                pos[pass] = min(max(pos[pass], 0), a.rope_axis_len - 1);
+            }
+            const float *tc = a.rope_axis + (hl & 3) * 4, *ts = tc + (size_t)a.rope_axis_len * 16;
+#pragma unroll
+            for (int pass = 0; pass < 8; pass++) {
+                c4[pass] = *(const float4 *)(tc + pos[pass] * 16);
+                s4[pass] = *(const float4 *)(ts + pos[pass] * 16);
             }
         }
     }
@@ -602,6 +619,10 @@ extern "C" int iris_hip_attention(const iris_attn_args_t *a) {
     if (fuseq && (!a->qn_wB || ((uintptr_t)a->qn_wA | (uintptr_t)a->qn_wB | (uintptr_t)a->rope_cos |
                                 (uintptr_t)a->rope_sin) & 15 || (a->rope_cos && !a->rope_sin)))
         return iris_set_error("attention: Q prologue needs both norm weight sets and 16-byte aligned tables");
+    if (a->rope_pos && (!fuseq || !a->rope_axis || ((uintptr_t)a->rope_axis & 15) || a->rope_axis_len <= 0 ||
+                        a->rope_axis_len > (1 << 15)))
+        return iris_set_error("attention: factored RoPE needs the Q prologue, a 16-byte aligned table and "
+                              "1 .. 32768 positions");
     const int nqb = (a->sq + QB - 1) / QB;
     const long long total = (long long)nqb * a->heads * a->batch;
     if (total > (1LL << 28)) return iris_set_error("attention: grid too large");

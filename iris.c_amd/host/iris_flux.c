@@ -93,6 +93,11 @@ typedef struct {
     float *vel;              /* [B][C][I0] */
     float *rope_cos, *rope_sin;   /* [S][128] */
     float *rp_cos, *rp_sin;       /* [S][64]: one value per rotation pair (the attention's Q prologue) */
+    int16_t *rp_pos;              /* [S][4] axis positions (T, H, W, L) of each row, with rp_axis the
+                                   * factored form of rp_cos / rp_sin the Q prologue reads (NULL when
+                                   * it would not reproduce them bit for bit) */
+    float *rp_axis;               /* cos [rp_axis_len][16], then sin */
+    int rp_axis_len;
     float *krope_cos, *krope_sin; /* [S][128] K side: the reference rows' H/W bands scaled (SREF) */
     float kshf, kslf;             /* band scales the K tables hold */
     float kgamma;                 /* SREF strength the captured graph applies */
@@ -452,11 +457,65 @@ int iris_transformer_text_dim(iris_transformer_t *tf) { return tf->text_dim; }
 static void work_free(work_t *w) {
     iris_hip_graph_destroy(w->graph);
     void *bufs[] = {w->x, w->a, w->qkv, w->q, w->k, w->vt, w->cat, w->tok, w->txtb, w->txtf, w->lat, w->vel,
-                    w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->krope_cos, w->krope_sin, w->tsin, w->tmp,
+                    w->rope_cos, w->rope_sin, w->rp_cos, w->rp_sin, w->rp_pos, w->rp_axis, w->krope_cos, w->krope_sin,
+                    w->tsin, w->tmp,
                     w->temb, w->mod, w->attn_ws, w->fill_ws};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) iris_hip_free(bufs[i]);
     free(w->tsin_host);
     memset(w, 0, sizeof(*w));
+}
+
+/* The Q prologue's pair tables in factored form: every row's axis positions
+ * (text row t: (0, 0, 0, t); image row (y, x) of a latent with T-offset o:
+ * (o, y, x, 0), iris_transformer_flux.c:896-1087) and one table of the four
+ * axes' shared frequencies per position. Kept only when it reproduces the
+ * [S][64] tables bit for bit (pc, ps); otherwise the prologue reads those. */
+static int factored_rope(work_t *w, const float *pc, const float *ps, int T, int ih, int iw, const iris_ref_t *refs,
+                         int n_refs, int axis_dim, float theta) {
+    if (axis_dim != 32) return 0;   /* four axes of 16 pairs */
+    const size_t S = w->S;
+    int len = T > ih ? T : ih;
+    if (iw > len) len = iw;
+    for (int r = 0; r < n_refs; r++) {
+        if (refs[r].t_offset < 0) return 0;
+        if (refs[r].h > len) len = refs[r].h;
+        if (refs[r].w > len) len = refs[r].w;
+        if (refs[r].t_offset + 1 > len) len = refs[r].t_offset + 1;
+    }
+    if (len > (1 << 15)) return 0;
+    int16_t *pos = (int16_t *)calloc(S * 4, sizeof(int16_t));
+    float *tab = (float *)malloc((size_t)len * 32 * sizeof(float));
+    if (!pos || !tab) { free(pos); free(tab); return -1; }
+    size_t row = 0;
+    for (int t = 0; t < T; t++, row++) pos[row * 4 + 3] = (int16_t)t;
+    for (int r = -1; r < n_refs; r++) {
+        const int hh = r < 0 ? ih : refs[r].h, ww = r < 0 ? iw : refs[r].w, to = r < 0 ? 0 : refs[r].t_offset;
+        for (int y = 0; y < hh; y++)
+            for (int x = 0; x < ww; x++, row++) {
+                pos[row * 4] = (int16_t)to;
+                pos[row * 4 + 1] = (int16_t)y;
+                pos[row * 4 + 2] = (int16_t)x;
+            }
+    }
+    iris_rope_axis(tab, tab + (size_t)len * 16, len, axis_dim, theta);
+    int same = row == S;
+    for (size_t q = 0; same && q < S; q++)
+        for (int i = 0; i < 64 && same; i++) {
+            const int p = pos[q * 4 + i / 16];
+            same = !memcmp(&pc[q * 64 + i], &tab[p * 16 + i % 16], 4) &&
+                   !memcmp(&ps[q * 64 + i], &tab[((size_t)len + p) * 16 + i % 16], 4);
+        }
+    int rc = 0;
+    if (same) {
+        w->rp_pos = (int16_t *)iris_hip_malloc(S * 4 * sizeof(int16_t));
+        w->rp_axis = (float *)iris_hip_malloc((size_t)len * 32 * sizeof(float));
+        w->rp_axis_len = len;
+        rc = !w->rp_pos || !w->rp_axis || iris_hip_memcpy_h2d(w->rp_pos, pos, S * 4 * sizeof(int16_t)) ||
+             iris_hip_memcpy_h2d(w->rp_axis, tab, (size_t)len * 32 * sizeof(float)) || iris_hip_sync();
+    }
+    free(pos);
+    free(tab);
+    return rc ? -1 : 0;
 }
 
 static int same_geometry(const work_t *w, int ih, int iw, const iris_ref_t *refs, int n, int T, int B) {
@@ -597,6 +656,7 @@ int iris_flux_prepare(iris_transformer_t *tf, int ih, int iw, const iris_ref_t *
         float *pc = (float *)malloc(S * 64 * sizeof(float)), *ps = (float *)malloc(S * 64 * sizeof(float));
         int rc = !pc || !ps;
         if (!rc) iris_rope_pairs(pc, ps, c, s, S);
+        if (!rc) rc = factored_rope(w, pc, ps, T, ih, iw, refs, n_refs, tf->axis_dim, tf->theta);
         rc = rc || iris_hip_memcpy_h2d(w->rope_cos, c, S * 128 * 4) || iris_hip_memcpy_h2d(w->rope_sin, s, S * 128 * 4) ||
              iris_hip_memcpy_h2d(w->rp_cos, pc, S * 64 * 4) || iris_hip_memcpy_h2d(w->rp_sin, ps, S * 64 * 4) ||
              iris_hip_sync() || fill_ktables(tf, c, s);
@@ -675,6 +735,7 @@ static int attention(iris_transformer_t *tf, const float *wqA, const float *wqB,
     a.kv_lo0 = 0; a.kv_hi0 = w->S;
     a.qn_wA = wqA; a.qn_wB = wqB; a.qn_split = split; a.qn_eps = 1e-6f;
     a.rope_cos = w->rp_cos; a.rope_sin = w->rp_sin;
+    if (w->rp_pos) { a.rope_pos = w->rp_pos; a.rope_axis = w->rp_axis; a.rope_axis_len = w->rp_axis_len; }
     a.ws = w->attn_ws; a.ws_bytes = w->attn_ws_bytes;
     /* SREF strength (sref_set_strength_bias, iris_transformer_flux.c:1328-1338):
      * log gamma on the logits of the reference keys, the trailing I - I0 tokens */
@@ -970,6 +1031,8 @@ void *iris_flux_device_buffer(iris_transformer_t *tf, const char *name) {
     if (!strcmp(name, "rope_sin")) return w->rope_sin;
     if (!strcmp(name, "rope_pair_cos")) return w->rp_cos;
     if (!strcmp(name, "rope_pair_sin")) return w->rp_sin;
+    if (!strcmp(name, "rope_pos")) return w->rp_pos;
+    if (!strcmp(name, "rope_axis")) return w->rp_axis;
     if (!strcmp(name, "t_emb")) return w->temb;
     if (!strcmp(name, "mod")) return w->mod;
     if (!strcmp(name, "a")) return w->a;

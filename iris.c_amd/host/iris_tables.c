@@ -61,6 +61,21 @@ void iris_rope_img(float *cos_out, float *sin_out, int ph, int pw, int axis_dim,
         }
 }
 
+/* One axis's per-pair values at positions 0 .. len-1: [len][axis_dim / 2],
+ * through axis_fill (entry d of position p = column 2d of that axis's rows). */
+void iris_rope_axis(float *cos_out, float *sin_out, int len, int axis_dim, float theta) {
+    int half = axis_dim / 2;
+    float base[64], c[128], s[128];
+    rope_bases(base, half, axis_dim, theta);
+    for (int p = 0; p < len; p++) {
+        axis_fill(c, s, p, base, half);
+        for (int d = 0; d < half; d++) {
+            cos_out[(size_t)p * half + d] = c[2 * d];
+            sin_out[(size_t)p * half + d] = s[2 * d];
+        }
+    }
+}
+
 /* compute_rope_text (iris_transformer_flux.c:1055-1087): only axis L = s rotates */
 void iris_rope_txt(float *cos_out, float *sin_out, int txt_seq, int axis_dim, float theta) {
     int half = axis_dim / 2, hd = 4 * axis_dim;

@@ -12,6 +12,7 @@ void iris_rope_zimage(float *cos_out, float *sin_out, const int *pos, int seq, c
                       const int *lens, float theta);
 void iris_timestep_sincos(float *out, float t, int dim, float max_period);
 void iris_rope_pairs(float *pc, float *ps, const float *c, const float *s, size_t rows);
+void iris_rope_axis(float *cos_out, float *sin_out, int len, int axis_dim, float theta);
 #ifdef __cplusplus
 }
 #endif

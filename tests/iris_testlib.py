@@ -113,7 +113,8 @@ class AttnArgs(ctypes.Structure):
                 ("kv_group", ctypes.c_int), ("bias_from", ctypes.c_int), ("key_bias", ctypes.c_float),
                 ("qn_wA", ctypes.c_void_p), ("qn_wB", ctypes.c_void_p), ("qn_split", ctypes.c_int),
                 ("qn_eps", ctypes.c_float), ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p),
-                ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
+                ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t), ("rope_pos", ctypes.c_void_p),
+                ("rope_axis", ctypes.c_void_p), ("rope_axis_len", ctypes.c_int)]
 
 
 class Conv3x3(ctypes.Structure):

@@ -106,6 +106,22 @@ def test_multiref_rope_and_token_layout_bit_exact(lib, tiny):
     assert lib.iris_hip_memcpy_d2h(tok.ctypes.data, buf(lib, tiny, "tokens"), tok.nbytes) == 0
     want = np.concatenate([a.reshape(128, -1).T for a in (lat, r1, r2)])
     np.testing.assert_array_equal(tok, tl.to_bf16(want))
+    # the Q prologue's factored tables: axis positions (T, H, W, L) per row and
+    # one frequency table (32 positions here) expand to the per-row pair
+    # tables bit for bit
+    pos = np.empty((S, 4), np.int16)
+    assert lib.iris_hip_memcpy_d2h(pos.ctypes.data, buf(lib, tiny, "rope_pos"), pos.nbytes) == 0
+    np.testing.assert_array_equal(pos[5], [0, 0, 0, 5])
+    np.testing.assert_array_equal(pos[32 + 2 * 8 + 3], [0, 2, 3, 0])
+    np.testing.assert_array_equal(pos[96 + 7], [1, 0, 7, 0])
+    np.testing.assert_array_equal(pos[160 + 6 + 5], [2, 1, 5, 0])
+    tab = tl.d2h_f32(lib, buf(lib, tiny, "rope_axis"), (64, 16))
+    pc = tl.d2h_f32(lib, buf(lib, tiny, "rope_pair_cos"), (S, 64))
+    ps = tl.d2h_f32(lib, buf(lib, tiny, "rope_pair_sin"), (S, 64))
+    ec = np.stack([tab[pos[:, i // 16], i % 16] for i in range(64)], 1)
+    es = np.stack([tab[32 + pos[:, i // 16], i % 16] for i in range(64)], 1)
+    np.testing.assert_array_equal(ec.view(np.uint32), pc.view(np.uint32))
+    np.testing.assert_array_equal(es.view(np.uint32), ps.view(np.uint32))
 
 
 def test_double_block(lib, orc, tiny, tiny_orc):

@@ -782,6 +782,52 @@ def test_flash_attention_fused_q(lib, S, H, batch, split, rope, causal, group):
             assert tl.rel_l2(got[b, :, h * 128:(h + 1) * 128], ref) < 1e-2, (b, h)
 
 
+@pytest.mark.parametrize("S,H,batch,split_sched", [(1000, 3, 2, False), (2304, 30, 1, True)])
+def test_flash_attention_factored_rope(lib, S, H, batch, split_sched):
+    """The Q prologue's factored RoPE (per-row positions on four axes of 16
+    pairs and one shared frequency table) against the same values as per-row
+    pair tables: bit-identical outputs, on a ragged last query block and on
+    the balanced schedule (270 units: blocks start mid-unit)."""
+    rng = np.random.default_rng(S + H)
+    h = H * 128
+    ld = 3 * h
+    S_pad = (S + 63) // 64 * 64
+    raw = rng.standard_normal((batch, S, ld), np.float32)
+    k = rng.standard_normal((batch, S, h), np.float32)
+    vt = rng.standard_normal((batch, H, 128, S_pad), np.float32)
+    wA = (1 + 0.3 * rng.standard_normal(128)).astype(np.float32)
+    L = 80
+    pos = rng.integers(0, L, (S, 4)).astype(np.int16)
+    base = (np.float32(2000.0) ** (-np.arange(16, dtype=np.float32) * 2 / 32)).astype(np.float32)
+    ang = np.arange(L, dtype=np.float32)[:, None] * base[None, :]
+    tab = np.concatenate([np.cos(ang), np.sin(ang)]).astype(np.float32)     # [2L][16]
+    pc = np.stack([tab[pos[:, i // 16], i % 16] for i in range(64)], 1).astype(np.float32)
+    ps = np.stack([tab[L + pos[:, i // 16], i % 16] for i in range(64)], 1).astype(np.float32)
+    dq, dk, dvt = tl.Dev.of(tl.to_bf16(raw)), tl.Dev.of(tl.to_bf16(k)), tl.Dev.of(tl.to_bf16(vt))
+    dw, dpc, dps = tl.Dev.of(wA), tl.Dev.of(pc), tl.Dev.of(ps)
+    dpos, dtab = tl.Dev.of(np.ascontiguousarray(pos)), tl.Dev.of(tab)
+    wsb = lib.iris_hip_attention_workspace_bytes() if split_sched else 0
+    ws = tl.Dev(wsb) if split_sched else None
+    if split_sched:
+        assert lib.iris_hip_memset(ws.ptr, 0, wsb) == 0
+    outs = []
+    for factored in (False, True):
+        o = tl.Dev(batch * S * h * 2)
+        a = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, o.ptr, ld, h, S_pad, h, S, S, H, batch, S * ld, S * h,
+                        H * 128 * S_pad, S * h, 1 / math.sqrt(128), 0, S, 0, 0, 0, 0, 0, 0.0, dw.ptr, dw.ptr, S,
+                        1e-6, dpc.ptr, dps.ptr, ws.ptr if split_sched else None, wsb,
+                        dpos.ptr if factored else None, dtab.ptr if factored else None, L if factored else 0)
+        assert lib.iris_hip_attention(ctypes.byref(a)) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+        outs.append(o.get(np.uint16, (batch, S, h)))
+        o.close()
+    assert np.array_equal(outs[0], outs[1]), "factored tables give other bits"
+    bad = tl.AttnArgs(dq.ptr, dk.ptr, dvt.ptr, dq.ptr, ld, h, S_pad, h, S, S, H, batch, S * ld, S * h,
+                      H * 128 * S_pad, S * h, 1 / math.sqrt(128), 0, S, 0, 0, 0, 0, 0, 0.0, None, None, S,
+                      1e-6, None, None, None, 0, dpos.ptr, dtab.ptr, L)
+    assert lib.iris_hip_attention(ctypes.byref(bad)) != 0, "factored tables without the Q prologue accepted"
+
+
 @pytest.mark.parametrize("N,K,act", [(18432, 3072, 1), (3072, 256, 0), (100, 3840, 1), (1001, 128, 0), (7, 264, 1),
                                      (33, 8, 0), (61440, 256, 0)])
 def test_gemv(lib, N, K, act):
