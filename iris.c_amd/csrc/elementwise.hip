@@ -259,10 +259,22 @@ __global__ __launch_bounds__(NT) void qkv_prep_kernel(const iris_qkprep_args_t a
 
 /* y[n] = W[n, :] . act(x) + bias[n]. One wave per row, or for K <= 256 half
  * a wave per row (lanes 32..63 take the next row); each lane takes 8
- * consecutive elements of every 512- (256-) wide chunk, and up to four
- * chunks' loads are issued before their products. */
+ * consecutive elements of every 512- (256-) wide chunk. XLDS (K <= 4096):
+ * the block first writes act(x) to LDS once, so the SiLU of the input is not
+ * recomputed for every row. */
+constexpr int GEMV_XLDS = 4096;
+template <bool XLDS>
 __global__ __launch_bounds__(NT) void gemv_kernel(float *y, const uint16_t *W, const float *x, const float *bias,
                                                   int N, int K, int act_in) {
+    __shared__ __attribute__((aligned(16))) float xl[XLDS ? GEMV_XLDS : 4];
+    if constexpr (XLDS) {
+        for (int k = threadIdx.x; k < K; k += NT) {
+            float v = x[k];
+            if (act_in == 1) v = v / (1.0f + __expf(-v));
+            xl[k] = v;
+        }
+        __syncthreads();
+    }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const bool half = K <= 256;
     const int gw = blockIdx.x * (NT / IRIS_WAVE) + wave;
@@ -271,29 +283,22 @@ __global__ __launch_bounds__(NT) void gemv_kernel(float *y, const uint16_t *W, c
     float acc = 0.0f;
     if (n < N) {
         const uint16_t *w = W + (size_t)n * K;
-        for (int k0 = l * 8; k0 < K; k0 += 4 * step) {
-            u16x8 wv[4];
-            float4 xa[4], xb[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int k = k0 + u * step;
-                wv[u] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-                xa[u] = xb[u] = make_float4(0, 0, 0, 0);
-                if (k < K) {
-                    wv[u] = *(const u16x8 *)(w + k);
-                    xa[u] = *(const float4 *)(x + k);
-                    xb[u] = *(const float4 *)(x + k + 4);
-                }
+        for (int k = l * 8; k < K; k += step) {
+            const u16x8 wv = *(const u16x8 *)(w + k);
+            float4 xa, xb;
+            if constexpr (XLDS) {
+                xa = *(const float4 *)(xl + k);
+                xb = *(const float4 *)(xl + k + 4);
+            } else {
+                xa = *(const float4 *)(x + k);
+                xb = *(const float4 *)(x + k + 4);
             }
+            float xs[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float xs[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    float xv = xs[e];
-                    if (act_in == 1) xv = xv / (1.0f + __expf(-xv));
-                    acc += bf2f(wv[u][e]) * xv;
-                }
+            for (int e = 0; e < 8; e++) {
+                float xv = xs[e];
+                if (!XLDS && act_in == 1) xv = xv / (1.0f + __expf(-xv));
+                acc += bf2f(wv[e]) * xv;
             }
         }
     }
@@ -493,8 +498,11 @@ int iris_hip_gemv(float *y, const uint16_t *W, const float *x, const float *bias
     if (N <= 0) return 0;
     if (K % 8) return iris_set_error("gemv: K=%d must be a multiple of 8", K);
     const int rows_per_block = (K <= 256 ? 2 : 1) * (NT / IRIS_WAVE);
-    IRIS_LAUNCH(gemv_kernel, dim3((N + rows_per_block - 1) / rows_per_block), dim3(NT), 0, iris_stream(), y, W, x,
-                bias, N, K, act_in);
+    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
+    if (K <= GEMV_XLDS)
+        IRIS_LAUNCH(gemv_kernel<true>, grid, dim3(NT), 0, iris_stream(), y, W, x, bias, N, K, act_in);
+    else
+        IRIS_LAUNCH(gemv_kernel<false>, grid, dim3(NT), 0, iris_stream(), y, W, x, bias, N, K, act_in);
     return iris_launch_check("gemv_kernel");
 }
 
