@@ -1,6 +1,6 @@
 /*
  * orc_vae.c - f32 CPU restatement of the reference's VAE decoder and encoder
- * (TEST INFRASTRUCTURE ONLY: the checker of the GPU VAE, never shipped).
+ * (TEST INFRASTRUCTURE ONLY: the reference for the GPU VAE in the tests, never shipped).
  *
  * Follows iris_vae.c of the reference: iris_vae_decode (:835-998),
  * iris_vae_encode (:363-482),

@@ -416,7 +416,7 @@ C1_PATH = os.path.join(tl.GOLDEN, "reference_c1_single_block.npz")
 
 @pytest.mark.skipif(not os.path.exists(C1_PATH), reason="C1 golden not generated")
 def test_c1_single_block_4b_shape(lib):
-    """one 4B-shaped single block, 128 txt + 256 img (16x16)."""
+    """The single-block workload at 4B widths: one single block, 128 txt + 256 img (16x16)."""
     g = np.load(C1_PATH, allow_pickle=False)
     c1 = MAN["c1"]
     m = ctypes.c_void_p(lib.orc_flux_create_synth(3072, 24, 1, 1, 7680, 128, 3.0, 2000.0, c1["seed"]))
