@@ -317,8 +317,8 @@ def c1_models(lib, orc):
     orc.orc_flux_free(m)
 
 
+def test_c1_single_block_4b_shape(lib, orc, c1_models):
     """The single-block workload at 4B widths: one single block, 128 txt + 256 img (16x16),
-    """BASELINE config 0: one 4B-shaped single block, 128 txt + 256 img (16x16),
     x ~ N(0,1), conditioning ~ N(0,1); vs the oracle and the reference golden."""
     tf, m = c1_models
     T, I, h = 128, 256, 3072
