@@ -119,6 +119,8 @@ struct iris_transformer {
     int hidden, heads, head_dim, mlp, n_double, n_single, text_dim, latent_ch, axis_dim;
     float theta;
     uint16_t *img_in, *txt_in, *t_fc1, *t_fc2, *mod_dimg, *mod_dtxt, *mod_single, *final_mod, *proj_out;
+    uint16_t *mod_all;   /* [17 h][h]: the four modulation linears stacked (mod_dimg .. final_mod point
+                          * into it), so one GEMV fills the step's modulation vector */
     dev_double_t *dbl;
     dev_single_t *sgl;
     work_t w;
@@ -291,10 +293,16 @@ static int load_weights(iris_transformer_t *tf, source_t *s) {
     UP(tf->txt_in, "context_embedder.weight", h * tf->text_dim);
     UP(tf->t_fc1, "time_guidance_embed.timestep_embedder.linear_1.weight", h * 256);
     UP(tf->t_fc2, "time_guidance_embed.timestep_embedder.linear_2.weight", h * h);
-    UP(tf->mod_dimg, "double_stream_modulation_img.linear.weight", 6 * h * h);
-    UP(tf->mod_dtxt, "double_stream_modulation_txt.linear.weight", 6 * h * h);
-    UP(tf->mod_single, "single_stream_modulation.linear.weight", 3 * h * h);
-    UP(tf->final_mod, "norm_out.linear.weight", 2 * h * h);
+    if (!(tf->mod_all = (uint16_t *)iris_hip_malloc((size_t)17 * h * h * 2))) return -1;
+    tf->mod_dimg = tf->mod_all;
+    tf->mod_dtxt = tf->mod_all + (size_t)6 * h * h;
+    tf->mod_single = tf->mod_all + (size_t)12 * h * h;
+    tf->final_mod = tf->mod_all + (size_t)15 * h * h;
+    if (upload_rows(s, "double_stream_modulation_img.linear.weight", tf->mod_dimg, 6 * h, h) ||
+        upload_rows(s, "double_stream_modulation_txt.linear.weight", tf->mod_dtxt, 6 * h, h) ||
+        upload_rows(s, "single_stream_modulation.linear.weight", tf->mod_single, 3 * h, h) ||
+        upload_rows(s, "norm_out.linear.weight", tf->final_mod, 2 * h, h))
+        return -1;
     UP(tf->proj_out, "proj_out.weight", C * h);
     tf->dbl = (dev_double_t *)calloc((size_t)tf->n_double, sizeof(dev_double_t));
     tf->sgl = (dev_single_t *)calloc((size_t)tf->n_single, sizeof(dev_single_t));
@@ -370,8 +378,7 @@ void iris_transformer_free(iris_transformer_t *tf) {
     free(tf->csd_zero);
     iris_hip_free(tf->d_csd);
     iris_hip_free(tf->img_in); iris_hip_free(tf->txt_in); iris_hip_free(tf->t_fc1); iris_hip_free(tf->t_fc2);
-    iris_hip_free(tf->mod_dimg); iris_hip_free(tf->mod_dtxt); iris_hip_free(tf->mod_single);
-    iris_hip_free(tf->final_mod); iris_hip_free(tf->proj_out);
+    iris_hip_free(tf->mod_all); iris_hip_free(tf->proj_out);
     for (int i = 0; tf->dbl && i < tf->n_double; i++) {
         dev_double_t *b = &tf->dbl[i];
         iris_hip_free(b->img_qkv); iris_hip_free(b->img_o); iris_hip_free(b->img_ffin); iris_hip_free(b->img_down);
@@ -873,10 +880,9 @@ static int enqueue_forward(iris_transformer_t *tf) {
     /* the CSD style delta is added to temb before its SiLU (iris_transformer_flux.c:3969-3972):
      * the bias of the second time-MLP linear */
     CK(iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, w->csd_on ? tf->d_csd : NULL, h, h, 1));
-    CK(iris_hip_gemv(w->mod, tf->mod_dimg, w->temb, NULL, 6 * h, h, 1));
-    CK(iris_hip_gemv(w->mod + 6 * h, tf->mod_dtxt, w->temb, NULL, 6 * h, h, 1));
-    CK(iris_hip_gemv(w->mod + 12 * h, tf->mod_single, w->temb, NULL, 3 * h, h, 1));
-    CK(iris_hip_gemv(w->mod + 15 * h, tf->final_mod, w->temb, NULL, 2 * h, h, 1));
+    /* the four modulation linears in one GEMV over their stacked rows:
+     * mod = dimg 6h | dtxt 6h | single 3h | final 2h */
+    CK(iris_hip_gemv(w->mod, tf->mod_all, w->temb, NULL, 17 * h, h, 1));
     /* NCHW -> token rows for the target and each reference (:3986-3993, :4667-4689) */
     size_t off = 0;
     CK(iris_hip_nchw_to_tokens(w->tok, w->lat, C, I0));
