@@ -163,3 +163,34 @@ def test_schedules_equal_reference_build(prod, fn, args, monkeypatch):
             for n in range(1, 40):
                 np.testing.assert_array_equal(bits(take(prod.iris_zimage_schedule(n, 1), n + 1)),
                                               bits(take(ref.iris_zimage_schedule(n, 1), n + 1)))
+
+
+def test_factored_rope_axis_reproduces_tables(prod):
+    """The attention prologue's factored RoPE (iris_rope_axis: one axis's
+    per-pair cos / sin by position) against the full per-row tables of
+    iris_rope_img / iris_rope_txt (4 axes of 32 dims, theta 2000): every
+    image row's H and W pairs and T pairs (T-offset 2) and every text row's
+    L pairs are the axis table's entries at the row's positions, bit for bit,
+    and the identity axes (position 0) are the table's row 0."""
+    prod.iris_rope_axis.argtypes = [tl.FP, tl.FP, ctypes.c_int, ctypes.c_int, F]
+    prod.iris_rope_img.argtypes = [tl.FP, tl.FP, ctypes.c_int, ctypes.c_int, ctypes.c_int, F, ctypes.c_int]
+    prod.iris_rope_txt.argtypes = [tl.FP, tl.FP, ctypes.c_int, ctypes.c_int, F]
+    ph, pw, T, L = 24, 40, 77, 80
+    ac, as_ = np.zeros((L, 16), np.float32), np.zeros((L, 16), np.float32)
+    prod.iris_rope_axis(tl.fptr(ac), tl.fptr(as_), L, 32, F(2000.0))
+    ic, is_ = np.zeros((ph * pw, 128), np.float32), np.zeros((ph * pw, 128), np.float32)
+    prod.iris_rope_img(tl.fptr(ic), tl.fptr(is_), ph, pw, 32, F(2000.0), 2)
+    tc, ts = np.zeros((T, 128), np.float32), np.zeros((T, 128), np.float32)
+    prod.iris_rope_txt(tl.fptr(tc), tl.fptr(ts), T, 32, F(2000.0))
+    y, x = np.arange(ph * pw) // pw, np.arange(ph * pw) % pw
+    for tab, full in ((ac, ic), (as_, is_)):
+        pairs = full[:, 0::2]
+        np.testing.assert_array_equal(pairs[:, 0:16].view(np.uint32), np.broadcast_to(tab[2], (ph * pw, 16)).view(np.uint32))
+        np.testing.assert_array_equal(pairs[:, 16:32].view(np.uint32), tab[y].view(np.uint32))
+        np.testing.assert_array_equal(pairs[:, 32:48].view(np.uint32), tab[x].view(np.uint32))
+        np.testing.assert_array_equal(pairs[:, 48:64].view(np.uint32), np.broadcast_to(tab[0], (ph * pw, 16)).view(np.uint32))
+    for tab, full in ((ac, tc), (as_, ts)):
+        pairs = full[:, 0::2]
+        np.testing.assert_array_equal(pairs[:, 48:64].view(np.uint32), tab[np.arange(T)].view(np.uint32))
+        np.testing.assert_array_equal(pairs[:, 0:48].view(np.uint32),
+                                      np.tile(tab[0], (T, 3)).reshape(T, 48).view(np.uint32))
