@@ -28,6 +28,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -43,6 +44,7 @@ F = ctypes.c_float
 
 CONFIGS = {
     "ns": dict(kind="flux", h=3072, H=24, nd=5, ns=20, td=7680, ih=64, iw=64, T=512, steps=4, refs=[], B=1,
+               golden="oracle_4b_ns_sample.npz",
                workload="Flux.2-Klein-4B-shaped denoise, 1024x1024 (4096 img + 512 txt tokens), 4 steps"),
     "c2": dict(kind="flux", h=3072, H=24, nd=5, ns=20, td=7680, ih=32, iw=32, T=512, steps=4, refs=[], B=1,
                workload="Flux.2-Klein-4B-shaped denoise, 512x512 (1024 img + 512 txt tokens), 4 steps"),
@@ -62,7 +64,7 @@ CONFIGS = {
                 workload="Flux.2 VAE decoder, 128x64x64 latent -> 1024x1024 RGB (z_channels 32, batch-norm "
                          "denormalization, post_quant_conv, 16384-token bottleneck attention)"),
     "c5": dict(kind="zimage", d=3840, H=30, layers=30, refiners=2, cap_dim=2560, ffn=10240, t_mid=1024, lh=128,
-               lw=128, cap=512, steps=8,
+               lw=128, cap=512, steps=8, golden="oracle_zimage_turbo_sample.npz",
                workload="Z-Image-Turbo-6B-shaped S3-DiT, 1024x1024 (4096 img + 512 caption tokens), 8 NFE"),
 }
 
@@ -92,6 +94,35 @@ def zimage_flops(c):
             + 2 * I * 64 * d + 2 * T * c["cap_dim"] * d + 2 * I * d * 64)
 
 
+def synth_f32(shape, seed, mean=0.0, std=1.0):
+    """Seeded N(mean, std) float32 inputs from the HIP library's own generator
+    (iris_synth_fill_f32, include/iris_synth.h): the same values the tests'
+    helper draws, without loading anything else."""
+    lib = tl.hip()
+    lib.iris_synth_fill_f32.argtypes = [tl.FP, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
+                                        ctypes.c_float]
+    n = int(np.prod(shape))
+    a = np.empty(n, np.float32)
+    lib.iris_synth_fill_f32(tl.fptr(a), n, seed, 0, mean, std)
+    return a.reshape(shape)
+
+
+def lscpu_model():
+    """`Model name` as lscpu prints it (run as a child process before the GPU
+    is touched), or None."""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    for line in out.splitlines():
+        if line.startswith("Model name:"):
+            return line.split(":", 1)[1].strip()
+    return None
+
+
+LSCPU_MODEL = None
+
+
 def host_cpu():
     """(threads, description) of the host cores the CPU baseline runs on: the
     `model name` of /proc/cpuinfo, the online CPU count (nproc) and the
@@ -109,6 +140,8 @@ def host_cpu():
     online = os.cpu_count() or 1
     avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else online
     threads = int(os.environ.get("IRIS_ORACLE_THREADS", min(avail, 16)))
+    if LSCPU_MODEL and LSCPU_MODEL != model:
+        model = f"{model} (lscpu: {LSCPU_MODEL})"
     return threads, (f"{model}, nproc {online}, {avail} available to the process, {threads} threads "
                      f"(the 16-core host share of one GPU)")
 
@@ -176,6 +209,31 @@ def gemm_grid(shapes):
     return 8 * -(-t // 8)
 
 
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def check_vs_golden(got, z0, g, sign, cfg_name):
+    """The timed workload's own output against the oracle's sample of it
+    (same seeds, same schedule): the final latent after all steps against the
+    oracle's Euler trajectory rebuilt from its per-step velocities
+    (z += dt * sign * v in float32). Data files only; nothing is run."""
+    z = z0.copy()
+    sched = g["schedule"]
+    for i in range(len(sched) - 1):
+        z = z + np.float32(sched[i + 1] - sched[i]) * (np.float32(sign) * g[f"velocity_{i}"])
+    rel = float(np.linalg.norm((got - z).astype(np.float64)) / np.linalg.norm(z.astype(np.float64)))
+    cos = float(np.dot(got.astype(np.float64), z.astype(np.float64)) /
+                (np.linalg.norm(got.astype(np.float64)) * np.linalg.norm(z.astype(np.float64))))
+    return {"golden": "tests/golden/" + cfg_name, "steps": len(sched) - 1,
+            "final_latent_rel_l2": round(rel, 6), "final_latent_cosine": round(cos, 7),
+            "pass": bool(rel <= 1e-2 and cos >= 0.999)}
+
+
+def golden_for(name):
+    path = os.path.join(GOLDEN, name)
+    return np.load(path, allow_pickle=False) if os.path.exists(path) else None
+
+
 def run_flux(lib, c, args):
     t0 = time.time()
     tf = ctypes.c_void_p(lib.iris_transformer_create_synthetic(c["h"], c["H"], c["nd"], c["ns"], c["td"], 128, 3.0,
@@ -186,8 +244,8 @@ def run_flux(lib, c, args):
     lib.iris_init_noise.argtypes = [ctypes.c_int] * 4 + [ctypes.c_int64]
     zp = lib.iris_init_noise(1, 128, c["ih"], c["iw"], 42)
     z = np.ctypeslib.as_array(ctypes.cast(zp, tl.FP), shape=(128 * I0,)).copy()
-    txt = tl.synth_f32((c["B"], c["T"], c["td"]), 7)
-    refs_np = [tl.synth_f32((128, rh, rw), 100 + i) for i, (rh, rw, _) in enumerate(c["refs"])]
+    txt = synth_f32((c["B"], c["T"], c["td"]), 7)
+    refs_np = [synth_f32((128, rh, rw), 100 + i) for i, (rh, rw, _) in enumerate(c["refs"])]
     refs = (tl.IrisRef * max(1, len(refs_np)))(*[tl.IrisRef(tl.fptr(r), rh, rw, to) for r, (rh, rw, to)
                                                  in zip(refs_np, c["refs"])])
     nref = len(refs_np)
@@ -196,14 +254,28 @@ def run_flux(lib, c, args):
     lib.iris_official_schedule.argtypes = [ctypes.c_int, ctypes.c_int]
     sp = lib.iris_official_schedule(c["steps"], I0)
     sched = np.ctypeslib.as_array(ctypes.cast(sp, tl.FP), shape=(c["steps"] + 1,)).copy()
-    g = 4.0 if c["B"] == 2 else 0.0
+    g_cfg = 4.0 if c["B"] == 2 else 0.0
 
     def step(i):
         j = i % c["steps"]
-        assert lib.iris_flux_step(tf, float(sched[j]), float(sched[j + 1]), g) == 0, lib.iris_hip_last_error()
+        assert lib.iris_flux_step(tf, float(sched[j]), float(sched[j + 1]), g_cfg) == 0, lib.iris_hip_last_error()
 
     ms_step, wall = timed_steps(lib, step, args)
     prof = profile_step(lib, step, args.warmup + args.steps)
+    parity = None
+    g = golden_for(c["golden"]) if c.get("golden") else None
+    if g is not None:
+        # the same workload once more from its noise, all steps, output kept
+        # (on the golden's schedule: the reference build's, whose last bit
+        # can differ from this host's by the CPU's reciprocal estimate)
+        gs = g["schedule"]
+        assert np.abs(gs - sched).max() <= 2.4e-7, (gs, sched)
+        assert lib.iris_flux_upload(tf, tl.fptr(z), refs if nref else None, None) == 0
+        for j in range(c["steps"]):
+            assert lib.iris_flux_step(tf, float(gs[j]), float(gs[j + 1]), g_cfg) == 0, lib.iris_hip_last_error()
+        got = np.empty_like(z)
+        assert lib.iris_flux_download_latent(tf, tl.fptr(got)) == 0, lib.iris_hip_last_error()
+        parity = check_vs_golden(got, z, g, 1.0, c["golden"])
 
     # kernel classes on the step's own resident buffers
     h, mlp, H, B = c["h"], 3 * c["h"], c["H"], c["B"]
@@ -212,7 +284,7 @@ def run_flux(lib, c, args):
     BS = B * S
     dbuf = {n: lib.iris_flux_device_buffer(tf, n.encode()) for n in ("a", "qkv", "cat", "q", "k", "vt")}
     wdev = tl.Dev(2 * mlp * h * 2)
-    wdev.put(tl.to_bf16(tl.synth_f32((2 * mlp * h,), 9, 0, 0.02)))
+    wdev.put(tl.to_bf16(synth_f32((2 * mlp * h,), 9, 0, 0.02)))
     P = tl.GemmProblem
     probs = (P * 1)(P(dbuf["a"], wdev.ptr, dbuf["cat"] + h * 2, None, BS, 2 * mlp, h, h, h, h + mlp, 3))
     g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(probs, 1))
@@ -242,7 +314,7 @@ def run_flux(lib, c, args):
     cfg = {"workload": c["workload"], "hidden": h, "heads": H, "double_blocks": c["nd"], "single_blocks": c["ns"],
            "image_tokens": I0, "reference_tokens": S - I0 - c["T"], "text_tokens": c["T"], "seq": S, "batch": B,
            "steps_per_image": c["steps"]}
-    return ms_step, wall, flux_flops(c), kernels, cfg, t_load, prof
+    return ms_step, wall, flux_flops(c), kernels, cfg, t_load, prof, parity
 
 
 def run_zimage(lib, c, args):
@@ -256,7 +328,7 @@ def run_zimage(lib, c, args):
     lib.iris_init_noise.argtypes = [ctypes.c_int] * 4 + [ctypes.c_int64]
     zp = lib.iris_init_noise(1, 16, c["lh"], c["lw"], 42)
     z = np.ctypeslib.as_array(ctypes.cast(zp, tl.FP), shape=(16 * c["lh"] * c["lw"],)).copy()
-    cap = tl.synth_f32((c["cap"], c["cap_dim"]), 7)
+    cap = synth_f32((c["cap"], c["cap_dim"]), 7)
     assert lib.zi_prepare(tf, c["lh"], c["lw"], c["cap"]) == 0, lib.iris_hip_last_error()
     assert lib.zi_upload(tf, tl.fptr(z), tl.fptr(cap)) == 0
     I = (c["lh"] // 2) * (c["lw"] // 2)
@@ -270,20 +342,31 @@ def run_zimage(lib, c, args):
 
     ms_step, wall = timed_steps(lib, step, args)
     prof = profile_step(lib, step, args.warmup + args.steps)
+    parity = None
+    g = golden_for(c["golden"]) if c.get("golden") else None
+    if g is not None:
+        gs = g["schedule"]
+        assert np.abs(gs - sched).max() <= 2.4e-7, (gs, sched)
+        assert lib.zi_upload(tf, tl.fptr(z), None) == 0
+        for j in range(c["steps"]):
+            assert lib.zi_step(tf, float(gs[j]), float(gs[j + 1])) == 0, lib.iris_hip_last_error()
+        got = np.empty_like(z)
+        assert lib.zi_download_latent(tf, tl.fptr(got)) == 0, lib.iris_hip_last_error()
+        parity = check_vs_golden(got, z, g, -1.0, c["golden"])
 
     d, f, H = c["d"], c["ffn"], c["H"]
     S = I + c["cap"]
     S_pad = (S + 63) // 64 * 64
     dbuf = {n: lib.zi_device_buffer(tf, n.encode()) for n in ("a", "qkv", "cat")}
     wdev = tl.Dev(2 * f * d * 2)
-    wdev.put(tl.to_bf16(tl.synth_f32((2 * f * d,), 9, 0, 0.02)))
+    wdev.put(tl.to_bf16(synth_f32((2 * f * d,), 9, 0, 0.02)))
     P = tl.GemmProblem
     prob = (P * 1)(P(dbuf["a"], wdev.ptr, dbuf["cat"], None, S, 2 * f, d, d, d, f, 3))
     g_ms = time_launches(lib, lambda: lib.iris_hip_gemm(prob, 1))
     wdev.close()
     q, k, vt, o = (tl.Dev(S * d * 2), tl.Dev(S * d * 2), tl.Dev(H * 128 * S_pad * 2), tl.Dev(S * d * 2))
     for b in (q, k, vt):
-        b.put(tl.to_bf16(tl.synth_f32((b.n // 2,), 11)))
+        b.put(tl.to_bf16(synth_f32((b.n // 2,), 11)))
     wsb = lib.iris_hip_attention_workspace_bytes()
     aws = tl.Dev(wsb)
     assert lib.iris_hip_memset(aws.ptr, 0, wsb) == 0
@@ -303,7 +386,7 @@ def run_zimage(lib, c, args):
     lib.zi_transformer_free(tf)
     cfg = {"workload": c["workload"], "dim": d, "heads": H, "layers": c["layers"], "refiners": c["refiners"],
            "image_tokens": I, "caption_tokens": c["cap"], "seq": S, "batch": 1, "steps_per_image": c["steps"]}
-    return ms_step, wall, zimage_flops(c), kernels, cfg, t_load, prof
+    return ms_step, wall, zimage_flops(c), kernels, cfg, t_load, prof, parity
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_rocprof_pmc.md")
@@ -338,7 +421,7 @@ def probe(kind, n):
     def dev(nbytes, seed=None, scale=1.0):
         d = tl.Dev(nbytes)
         if seed is not None:
-            d.put(tl.to_bf16(tl.synth_f32((nbytes // 2,), seed, 0, scale)))
+            d.put(tl.to_bf16(synth_f32((nbytes // 2,), seed, 0, scale)))
         bufs.append(d)
         return d.ptr
 
@@ -368,7 +451,7 @@ def probe(kind, n):
         # the double block's AdaLN: LayerNorm + (1 + scale) x + shift of the f32 residual rows, bf16 out,
         # txt rows with one modulation set, img rows with the other
         x, a = dev(S * h * 4), dev(S * h * 2)
-        mods = [tl.Dev.of(tl.synth_f32((h,), 20 + i, 0, 0.1)) for i in range(4)]
+        mods = [tl.Dev.of(synth_f32((h,), 20 + i, 0, 0.1)) for i in range(4)]
         bufs.extend(mods)
         na = tl.NormArgs(x, h, a, h, 1, S, h, 0, 1e-6, c["T"], S, mods[0].ptr, mods[1].ptr, None, mods[2].ptr,
                          mods[3].ptr, None)
@@ -444,9 +527,9 @@ def run_qwen3(lib, c, args):
     # the dominant launch, on buffers of its shape: gate/up with the SwiGLU epilogue
     h, I = c["h"], c["inter"]
     a = tl.Dev(S * h * 2)
-    a.put(tl.to_bf16(tl.synth_f32((S * h,), 3)))
+    a.put(tl.to_bf16(synth_f32((S * h,), 3)))
     w = tl.Dev(2 * I * h * 2)
-    w.put(tl.to_bf16(tl.synth_f32((2 * I * h,), 9, 0, 0.02)))
+    w.put(tl.to_bf16(synth_f32((2 * I * h,), 9, 0, 0.02)))
     o = tl.Dev(S * I * 2)
     P = tl.GemmProblem
     pr = (P * 1)(P(a.ptr, w.ptr, o.ptr, None, S, 2 * I, h, h, h, I, 3))
@@ -457,7 +540,7 @@ def run_qwen3(lib, c, args):
                             "gemm_qwen3_gateup")]
     cfg = {"workload": c["workload"], "hidden": h, "intermediate": I, "heads": c["H"], "kv_heads": c["KV"],
            "layers": c["layers"], "layers_run": 27, "tokens": S, "real_tokens": c["n_real"], "vocab": c["vocab"]}
-    return ms_step, wall, qwen3_flops(c), kernels, cfg, t_load, None
+    return ms_step, wall, qwen3_flops(c), kernels, cfg, t_load, None, None
 
 
 def cpu_baseline_qwen3(c):
@@ -522,9 +605,9 @@ def run_vae(lib, c, args):
     H = W = 8 * lh
     cin = cout = 256
     x = tl.Dev(H * W * cin * 2)
-    x.put(tl.to_bf16(tl.synth_f32((H * W * cin,), 3)))
+    x.put(tl.to_bf16(synth_f32((H * W * cin,), 3)))
     wt = tl.Dev(cout * 9 * cin * 2)
-    wt.put(tl.to_bf16(tl.synth_f32((cout * 9 * cin,), 9, 0, 1.0 / 48)))
+    wt.put(tl.to_bf16(synth_f32((cout * 9 * cin,), 9, 0, 1.0 / 48)))
     o = tl.Dev(H * W * cout * 4)
     conv = tl.Conv3x3(x.ptr, wt.ptr, o.ptr, None, H, W, cin, cout, 0, cout, 0, 1, None, 0)
     c_ms = time_launches(lib, lambda: lib.iris_hip_conv3x3(ctypes.byref(conv)))
@@ -534,7 +617,7 @@ def run_vae(lib, c, args):
                             2.0 * H * W * cin * cout * 9, 5, "conv_256_512")]
     cfg = {"workload": c["workload"], "latent": [4 * c["z"], lh, lw], "image": [16 * lh, 16 * lw],
            "z_channels": c["z"], "bottleneck_tokens": 4 * lh * lw}
-    return ms_step, wall, vae_flops(c), kernels, cfg, t_load, None
+    return ms_step, wall, vae_flops(c), kernels, cfg, t_load, None, None
 
 
 def cpu_baseline_vae(c):
@@ -579,9 +662,12 @@ def main():
         probe(args.probe, args.probe_launches)
         return
     c = CONFIGS[args.config]
+    if not args.no_cpu_baseline:
+        global LSCPU_MODEL
+        LSCPU_MODEL = lscpu_model()
     lib = tl.hip()
     run = {"flux": run_flux, "zimage": run_zimage, "qwen3": run_qwen3, "vae": run_vae}[c["kind"]]
-    ms_step, wall_ms, flops, kernels, cfg, t_load, prof = run(lib, c, args)
+    ms_step, wall_ms, flops, kernels, cfg, t_load, prof, parity = run(lib, c, args)
     images_per_s = 1000.0 / (ms_step * c["steps"])   # one image per pass (CFG: both branches in one)
     dom = max(kernels, key=lambda k: k["ms_per_step"])
     result = {
@@ -612,6 +698,8 @@ def main():
         "kernels": kernels,
         "device": lib.iris_hip_device_name().decode(),
     }
+    if parity:
+        result["parity"] = parity
     if prof:
         # the profiled step: every launch between two events, the launches issued one by one
         result["profiled_step"] = {"kernel_ms": round(sum(r["total_ms"] for r in prof), 3),

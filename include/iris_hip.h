@@ -127,15 +127,29 @@ int iris_hip_gemm_splitk(const iris_gemm_problem_t *problem, int splits, float *
  * final projection) that leave most of the chip idle. */
 int iris_hip_gemm_fill(const iris_gemm_problem_t *problem, float *d_workspace, size_t workspace_bytes);
 
+/* No counterpart in the reference. iris_hip_gemm_fill over up to 4
+ * independent problems in one launch (the txt and img streams of a double
+ * block): when their 256x256 tiles together fill at most half of the CUs and
+ * every K has at least 8 steps, each problem is split into the same number of
+ * K chunks (its partials after those of the problems before it in the
+ * workspace: splits * sum of M * N floats) and one reduce launch applies the
+ * epilogues; otherwise one plain launch, as iris_hip_gemm. For the output
+ * and down projections of a 512x512 image (1536 rows), which make 72 tiles
+ * on a 256-CU device. */
+int iris_hip_gemm_fill_n(const iris_gemm_problem_t *problems, int n_problems, float *d_workspace,
+                         size_t workspace_bytes);
+
 /* No counterpart in the reference. iris_hip_gemm_splitk without a
  * workspace, for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
  * f32 partials go to a device array the library holds, of
  * IRIS_NOALLOC_SCRATCH_BYTES per GPU, kept until the process ends. Calls no
- * allocating routine. Rejects problems whose chunks x M x N f32 partials
- * exceed the array (error, -1). Every call on one GPU shares its array:
- * calls that overlap on one GPU race. Results equal iris_hip_gemm_splitk's
- * bit for bit. */
+ * allocating routine (with the per-kernel profile of iris_hip_profile_enable
+ * on, a debugging mode, the profile's own event pairs are created on their
+ * first use). Rejects problems whose chunks x M x N f32 partials exceed the
+ * array (error, -1); a K of one step is the plain product and needs none.
+ * Every call on one GPU shares its array: calls that overlap on one GPU race.
+ * Results equal iris_hip_gemm_splitk's bit for bit. */
 #define IRIS_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int iris_hip_gemm_splitk_noalloc(const iris_gemm_problem_t *problem, int splits);
 

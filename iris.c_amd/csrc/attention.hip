@@ -519,7 +519,8 @@ __device__ __forceinline__ void attn_segment(const iris_attn_args_t &a, float sc
 
     /* normalise and store O[q][d]: lane holds query lr, d = dsub*32 + (r>>2)*8 + lg*4 + (r&3) */
     const float l = l_run + __shfl_xor(l_run, 32, 64);
-    if ((a.ld_o & 7) == 0 && ((uintptr_t)a.o & 15) == 0) {
+    /* 16-byte stores need every batch slot's rows 16-byte aligned as well */
+    if ((a.ld_o & 7) == 0 && ((uintptr_t)a.o & 15) == 0 && (a.batch == 1 || (a.o_bstride & 7) == 0)) {
         /* through LDS (every stage is free after the last barrier): the block's
          * 256 rows of 128 + 8 elements, then 16-byte chunks of whole rows, so a
          * store instruction writes 4 full rows instead of 16-byte pieces of 32 */

@@ -55,11 +55,13 @@ struct GemmParams {
     iris_gemm_problem_t p[MAXP];
     int tiles_m[MAXP], tiles_n[MAXP], tile_start[MAXP + 1];
     int nprob, total, per_xcd;
-    /* split-K (one problem): block t works on K chunk t / (tiles) and writes
-     * its f32 partial product to ws + chunk * ws_stride */
-    int splits, kchunk;
-    float *ws;
-    long long ws_stride;
+    /* split-K: problem i with chunks[i] > 1 has tiles_m[i] * tiles_n[i] *
+     * chunks[i] blocks; block t of it works on K chunk t / (tiles_m * tiles_n)
+     * (kchunk[i] elements) and writes its f32 partial product to
+     * ws[i] + chunk * ws_stride[i] (M x N, row stride N) */
+    int chunks[MAXP], kchunk[MAXP];
+    float *ws[MAXP];
+    long long ws_stride[MAXP];
     /* implicit 3x3 convolution (one problem, CONV kernels only): A is the bf16
      * NHWC input of (conv_h >> up) x (conv_w >> up) pixels, 2^cin_bshift bytes
      * per pixel; output row m is pixel (m / conv_w, m % conv_w) and K index
@@ -174,16 +176,16 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     iris_gemm_problem_t pr = P.p[pi];
     int t = L - P.tile_start[pi];
     int kt0 = 0;   /* first K step of this block's chunk (split-K convolution) */
-    if (P.splits > 1) {
-        const int per = P.tiles_m[0] * P.tiles_n[0];
+    if (P.chunks[pi] > 1) {
+        const int per = P.tiles_m[pi] * P.tiles_n[pi];
         const int chunk = t / per;
-        const int k0 = chunk * P.kchunk;
+        const int k0 = chunk * P.kchunk[pi];
         t -= chunk * per;
         if (CONV) kt0 = k0 / BK;
         else pr.A += k0;
         pr.W += k0;
-        pr.K = min(P.kchunk, pr.K - k0);
-        pr.out = P.ws + chunk * P.ws_stride;
+        pr.K = min(P.kchunk[pi], pr.K - k0);
+        pr.out = P.ws[pi] + chunk * P.ws_stride[pi];
         pr.ldo = pr.N;
         pr.vec = nullptr;
         pr.epi = IRIS_EPI_F32;
@@ -560,15 +562,90 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
 }
 
-/* Sum of the split-K partials in chunk order (deterministic), then the
- * problem's epilogue. One thread per output element. */
-__global__ void splitk_reduce_kernel(const iris_gemm_problem_t p, const float *ws, long long stride, int splits) {
+/* Split-K partials of up to MAXP problems, reduced in one launch: each
+ * output element is the sum of its problem's partials in chunk order
+ * (deterministic), then that problem's epilogue. A thread takes VW = vw[i]
+ * consecutive output elements of a row (4 where the partial rows, the output
+ * and the bias allow 16-byte accesses, else 1); each element gets the same
+ * additions either way. */
+struct ReduceParams {
+    iris_gemm_problem_t p[MAXP];
+    const float *ws[MAXP];
+    long long stride[MAXP];
+    int chunks[MAXP], vw[MAXP];
+    long long start[MAXP + 1];   /* first work item of each problem; start[n] = all */
+    int n;
+};
+
+__global__ void splitk_reduce_kernel(const ReduceParams R) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= R.start[R.n]) return;
+    int pi = 0;
+#pragma unroll
+    for (int j = 1; j < MAXP; j++)
+        if (j < R.n && i >= R.start[j]) pi = j;
+    const iris_gemm_problem_t p = R.p[pi];
+    const float *ws = R.ws[pi];
+    const long long stride = R.stride[pi];
+    const int splits = R.chunks[pi];
     const int nout = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.N;
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)p.M * nout) return;
-    const int m = (int)(i / nout), c = (int)(i % nout);
+    if (R.vw[pi] == 4) {
+        const long long e = (i - R.start[pi]) * 4;
+        const int m = (int)(e / nout), c = (int)(e % nout);
+        if (p.epi == IRIS_EPI_SWIGLU) {
+            /* W rows interleaved in 32-row gate / up groups; c % 4 == 0 keeps
+             * the four columns in one group */
+            const int gc = (c >> 5) * 64 + (c & 31);
+            float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
+            for (int k = 0; k < splits; k++) {
+                const float *row = ws + k * stride + (size_t)m * p.N;
+                const float4 a = *(const float4 *)(row + gc), b = *(const float4 *)(row + gc + 32);
+                g.x += a.x; g.y += a.y; g.z += a.z; g.w += a.w;
+                u.x += b.x; u.y += b.y; u.z += b.z; u.w += b.w;
+            }
+            *(uint2 *)((uint16_t *)p.out + (size_t)m * p.ldo + c) =
+                make_uint2((uint32_t)f2bf_hw(silu_fast(g.x) * u.x) | ((uint32_t)f2bf_hw(silu_fast(g.y) * u.y) << 16),
+                           (uint32_t)f2bf_hw(silu_fast(g.z) * u.z) | ((uint32_t)f2bf_hw(silu_fast(g.w) * u.w) << 16));
+            return;
+        }
+        float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int k = 0; k < splits; k++) {
+            const float4 a = *(const float4 *)(ws + k * stride + (size_t)m * p.N + c);
+            s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
+        }
+        const float vd = p.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f;
+        const float4 v = p.vec ? *(const float4 *)(p.vec + c) : make_float4(vd, vd, vd, vd);
+        const size_t o = (size_t)m * p.ldo + c;
+        switch (p.epi) {
+        case IRIS_EPI_F32:
+            *(float4 *)((float *)p.out + o) = make_float4(s.x + v.x, s.y + v.y, s.z + v.z, s.w + v.w);
+            break;
+        case IRIS_EPI_BF16:
+            *(uint2 *)((uint16_t *)p.out + o) =
+                make_uint2((uint32_t)f2bf_hw(s.x + v.x) | ((uint32_t)f2bf_hw(s.y + v.y) << 16),
+                           (uint32_t)f2bf_hw(s.z + v.z) | ((uint32_t)f2bf_hw(s.w + v.w) << 16));
+            break;
+        case IRIS_EPI_GATED_ADD: {
+            float4 *dst = (float4 *)((float *)p.out + o);
+            float4 y = *dst;
+            y.x += v.x * s.x; y.y += v.y * s.y; y.z += v.z * s.z; y.w += v.w * s.w;
+            *dst = y;
+            break;
+        }
+        case IRIS_EPI_ADD: {
+            float4 *dst = (float4 *)((float *)p.out + o);
+            float4 y = *dst;
+            y.x += s.x + v.x; y.y += s.y + v.y; y.z += s.z + v.z; y.w += s.w + v.w;
+            *dst = y;
+            break;
+        }
+        default: break;
+        }
+        return;
+    }
+    const long long e = i - R.start[pi];
+    const int m = (int)(e / nout), c = (int)(e % nout);
     if (p.epi == IRIS_EPI_SWIGLU) {
-        /* W rows interleaved in 32-row gate / up groups */
         const int gc = (c >> 5) * 64 + (c & 31);
         float g = 0.0f, u = 0.0f;
         for (int k = 0; k < splits; k++) {
@@ -588,6 +665,32 @@ __global__ void splitk_reduce_kernel(const iris_gemm_problem_t p, const float *w
     case IRIS_EPI_ADD: ((float *)p.out)[(size_t)m * p.ldo + c] += s + (p.vec ? p.vec[c] : 0.0f); break;
     default: break;
     }
+}
+
+/* the reduce launch over the split problems of a launch (n of them) */
+int launch_reduce(const iris_gemm_problem_t *ps, float *const *ws, const long long *stride, const int *chunks, int n) {
+    ReduceParams R;
+    memset(&R, 0, sizeof(R));
+    R.n = n;
+    long long items = 0;
+    for (int i = 0; i < n; i++) {
+        const iris_gemm_problem_t &p = ps[i];
+        R.p[i] = p;
+        R.ws[i] = ws[i];
+        R.stride[i] = stride[i];
+        R.chunks[i] = chunks[i];
+        const int nout = p.epi == IRIS_EPI_SWIGLU ? p.N / 2 : p.N;
+        const int ob = p.epi == IRIS_EPI_BF16 || p.epi == IRIS_EPI_SWIGLU ? 8 : 16;
+        const bool v4 = p.epi != IRIS_EPI_F32_T && nout % 4 == 0 && p.N % 4 == 0 && p.ldo % 4 == 0 &&
+                        ((uintptr_t)p.out % ob) == 0 && ((uintptr_t)p.vec % 16) == 0 && ((uintptr_t)ws[i] % 16) == 0;
+        R.vw[i] = v4 ? 4 : 1;
+        R.start[i] = items;
+        items += (long long)p.M * nout / R.vw[i];
+    }
+    for (int i = n; i <= MAXP; i++) R.start[i] = items;
+    if (items == 0) return 0;
+    IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, iris_stream(), R);
+    return iris_launch_check("splitk_reduce_kernel");
 }
 
 int check_problem(const iris_gemm_problem_t &p) {
@@ -617,60 +720,98 @@ int check_problem(const iris_gemm_problem_t &p) {
 
 }  // namespace
 
-extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) {
-    if (n < 1 || n > MAXP) return iris_set_error("gemm: %d problems (1..%d)", n, MAXP);
+namespace {
+
+/* One launch of up to MAXP problems. want[i] > 1 (want may be NULL) splits
+ * problem i over K into that many chunks of whole K steps: its f32 partials
+ * go to the workspace (after those of the split problems before it) and one
+ * reduce launch after the GEMM sums them and applies the epilogues. Tiles
+ * are 256 wide, or 224 wide (plain GEMM, no SwiGLU output written by the
+ * tiles) when that needs fewer rounds of tile widths: with one block per CU
+ * a launch takes ceil(blocks / CUs) rounds, each as long as one tile's width.
+ * The tile width does not change any output element's accumulation order. */
+int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float *ws, size_t ws_bytes) {
+    if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm: %d problems (1..%d)", n, MAXP);
     GemmParams P;
     memset(&P, 0, sizeof(P));
     P.nprob = n;
-    int total = 0;
+    bool seg2 = false, swiglu_tiles = false, split = false;
+    size_t ws_used = 0;
     for (int i = 0; i < n; i++) {
         const iris_gemm_problem_t &p = probs[i];
         P.p[i] = p;
-        P.tile_start[i] = total;
-        if (p.M <= 0 || p.N <= 0) { P.tiles_m[i] = P.tiles_n[i] = 0; continue; }
+        P.chunks[i] = 1;
+        if (p.M <= 0 || p.N <= 0) continue;
         if (check_problem(p)) return -1;
         P.tiles_m[i] = (p.M + BM - 1) / BM;
-        P.tiles_n[i] = (p.N + BN - 1) / BN;
-        total += P.tiles_m[i] * P.tiles_n[i];
+        if (want && want[i] > 1) {
+            const int nk = p.K / BK;
+            const int kchunk = (nk + want[i] - 1) / want[i] * BK;
+            const int chunks = (p.K + kchunk - 1) / kchunk;
+            /* K of one step leaves one chunk: that is the plain product */
+            if (chunks > 1) {
+                if (p.K2) return iris_set_error("gemm_splitk: no second K segment");
+                P.chunks[i] = chunks;
+                P.kchunk[i] = kchunk;
+                P.ws_stride[i] = (long long)p.M * p.N;
+                P.ws[i] = ws + ws_used / sizeof(float);
+                ws_used += (size_t)chunks * P.ws_stride[i] * sizeof(float);
+                split = true;
+            }
+        }
+        seg2 = seg2 || p.K2 > 0;
+        swiglu_tiles = swiglu_tiles || (p.epi == IRIS_EPI_SWIGLU && P.chunks[i] == 1);
+    }
+    if (split && (!ws || ((uintptr_t)ws & 15) || ws_used > ws_bytes))
+        return iris_set_error("gemm_splitk: workspace of %zu bytes for %zu bytes of f32 partials", ws_bytes, ws_used);
+    long long t256 = 0, t224 = 0;
+    for (int i = 0; i < n; i++) {
+        if (!P.tiles_m[i]) continue;
+        t256 += (long long)P.tiles_m[i] * ((probs[i].N + 255) / 256) * P.chunks[i];
+        t224 += (long long)P.tiles_m[i] * ((probs[i].N + 223) / 224) * P.chunks[i];
+    }
+    if (t256 == 0) return 0;
+    int bnt = BN;
+    const int cus = iris_cu_count();
+    if (!seg2 && !swiglu_tiles && cus > 0) {
+        const long long w256 = (t256 + cus - 1) / cus * BN, w224 = (t224 + cus - 1) / cus * 224;
+        if (w224 * 100 < w256 * 97) bnt = 224;
+    }
+    int total = 0;
+    for (int i = 0; i < n; i++) {
+        P.tile_start[i] = total;
+        if (!P.tiles_m[i]) continue;
+        P.tiles_n[i] = (probs[i].N + bnt - 1) / bnt;
+        total += P.tiles_m[i] * P.tiles_n[i] * P.chunks[i];
     }
     for (int i = n; i <= MAXP; i++) P.tile_start[i] = total;
-    if (total == 0) return 0;
     P.total = total;
     P.per_xcd = (total + 7) / 8;
-    bool seg2 = false, swiglu = false;
-    for (int i = 0; i < n; i++) {
-        seg2 = seg2 || probs[i].K2 > 0;
-        swiglu = swiglu || probs[i].epi == IRIS_EPI_SWIGLU;
-    }
-    /* 224-wide tiles when they need fewer rounds of tile-widths: with one
-     * block per CU a launch takes ceil(tiles / CUs) rounds, each as long as
-     * one tile's width */
-    const int cus = iris_cu_count();
-    if (!seg2 && !swiglu && cus > 0) {
-        int t224 = 0;
-        for (int i = 0; i < n; i++)
-            if (P.tiles_m[i]) t224 += P.tiles_m[i] * ((probs[i].N + 223) / 224);
-        const long long w256 = (long long)((total + cus - 1) / cus) * BN;
-        const long long w224 = (long long)((t224 + cus - 1) / cus) * 224;
-        if (w224 * 100 < w256 * 97) {
-            for (int i = 0, acc = 0; i < n; i++) {
-                P.tile_start[i] = acc;
-                if (P.tiles_m[i]) P.tiles_n[i] = (probs[i].N + 223) / 224;
-                acc += P.tiles_m[i] * P.tiles_n[i];
-            }
-            for (int i = n; i <= MAXP; i++) P.tile_start[i] = t224;
-            P.total = t224;
-            P.per_xcd = (t224 + 7) / 8;
-            IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
-            return iris_launch_check("gemm_bf16_kernel");
-        }
-    }
-    if (seg2)
+    if (bnt == 224)
+        IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    else if (seg2)
         IRIS_LAUNCH(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     else
         IRIS_LAUNCH(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
-    return iris_launch_check("gemm_bf16_kernel");
+    if (iris_launch_check("gemm_bf16_kernel")) return -1;
+    if (!split) return 0;
+    iris_gemm_problem_t rp[MAXP];
+    float *rws[MAXP];
+    long long rstride[MAXP];
+    int rchunks[MAXP], nr = 0;
+    for (int i = 0; i < n; i++)
+        if (P.chunks[i] > 1) {
+            rp[nr] = probs[i];
+            rws[nr] = P.ws[i];
+            rstride[nr] = P.ws_stride[i];
+            rchunks[nr++] = P.chunks[i];
+        }
+    return launch_reduce(rp, rws, rstride, rchunks, nr);
 }
+
+}  // namespace
+
+extern "C" int iris_hip_gemm(const iris_gemm_problem_t *probs, int n) { return launch_gemm(probs, n, nullptr, nullptr, 0); }
 
 /* Split-K partials without a caller workspace: a file-scope device array of
  * IRIS_NOALLOC_SCRATCH_BYTES, held by each GPU the library runs on until the
@@ -712,6 +853,8 @@ extern "C" int iris_hip_gemm_splitk_noalloc(const iris_gemm_problem_t *p, int sp
     const int nk = p->K / BK;
     const int kchunk = (nk + splits - 1) / splits * BK;
     const size_t chunks = (size_t)((p->K + kchunk - 1) / kchunk);
+    /* one chunk is the plain product, which needs no scratch */
+    if (chunks <= 1) return iris_hip_gemm(p, 1);
     const size_t need = chunks * (size_t)p->M * (size_t)p->N * sizeof(float);
     if (need > IRIS_NOALLOC_SCRATCH_BYTES)
         return iris_set_error("gemm_splitk_noalloc: %zu chunks x %d x %d f32 partials need %zu bytes, the scratch "
@@ -722,56 +865,42 @@ extern "C" int iris_hip_gemm_splitk_noalloc(const iris_gemm_problem_t *p, int sp
 }
 
 extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, float *ws, size_t ws_bytes) {
-    if (splits <= 1) return iris_hip_gemm(p, 1);
-    if (p->M <= 0 || p->N <= 0) return 0;
-    if (check_problem(*p)) return -1;
-    if (p->K2) return iris_set_error("gemm_splitk: no second K segment");
-    const int nk = p->K / BK;
-    const int kchunk = (nk + splits - 1) / splits * BK;
-    const int chunks = (p->K + kchunk - 1) / kchunk;
-    /* K of one step leaves one chunk: that is the plain product (the kernel
-     * applies the epilogue itself and writes no partials to reduce) */
-    if (chunks <= 1) return iris_hip_gemm(p, 1);
-    const long long stride = (long long)p->M * p->N;
-    if (!ws || ((uintptr_t)ws & 15) || (size_t)chunks * stride * sizeof(float) > ws_bytes)
-        return iris_set_error("gemm_splitk: workspace of %zu bytes for %d x %d x %d f32", ws_bytes, chunks, p->M,
-                              p->N);
-    GemmParams P;
-    memset(&P, 0, sizeof(P));
-    P.nprob = 1;
-    P.p[0] = *p;
-    P.tiles_m[0] = (p->M + BM - 1) / BM;
-    P.tiles_n[0] = (p->N + BN - 1) / BN;
-    P.total = P.tiles_m[0] * P.tiles_n[0] * chunks;
-    for (int i = 1; i <= MAXP; i++) P.tile_start[i] = P.total;
-    P.per_xcd = (P.total + 7) / 8;
-    P.splits = chunks;
-    P.kchunk = kchunk;
-    P.ws = ws;
-    P.ws_stride = stride;
-    IRIS_LAUNCH(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
-    if (iris_launch_check("gemm_bf16_kernel")) return -1;
-    const size_t n_out = (size_t)p->M * (p->epi == IRIS_EPI_SWIGLU ? p->N / 2 : p->N);
-    IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), *p,
-                       ws, stride, chunks);
-    return iris_launch_check("splitk_reduce_kernel");
+    if (!p) return iris_set_error("gemm_splitk: null problem");
+    return launch_gemm(p, 1, &splits, ws, ws_bytes);
+}
+
+extern "C" int iris_hip_gemm_fill_n(const iris_gemm_problem_t *probs, int n, float *ws, size_t ws_bytes) {
+    if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm_fill: %d problems (1..%d)", n, MAXP);
+    const int cus = iris_cu_count();
+    long long tiles = 0;
+    size_t per = 0;
+    int min_nk = 1 << 30;
+    bool seg2 = false;
+    for (int i = 0; i < n; i++) {
+        const iris_gemm_problem_t &p = probs[i];
+        if (p.M <= 0 || p.N <= 0) continue;
+        tiles += (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+        per += (size_t)p.M * (size_t)p.N * sizeof(float);
+        min_nk = std::min(min_nk, p.K / BK);
+        seg2 = seg2 || p.K2 > 0;
+    }
+    /* tiles filling at most half of the CUs and a long K: split K into up to
+     * CUs / tiles chunks of at least 4 K steps, as many as the workspace holds */
+    if (tiles > 0 && !seg2 && cus > 0 && ws && 2 * tiles <= cus && min_nk >= 8) {
+        int splits = (int)std::min<long long>(cus / tiles, min_nk / 4);
+        while (splits > 1 && (size_t)splits * per > ws_bytes) splits--;
+        if (splits > 1) {
+            int want[MAXP];
+            for (int i = 0; i < n; i++) want[i] = splits;
+            return launch_gemm(probs, n, want, ws, ws_bytes);
+        }
+    }
+    return launch_gemm(probs, n, nullptr, nullptr, 0);
 }
 
 extern "C" int iris_hip_gemm_fill(const iris_gemm_problem_t *p, float *ws, size_t ws_bytes) {
     if (!p) return iris_set_error("gemm_fill: null problem");
-    if (p->M <= 0 || p->N <= 0) return 0;
-    const int cus = iris_cu_count();
-    const long long tiles = (long long)((p->M + BM - 1) / BM) * ((p->N + BN - 1) / BN);
-    const int nk = p->K / BK;
-    /* tiles filling less than half of the CUs and a long K: split K into up to
-     * CUs / tiles chunks of at least 4 K steps, as many as the workspace holds */
-    if (p->K2 == 0 && cus > 0 && ws && 2 * tiles <= cus && nk >= 8) {
-        int splits = (int)std::min<long long>(cus / tiles, nk / 4);
-        const size_t per = (size_t)p->M * (size_t)p->N * sizeof(float);
-        while (splits > 1 && (size_t)splits * per > ws_bytes) splits--;
-        if (splits > 1) return iris_hip_gemm_splitk(p, splits, ws, ws_bytes);
-    }
-    return iris_hip_gemm(p, 1);
+    return iris_hip_gemm_fill_n(p, 1, ws, ws_bytes);
 }
 
 extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
@@ -816,10 +945,11 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     P.conv_in_bytes = (unsigned)in_bytes;
     int chunks = 1;
     long long stride = 0;
+    P.chunks[0] = 1;
     if (c->splits > 1) {
         const int nk = p.K / BK;
-        P.kchunk = (nk + c->splits - 1) / c->splits * BK;
-        chunks = (p.K + P.kchunk - 1) / P.kchunk;
+        P.kchunk[0] = (nk + c->splits - 1) / c->splits * BK;
+        chunks = (p.K + P.kchunk[0] - 1) / P.kchunk[0];
         stride = (long long)p.M * p.N;
         if (!c->ws || ((uintptr_t)c->ws & 15) || (size_t)chunks * stride * sizeof(float) > c->ws_bytes)
             return iris_set_error("conv3x3: split-K workspace of %zu bytes for %d x %d x %d f32", c->ws_bytes, chunks,
@@ -829,9 +959,9 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     for (int i = 1; i <= MAXP; i++) P.tile_start[i] = P.total;
     P.per_xcd = (P.total + 7) / 8;
     if (chunks > 1) {
-        P.splits = chunks;
-        P.ws = c->ws;
-        P.ws_stride = stride;
+        P.chunks[0] = chunks;
+        P.ws[0] = c->ws;
+        P.ws_stride[0] = stride;
     }
     if (c->up == 2)
         IRIS_LAUNCH(gemm_bf16_kernel<2>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
@@ -839,8 +969,6 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
         IRIS_LAUNCH(gemm_bf16_kernel<1>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel<conv>")) return -1;
     if (chunks == 1) return 0;
-    const size_t n_out = (size_t)p.M * p.N;
-    IRIS_LAUNCH(splitk_reduce_kernel, dim3((unsigned)((n_out + 255) / 256)), dim3(256), 0, iris_stream(), p,
-                       c->ws, stride, chunks);
-    return iris_launch_check("splitk_reduce_kernel");
+    float *rws = c->ws;
+    return launch_reduce(&p, &rws, &stride, &chunks, 1);
 }

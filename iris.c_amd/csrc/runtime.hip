@@ -11,6 +11,7 @@
 #include <thread>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 static int g_init = 0;
@@ -73,6 +74,9 @@ int iris_hip_init(int device) {
     g_cus = p.multiProcessorCount;
     g_device = device;
     g_init = 1;
+    /* the per-kernel profile from the start (iris_print_blas_profile reports it) */
+    const char *prof = getenv("IRIS_PROFILE");
+    if (prof && atoi(prof) > 0) return iris_hip_profile_enable(1);
     return 0;
 }
 

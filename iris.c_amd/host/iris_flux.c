@@ -69,7 +69,7 @@ typedef struct {
     float *nq, *nk;
 } dev_single_t;
 
-/* split-K partials of one product on few rows (iris_hip_gemm_fill picks the
+/* split-K partials of the products on few rows (iris_hip_gemm_fill_n picks the
  * chunk count that fits) */
 #define FILL_WS_BYTES ((size_t)64 << 20)
 
@@ -111,7 +111,7 @@ typedef struct {
                               * it into pinned slots before iris_hip_memcpy_h2d returns) */
     void *attn_ws;           /* the attention's balanced-schedule workspace (zeroed) */
     size_t attn_ws_bytes;
-    float *fill_ws;          /* split-K partials of the products on few rows (iris_hip_gemm_fill) */
+    float *fill_ws;          /* split-K partials of the products on few rows (iris_hip_gemm_fill_n) */
     void *graph;
 } work_t;
 
@@ -684,10 +684,10 @@ fail:
 #define CK(x) do { if ((x) != 0) return -1; } while (0)
 
 static int gemm(const iris_gemm_problem_t *p, int n) { return iris_hip_gemm(p, n); }
-/* one product on few rows: split-K through the forward's workspace when its
- * tiles leave most of the chip idle */
-static int gemm_fill(iris_transformer_t *tf, const iris_gemm_problem_t *p) {
-    return iris_hip_gemm_fill(p, tf->w.fill_ws, FILL_WS_BYTES);
+/* products on few rows (one launch of n problems): split-K through the
+ * forward's workspace when their tiles leave most of the chip idle */
+static int gemm_fill(iris_transformer_t *tf, const iris_gemm_problem_t *p, int n) {
+    return iris_hip_gemm_fill_n(p, n, tf->w.fill_ws, FILL_WS_BYTES);
 }
 
 static iris_gemm_problem_t prob(const void *A, int lda, const uint16_t *W, int ldw, void *out, int ldo,
@@ -805,7 +805,7 @@ static int double_block_forward(iris_transformer_t *tf, int i) {
                     IRIS_EPI_GATED_ADD);
         lora_seg(tf, &p[n++], l_ip, r0 + T, 0);
     }
-    CK(gemm(p, n));
+    CK(gemm_fill(tf, p, n));
     /* AdaLN (shift2, scale2) -> SwiGLU FFN -> gated residual (gate2) */
     CK(adaln(tf, mt + 3 * h, mt + 4 * h, mi + 3 * h, mi + 4 * h, T));
     n = 0;
@@ -824,7 +824,7 @@ static int double_block_forward(iris_transformer_t *tf, int i) {
         p[n++] = prob(w->cat + (r0 + T) * hm + h, hm, bw->img_down, mlp, w->x + (r0 + T) * h, h, mi + 5 * h, I, h, mlp,
                       IRIS_EPI_GATED_ADD);
     }
-    CK(gemm(p, n));
+    CK(gemm_fill(tf, p, n));
     return 0;
 }
 
@@ -855,18 +855,20 @@ static int single_block_forward(iris_transformer_t *tf, int i) {
         CK(iris_hip_fork());
         iris_hip_side(1);
     }
-    const int rc_mlp = gemm(&p[1], 1);
+    /* once forked, the side stream is joined whatever fails after the fork
+     * (an unjoined fork would leave a graph capture unable to end) */
+    int rc = gemm(&p[1], 1);
     iris_hip_side(0);
-    CK(rc_mlp);
-    CK(gemm(&p[0], 1));
-    CK(kv_prepare(tf, bw->nk, bw->nk, w->S, 1));
-    CK(attention(tf, bw->nq, bw->nq, w->S, w->cat, hm));
-    if (side) CK(iris_hip_join());
+    if (!rc) rc = gemm(&p[0], 1);
+    if (!rc) rc = kv_prepare(tf, bw->nk, bw->nk, w->S, 1);
+    if (!rc) rc = attention(tf, bw->nq, bw->nq, w->S, w->cat, hm);
+    if (side && iris_hip_join() && !rc) rc = -1;
+    CK(rc);
     /* [attn | mlp] . W_out^T, gated residual */
     CK(lora_down(tf, l2, w->cat, hm, 0, BS));
     p[0] = prob(w->cat, hm, bw->out, hm, w->x, h, ms + 2 * h, BS, h, hm, IRIS_EPI_GATED_ADD);
     lora_seg(tf, &p[0], l2, 0, 0);
-    CK(gemm(p, 1));
+    CK(gemm_fill(tf, p, 1));
     return 0;
 }
 
@@ -904,7 +906,7 @@ static int enqueue_forward(iris_transformer_t *tf) {
     for (int b = 0; b < B; b++) {
         p[0] = prob(w->txtb + (size_t)b * T * td, td, tf->txt_in, td, w->x + (size_t)b * S * h, h, NULL, T, h, td,
                     IRIS_EPI_F32);
-        CK(gemm_fill(tf, p));
+        CK(gemm_fill(tf, p, 1));
     }
     for (int i = 0; i < tf->n_double; i++) CK(double_block_forward(tf, i));
     for (int i = 0; i < tf->n_single; i++) CK(single_block_forward(tf, i));
@@ -921,7 +923,7 @@ static int enqueue_forward(iris_transformer_t *tf) {
         CK(iris_hip_rownorm(&a));
         p[0] = prob(w->a + (size_t)b * I0 * h, h, tf->proj_out, h, w->vel + (size_t)b * C * I0, I0, NULL, I0, C, h,
                     IRIS_EPI_F32_T);
-        CK(gemm_fill(tf, p));
+        CK(gemm_fill(tf, p, 1));
     }
     return 0;
 }
@@ -1364,7 +1366,16 @@ iris_transformer_t *iris_transformer_load(FILE *f) {
  * breakdown becomes the per-kernel table of the library's profile (eager
  * steps with an event pair around every launch). reset starts a profile,
  * print writes the table to stderr and leaves the profile running. */
-void iris_reset_blas_profile(void) { iris_hip_profile_enable(1); }
+/* The reference zeroes its cumulative counters here
+ * (iris_transformer_flux.c:73-77). Here the counters are the per-kernel
+ * records of iris_hip_profile_enable, which is also what turns them on (and
+ * makes the forward run launch by launch instead of replaying its graph);
+ * this call only clears them, and leaves the execution mode as it is. With
+ * IRIS_PROFILE=1 in the environment the library starts with the profile on,
+ * for callers written against the reference's interface. */
+void iris_reset_blas_profile(void) {
+    if (iris_hip_profile_enabled()) iris_hip_profile_enable(1);
+}
 
 void iris_print_blas_profile(void) {
     if (!iris_hip_profile_enabled()) return;

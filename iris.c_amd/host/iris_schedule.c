@@ -22,6 +22,13 @@
  * reference build's schedule; the lane classes follow the element count, not
  * the CPU. The file is compiled with -ffp-contract=off so that only the fused
  * operations written here are fused.
+ *
+ * The vector lanes need AVX2 and FMA, as the reference's -march=native build
+ * does on the hosts whose bits it reproduces. On a CPU without them every
+ * element takes the scalar formula (the build's scalar tail), checked once
+ * per process with __builtin_cpu_supports; the values then equal the
+ * reference formulas evaluated in plain IEEE float (the reference build's
+ * scalar tail), not its vector lanes.
  */
 #include "../../include/iris_sample.h"
 
@@ -35,6 +42,19 @@ __m256 _ZGVdN8vv_powf(__m256, __m256);
 __m128 _ZGVbN4vv_powf(__m128, __m128);
 
 #define VEC __attribute__((target("avx2,fma")))
+
+/* the vector lanes run only where the CPU has AVX2 and FMA
+ * (IRIS_SCHEDULE_SCALAR=1 in the environment takes the scalar formulas
+ * everywhere, as on a CPU without them) */
+static int vec_ok(void) {
+    static int ok = -1;
+    if (ok < 0) {
+        const char *e = getenv("IRIS_SCHEDULE_SCALAR");
+        __builtin_cpu_init();
+        ok = !(e && atoi(e) > 0) && __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma");
+    }
+    return ok;
+}
 
 /* elements handled 8-wide, then 4-wide, before the scalar tail */
 static void lane_plan(int count, int *n8, int *n4) {
@@ -64,7 +84,7 @@ static float *alloc_sched(int num_steps) {
 }
 
 /* iris_linear_schedule (:61-68): 1 - i * (1 / n), fused, in every lane class */
-VEC float *iris_linear_schedule(int num_steps) {
+float *iris_linear_schedule(int num_steps) {
     float *s = alloc_sched(num_steps);
     if (!s) return NULL;
     const float inv = 1.0f / (float)num_steps;
@@ -73,10 +93,7 @@ VEC float *iris_linear_schedule(int num_steps) {
 }
 
 /* iris_power_schedule (:75-84): 1 - powf(i * (1 / n), alpha) */
-VEC float *iris_power_schedule(int num_steps, float alpha) {
-    float *s = alloc_sched(num_steps);
-    if (!s) return NULL;
-    const float inv = 1.0f / (float)num_steps;
+VEC static int power_lanes(float *s, int num_steps, float inv, float alpha) {
     int n8, n4, i = 0;
     lane_plan(num_steps + 1, &n8, &n4);
     for (; i < n8; i += 8)
@@ -88,6 +105,14 @@ VEC float *iris_power_schedule(int num_steps, float alpha) {
                                                                           _mm_set1_ps(alpha))));
         i += 4;
     }
+    return i;
+}
+
+float *iris_power_schedule(int num_steps, float alpha) {
+    float *s = alloc_sched(num_steps);
+    if (!s) return NULL;
+    const float inv = 1.0f / (float)num_steps;
+    int i = vec_ok() ? power_lanes(s, num_steps, inv, alpha) : 0;
     for (; i <= num_steps; i++) s[i] = 1.0f - powf((float)i * inv, alpha);
     return s;
 }
@@ -95,10 +120,7 @@ VEC float *iris_power_schedule(int num_steps, float alpha) {
 /* iris_sigmoid_schedule (:90-107): 1 - 1 / (1 + expf(-((t - 0.5) * 10 + shift)))
  * with t = i * (1 / n); the exponent's argument is one fused
  * -((t - 0.5) * 10) - shift, itself from t - 0.5 = fma(i, 1/n, -0.5) */
-VEC float *iris_sigmoid_schedule(int num_steps, float shift) {
-    float *s = alloc_sched(num_steps);
-    if (!s) return NULL;
-    const float inv = 1.0f / (float)num_steps;
+VEC static int sigmoid_lanes(float *s, int num_steps, float inv, float shift) {
     int n8, n4, i = 0;
     lane_plan(num_steps + 1, &n8, &n4);
     for (; i < n8; i += 8) {
@@ -114,6 +136,14 @@ VEC float *iris_sigmoid_schedule(int num_steps, float shift) {
         _mm_storeu_ps(s + i, _mm_sub_ps(_mm_set1_ps(1.0f), rcp_nr4(d)));
         i += 4;
     }
+    return i;
+}
+
+float *iris_sigmoid_schedule(int num_steps, float shift) {
+    float *s = alloc_sched(num_steps);
+    if (!s) return NULL;
+    const float inv = 1.0f / (float)num_steps;
+    int i = vec_ok() ? sigmoid_lanes(s, num_steps, inv, shift) : 0;
     for (; i <= num_steps; i++) {
         const float tm = fmaf((float)i, inv, -0.5f);
         const float e = expf(-fmaf(tm, 10.0f, shift));
@@ -126,14 +156,7 @@ VEC float *iris_sigmoid_schedule(int num_steps, float shift) {
 
 /* iris_resolution_schedule (:113-136): 1 - powf(i * (1 / n), 1 + shift / 2)
  * for i >= 1 (the loop from i = 1 is the vectorized one), s[0] = 1 */
-VEC float *iris_resolution_schedule(int num_steps, int height, int width) {
-    float *s = alloc_sched(num_steps);
-    if (!s) return NULL;
-    const int pixels = height * width;
-    const float ex = pixels >= 1024 * 1024 ? 1.5f : pixels >= 512 * 512 ? 1.25f : 1.0f;
-    s[0] = 1.0f;
-    if (num_steps == 0) return s;
-    const float inv = 1.0f / (float)num_steps;
+VEC static int resolution_lanes(float *s, int num_steps, float inv, float ex) {
     int n8, n4, k = 0;
     lane_plan(num_steps, &n8, &n4);
     for (; k < n8; k += 8)
@@ -146,6 +169,18 @@ VEC float *iris_resolution_schedule(int num_steps, int height, int width) {
                                                            _mm_set1_ps(ex))));
         k += 4;
     }
+    return k;
+}
+
+float *iris_resolution_schedule(int num_steps, int height, int width) {
+    float *s = alloc_sched(num_steps);
+    if (!s) return NULL;
+    const int pixels = height * width;
+    const float ex = pixels >= 1024 * 1024 ? 1.5f : pixels >= 512 * 512 ? 1.25f : 1.0f;
+    s[0] = 1.0f;
+    if (num_steps == 0) return s;
+    const float inv = 1.0f / (float)num_steps;
+    int k = vec_ok() ? resolution_lanes(s, num_steps, inv, ex) : 0;
     for (; k < num_steps; k++) s[1 + k] = 1.0f - powf((float)(1 + k) * inv, ex);
     return s;
 }
@@ -166,11 +201,7 @@ static float empirical_mu(int seq, int n) {
  * (0, 1), e^mu / (e^mu + (1 / t - 1)); t >= 1 gives 1 and t <= 0 gives 0.
  * 8-wide lanes: e * rcp_nr(rcp_nr(t) + (e - 1)); 4-wide lanes:
  * e * rcp_nr((rcp_nr(t) - 1) + e); scalar: e / ((1 / t - 1) + e). */
-VEC float *iris_official_schedule(int num_steps, int image_seq_len) {
-    float *s = alloc_sched(num_steps);
-    if (!s) return NULL;
-    const float mu = empirical_mu(image_seq_len, num_steps);
-    const float inv = 1.0f / (float)num_steps;
+VEC static int official_lanes(float *s, int num_steps, float inv, float mu) {
     int n8, n4, i = 0;
     lane_plan(num_steps + 1, &n8, &n4);
     float u[8], v[8];
@@ -194,6 +225,15 @@ VEC float *iris_official_schedule(int num_steps, int image_seq_len) {
         for (int j = 0; j < 4; j++) s[i + j] = u[j] >= 1.0f ? 0.0f : u[j] <= 0.0f ? 1.0f : v[j];
         i += 4;
     }
+    return i;
+}
+
+float *iris_official_schedule(int num_steps, int image_seq_len) {
+    float *s = alloc_sched(num_steps);
+    if (!s) return NULL;
+    const float mu = empirical_mu(image_seq_len, num_steps);
+    const float inv = 1.0f / (float)num_steps;
+    int i = vec_ok() ? official_lanes(s, num_steps, inv, mu) : 0;
     for (; i <= num_steps; i++) {
         const float uu = (float)i * inv;
         if (uu >= 1.0f) s[i] = 0.0f;
@@ -210,7 +250,26 @@ VEC float *iris_official_schedule(int num_steps, int image_seq_len) {
  * (fused), shifted as shift raw / (1 + (shift - 1) raw) with the denominator
  * fused, then a terminal 0; smin = shift / 1000 / (1 + (shift - 1) / 1000).
  * The shift is 3, or IRIS_ZIMAGE_SHIFT when that parses to a positive value. */
-VEC float *iris_zimage_schedule(int num_steps, int image_seq_len) {
+VEC static int zimage_lanes(float *s, int num_steps, float c, float shift, float sm1) {
+    int n8, n4, i = 0;
+    lane_plan(num_steps, &n8, &n4);
+    for (; i < n8; i += 8) {
+        const __m256 raw = _mm256_fmadd_ps(iota8(i), _mm256_set1_ps(c), _mm256_set1_ps(1.0f));
+        const __m256 num = _mm256_mul_ps(raw, _mm256_set1_ps(shift));
+        const __m256 den = _mm256_fmadd_ps(raw, _mm256_set1_ps(sm1), _mm256_set1_ps(1.0f));
+        _mm256_storeu_ps(s + i, _mm256_mul_ps(num, rcp_nr8(den)));
+    }
+    if (n4) {
+        const __m128 raw = _mm_fmadd_ps(iota4(i), _mm_set1_ps(c), _mm_set1_ps(1.0f));
+        const __m128 num = _mm_mul_ps(raw, _mm_set1_ps(shift));
+        const __m128 den = _mm_fmadd_ps(raw, _mm_set1_ps(sm1), _mm_set1_ps(1.0f));
+        _mm_storeu_ps(s + i, _mm_mul_ps(num, rcp_nr4(den)));
+        i += 4;
+    }
+    return i;
+}
+
+float *iris_zimage_schedule(int num_steps, int image_seq_len) {
     (void)image_seq_len;
     float *s = alloc_sched(num_steps);
     if (!s) return NULL;
@@ -227,21 +286,7 @@ VEC float *iris_zimage_schedule(int num_steps, int image_seq_len) {
             s[0] = 1.0f;
         } else {
             const float c = (smin - 1.0f) * (1.0f / (float)(num_steps - 1));
-            int n8, n4, i = 0;
-            lane_plan(num_steps, &n8, &n4);
-            for (; i < n8; i += 8) {
-                const __m256 raw = _mm256_fmadd_ps(iota8(i), _mm256_set1_ps(c), _mm256_set1_ps(1.0f));
-                const __m256 num = _mm256_mul_ps(raw, _mm256_set1_ps(shift));
-                const __m256 den = _mm256_fmadd_ps(raw, _mm256_set1_ps(sm1), _mm256_set1_ps(1.0f));
-                _mm256_storeu_ps(s + i, _mm256_mul_ps(num, rcp_nr8(den)));
-            }
-            if (n4) {
-                const __m128 raw = _mm_fmadd_ps(iota4(i), _mm_set1_ps(c), _mm_set1_ps(1.0f));
-                const __m128 num = _mm_mul_ps(raw, _mm_set1_ps(shift));
-                const __m128 den = _mm_fmadd_ps(raw, _mm_set1_ps(sm1), _mm_set1_ps(1.0f));
-                _mm_storeu_ps(s + i, _mm_mul_ps(num, rcp_nr4(den)));
-                i += 4;
-            }
+            int i = vec_ok() ? zimage_lanes(s, num_steps, c, shift, sm1) : 0;
             for (; i < num_steps; i++) {
                 const float raw = fmaf((float)i, c, 1.0f);
                 s[i] = (raw * shift) / fmaf(raw, sm1, 1.0f);

@@ -247,6 +247,87 @@ def test_gemm_fill(lib, M, N, K, epi, ws_mb):
     print(f"fill {'split-K' if split else 'plain'}: rel_l2 {tl.rel_l2(outs[0], ref):.2e}")
 
 
+def cu_count(lib):
+    lib.iris_hip_device_name.restype = ctypes.c_char_p
+    return int(lib.iris_hip_device_name().decode().rsplit(",", 1)[1].split()[0])
+
+
+@pytest.mark.parametrize("rows,N,K,epi", [((512, 1024), 3072, 3072, EPI_GATED_ADD),
+                                          ((512, 1024), 3072, 9216, EPI_GATED_ADD),
+                                          ((1536,), 3072, 12288, EPI_GATED_ADD), ((300, 77), 640, 1024, EPI_F32),
+                                          ((200, 130), 512, 2048, EPI_SWIGLU), ((4608,), 3072, 3072, EPI_GATED_ADD)])
+def test_gemm_fill_n(lib, rows, N, K, epi):
+    """iris_hip_gemm_fill_n: the txt and img streams of a 512x512 double
+    block (512 + 1024 rows; out projection K 3072, down projection K 9216)
+    and the single block's out projection (1536 x 3072 x 12288), split over
+    K in one launch of both problems, against float64; bit for bit equal to
+    iris_hip_gemm_splitk of each problem alone with the same chunk count,
+    and repeatable. Also ragged rows with an output row stride that is not a
+    multiple of 4 (the reduce's one-element path), SwiGLU split, and a
+    product that fills the chip (4608 rows: the plain launch, equal to
+    iris_hip_gemm bit for bit)."""
+    rng = np.random.default_rng(sum(rows) + N + K)
+    cus = cu_count(lib)
+    P = tl.GemmProblem
+    nout = N // 2 if epi == EPI_SWIGLU else N
+    ins = []
+    for i, m in enumerate(rows):
+        a = bf(rng.standard_normal((m, K), np.float32))
+        w = bf(rng.standard_normal((N, K), np.float32) * 0.02)
+        vec = rng.standard_normal(N).astype(np.float32)
+        ldo = nout + 2 if (epi == EPI_F32 and i == 1) else nout
+        x0 = rng.standard_normal((m, ldo), np.float32)
+        ins.append((m, a, w, vec, x0, ldo, tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w)), tl.Dev.of(vec)))
+    tiles = sum((m + 255) // 256 for m in rows) * ((N + 255) // 256)
+    splits = min(cus // tiles, K // 64 // 4) if 2 * tiles <= cus else 1
+    ws_bytes = 64 << 20
+    ws = tl.Dev(ws_bytes)
+    lib.iris_hip_gemm_fill_n.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+
+    def run(mode):
+        outs, probs = [], []
+        for m, a, w, vec, x0, ldo, dA, dW, dV in ins:
+            bf16_out = epi == EPI_SWIGLU
+            o = tl.Dev(m * ldo * 2) if bf16_out else tl.Dev.of(x0)
+            probs.append(P(dA.ptr, dW.ptr, o.ptr, dV.ptr if epi != EPI_SWIGLU else None, m, N, K, K, K, ldo, epi))
+            outs.append(o)
+        arr = (P * len(probs))(*probs)
+        if mode == "fill":
+            assert lib.iris_hip_gemm_fill_n(arr, len(probs), ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+        elif mode == "alone":
+            for pr in probs:
+                assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, ws_bytes) == 0, \
+                    lib.iris_hip_last_error()
+        else:
+            assert lib.iris_hip_gemm(arr, len(probs)) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+        res = []
+        for o, (m, a, w, vec, x0, ldo, *_) in zip(outs, ins):
+            res.append(tl.bf16_to_f32(o.get(np.uint16, (m, ldo))) if epi == EPI_SWIGLU else
+                       o.get(np.float32, (m, ldo)))
+            o.close()
+        return res
+
+    got, again = run("fill"), run("fill")
+    for g, g2, (m, a, w, vec, x0, ldo, *_) in zip(got, again, ins):
+        assert np.array_equal(g, g2), "not repeatable"
+        y = a.astype(np.float64) @ w.astype(np.float64).T
+        if epi == EPI_SWIGLU:
+            gt = np.concatenate([y[:, c * 64:c * 64 + 32] for c in range(N // 64)], 1)
+            up = np.concatenate([y[:, c * 64 + 32:c * 64 + 64] for c in range(N // 64)], 1)
+            assert tl.rel_l2(g, gt / (1 + np.exp(-gt)) * up) < 4e-3
+        elif epi == EPI_GATED_ADD:
+            assert tl.rel_l2(g, x0 + vec * y) < 1e-5
+        else:
+            assert tl.rel_l2(g[:, :N], y + vec) < 1e-5
+            assert np.array_equal(g[:, N:], x0[:, N:]), "wrote past N"
+    want = run("alone" if splits > 1 else "plain")
+    for g, w_ in zip(got, want):
+        assert np.array_equal(g, w_), f"differs from the {'split-K' if splits > 1 else 'plain'} launch"
+    print(f"fill_n {rows} x {N} x {K}: {splits} chunks")
+
+
 @pytest.mark.parametrize("shapes,K", [([(4608, 3072)], 1024), ([(512, 9216), (4096, 9216)], 192),
                                       ([(4608, 3840)], 320), ([(700, 3000)], 128)])
 def test_gemm_narrow_tiles(lib, shapes, K):

@@ -145,6 +145,46 @@ def test_schedules_closed_form(prod, fn, args, monkeypatch):
         np.testing.assert_allclose(got, closed_form(fn, n, args), rtol=0, atol=tol, err_msg=f"{fn} n={n}")
 
 
+SCALAR_NS = (1, 2, 3, 4, 5, 7, 8, 9, 12, 20, 28, 50)
+
+
+def test_schedules_scalar_path_closed_form(tmp_path):
+    """The schedules on a CPU without AVX2 / FMA (forced with
+    IRIS_SCHEDULE_SCALAR=1 in a fresh process: the choice is made once per
+    process) take the scalar formulas for every element: within the
+    closed-form tolerances, and within 2e-6 of the vector lanes where those
+    run (their divisions go through a refined reciprocal estimate)."""
+    import subprocess
+    import sys
+    out = tmp_path / "scalar.npz"
+    script = (
+        "import ctypes, numpy as np, sys\n"
+        f"sys.path.insert(0, {os.path.dirname(os.path.abspath(__file__))!r})\n"
+        "import test_host_sampler as t\n"
+        f"lib = ctypes.CDLL({tl.HIP_SO!r})\n"
+        "res = {}\n"
+        "for k, (fn, args) in enumerate(t.SCHED_CASES):\n"
+        "    getattr(lib, fn).restype = ctypes.c_void_p\n"
+        "    for n in t.SCALAR_NS:\n"
+        "        res[f'{k}_{n}'] = t.take(getattr(lib, fn)(n, *args), n + 1)\n"
+        f"np.savez({str(out)!r}, **res)\n")
+    env = dict(os.environ, IRIS_SCHEDULE_SCALAR="1")
+    env.pop("IRIS_ZIMAGE_SHIFT", None)
+    subprocess.run([sys.executable, "-c", script], check=True, env=env, timeout=120)
+    got = np.load(out)
+    lib = ctypes.CDLL(tl.HIP_SO)
+    for k, (fn, args) in enumerate(SCHED_CASES):
+        getattr(lib, fn).restype = ctypes.c_void_p
+        for n in SCALAR_NS:
+            a = got[f"{k}_{n}"]
+            tol = 4e-5 if fn == "iris_official_schedule" else 2e-6
+            np.testing.assert_allclose(a.astype(np.float64), closed_form(fn, n, args), rtol=0, atol=tol,
+                                       err_msg=f"{fn} n={n} (scalar)")
+            v = take(getattr(lib, fn)(n, *args), n + 1)
+            d = np.abs(a.astype(np.float64) - v.astype(np.float64)).max()
+            assert d <= 2e-6, (fn, n, d)
+
+
 @pytest.mark.skipif(not os.path.exists(tl.REF_SO), reason="reference build (oracle/_ref) not present")
 @pytest.mark.parametrize("fn,args", SCHED_CASES, ids=lambda v: str(v))
 def test_schedules_equal_reference_build(prod, fn, args, monkeypatch):
