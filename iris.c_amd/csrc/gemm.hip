@@ -62,6 +62,12 @@ struct GemmParams {
     int chunks[MAXP], kchunk[MAXP];
     float *ws[MAXP];
     long long ws_stride[MAXP];
+    /* two-phase launch: blocks [0, phase_blocks) take tiles [0, phase_tiles)
+     * (phase_blocks = 8 ceil(phase_tiles / 8), XCD-major over that range),
+     * the blocks after them tiles [phase_tiles, total) (XCD-major, per_xcd
+     * each), so the tiles of the first phase are dispatched before any of the
+     * second's. 0: one phase. */
+    int phase_tiles, phase_blocks;
     /* implicit 3x3 convolution (one problem, CONV kernels only): A is the bf16
      * NHWC input of (conv_h >> up) x (conv_w >> up) pixels, 2^cin_bshift bytes
      * per pixel; output row m is pixel (m / conv_w, m % conv_w) and K index
@@ -167,8 +173,15 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     __shared__ __attribute__((aligned(16))) uint16_t lds0[2 * TILE_ELEMS];
     __shared__ __attribute__((aligned(16))) uint16_t lds1[2 * TILE_ELEMS];
     const int b = blockIdx.x;
-    const int L = (b & 7) * P.per_xcd + (b >> 3);
-    if (L >= P.total) return;
+    int L;
+    if (b < P.phase_blocks) {
+        L = (b & 7) * (P.phase_blocks >> 3) + (b >> 3);
+        if (L >= P.phase_tiles) return;
+    } else {
+        const int b2 = b - P.phase_blocks;
+        L = P.phase_tiles + (b2 & 7) * P.per_xcd + (b2 >> 3);
+        if (L >= P.total) return;
+    }
     int pi = 0;
 #pragma unroll
     for (int i = 1; i < MAXP; i++)
@@ -729,8 +742,12 @@ namespace {
  * are 256 wide, or 224 wide (plain GEMM, no SwiGLU output written by the
  * tiles) when that needs fewer rounds of tile widths: with one block per CU
  * a launch takes ceil(blocks / CUs) rounds, each as long as one tile's width.
- * The tile width does not change any output element's accumulation order. */
-int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float *ws, size_t ws_bytes) {
+ * The tile width does not change any output element's accumulation order.
+ * phase1 > 0: the tiles of the first phase1 problems are dispatched before
+ * those of the others (a launch whose last problems fill a part-empty last
+ * round); bnt > 0 forces the tile width. */
+int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float *ws, size_t ws_bytes,
+                int phase1 = 0, int force_bnt = 0) {
     if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm: %d problems (1..%d)", n, MAXP);
     GemmParams P;
     memset(&P, 0, sizeof(P));
@@ -773,7 +790,9 @@ int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float 
     if (t256 == 0) return 0;
     int bnt = BN;
     const int cus = iris_cu_count();
-    if (!seg2 && !swiglu_tiles && cus > 0) {
+    if (force_bnt == 224 && !seg2 && !swiglu_tiles) {
+        bnt = 224;
+    } else if (!force_bnt && !seg2 && !swiglu_tiles && cus > 0) {
         const long long w256 = (t256 + cus - 1) / cus * BN, w224 = (t224 + cus - 1) / cus * 224;
         if (w224 * 100 < w256 * 97) bnt = 224;
     }
@@ -786,13 +805,18 @@ int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float 
     }
     for (int i = n; i <= MAXP; i++) P.tile_start[i] = total;
     P.total = total;
-    P.per_xcd = (total + 7) / 8;
+    if (phase1 > 0 && phase1 < n) {
+        P.phase_tiles = P.tile_start[phase1];
+        P.phase_blocks = (P.phase_tiles + 7) / 8 * 8;
+    }
+    P.per_xcd = (total - P.phase_tiles + 7) / 8;
+    const dim3 grid(P.phase_blocks + 8 * P.per_xcd);
     if (bnt == 224)
-        IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), grid, dim3(NT), 0, iris_stream(), P);
     else if (seg2)
-        IRIS_LAUNCH(gemm_bf16_kernel<3>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<3>, grid, dim3(NT), 0, iris_stream(), P);
     else
-        IRIS_LAUNCH(gemm_bf16_kernel<0>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+        IRIS_LAUNCH(gemm_bf16_kernel<0>, grid, dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel")) return -1;
     if (!split) return 0;
     iris_gemm_problem_t rp[MAXP];
@@ -869,6 +893,74 @@ extern "C" int iris_hip_gemm_splitk(const iris_gemm_problem_t *p, int splits, fl
     return launch_gemm(p, 1, &splits, ws, ws_bytes);
 }
 
+namespace {
+
+/* the problem restricted to output rows [r0, M) (rows = true) or output
+ * columns [c0, N) */
+iris_gemm_problem_t sub_problem(const iris_gemm_problem_t &p, bool rows, int from) {
+    iris_gemm_problem_t q = p;
+    const size_t es = (p.epi == IRIS_EPI_BF16 || p.epi == IRIS_EPI_SWIGLU) ? 2 : 4;
+    if (rows) {
+        q.A = p.A + (size_t)from * p.lda;
+        q.out = (char *)p.out + es * (p.epi == IRIS_EPI_F32_T ? (size_t)from : (size_t)from * p.ldo);
+        q.M = p.M - from;
+    } else {
+        q.W = p.W + (size_t)from * p.ldw;
+        if (p.vec) q.vec = p.vec + from;
+        const size_t col = p.epi == IRIS_EPI_SWIGLU ? (size_t)from / 2 : (size_t)from;
+        q.out = (char *)p.out + es * (p.epi == IRIS_EPI_F32_T ? col * p.ldo : col);
+        q.N = p.N - from;
+    }
+    return q;
+}
+
+/* A product whose 256-wide tiles fill one or more whole rounds of blocks on
+ * the CUs and then a part-empty last round: the whole rounds run as they
+ * are, and the leftover tiles -- taken as whole tile rows (or columns) at
+ * the end of the output -- are split over K across the CUs the whole rounds
+ * free, in the same launch, with one reduce launch after it. Taken when a
+ * cost estimate in units of one round (the split pieces' share of a round,
+ * plus the reduce pass's traffic at 4.5 TB/s and its launch) beats the plain
+ * launch at either tile width by 8 %. Returns the number of chunks (0: not
+ * taken) and the two problems. */
+int tail_plan(const iris_gemm_problem_t &p, size_t ws_bytes, iris_gemm_problem_t parts[2]) {
+    const int cus = iris_cu_count();
+    if (cus <= 0 || p.K2 || p.M <= 0 || p.N <= 0) return 0;
+    const int tm = (p.M + BM - 1) / BM, tn = (p.N + BN - 1) / BN, nk = p.K / BK;
+    const long long T = (long long)tm * tn, full = T / cus, tail = T - full * cus;
+    if (full < 1 || tail == 0 || nk < 8) return 0;
+    const int kr = (int)((tail + tn - 1) / tn), kc = (int)((tail + tm - 1) / tm);
+    const bool rows_ok = kr < tm, cols_ok = kc < tn && !(p.epi == IRIS_EPI_SWIGLU && (p.N % 64));
+    if (!rows_ok && !cols_ok) return 0;
+    const bool rows = rows_ok && (!cols_ok || (long long)kr * tn <= (long long)kc * tm);
+    const int from = rows ? (tm - kr) * BM : (tn - kc) * BN;
+    const long long tail_tiles = rows ? (long long)kr * tn : (long long)kc * tm;
+    const size_t part_bytes = rows ? (size_t)(p.M - from) * p.N * 4 : (size_t)p.M * (p.N - from) * 4;
+    int pieces = (int)std::min<long long>(cus / tail_tiles, nk / 4);
+    while (pieces > 1 && (size_t)pieces * part_bytes > ws_bytes) pieces--;
+    if (pieces < 2) return 0;
+    /* estimates in units of one round of 256-wide tiles over the whole K */
+    const double round_us = 2.0 * BM * BN * (double)p.K / 5.1e12 * 1e6;
+    const bool rmw = p.epi == IRIS_EPI_GATED_ADD || p.epi == IRIS_EPI_ADD;
+    const double out_bytes = part_bytes / 4.0 * ((p.epi == IRIS_EPI_BF16 || p.epi == IRIS_EPI_SWIGLU) ? 2 : 4) *
+                             (rmw ? 2 : 1);
+    const double reduce_us = ((double)pieces * part_bytes + out_bytes) / 4.5e12 * 1e6 + 6.0;
+    const double split_cost = (double)full + 1.0 / pieces + reduce_us / round_us;
+    double plain = (double)full + 1.0;
+    if (p.epi != IRIS_EPI_SWIGLU) {
+        const long long t224 = (long long)tm * ((p.N + 223) / 224);
+        plain = std::min(plain, (double)((t224 + cus - 1) / cus) * 224.0 / 256.0);
+    }
+    if (split_cost > 0.92 * plain) return 0;
+    parts[0] = p;
+    if (rows) parts[0].M = from;
+    else parts[0].N = from;
+    parts[1] = sub_problem(p, rows, from);
+    return pieces;
+}
+
+}  // namespace
+
 extern "C" int iris_hip_gemm_fill_n(const iris_gemm_problem_t *probs, int n, float *ws, size_t ws_bytes) {
     if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm_fill: %d problems (1..%d)", n, MAXP);
     const int cus = iris_cu_count();
@@ -893,6 +985,15 @@ extern "C" int iris_hip_gemm_fill_n(const iris_gemm_problem_t *probs, int n, flo
             int want[MAXP];
             for (int i = 0; i < n; i++) want[i] = splits;
             return launch_gemm(probs, n, want, ws, ws_bytes);
+        }
+    }
+    if (n == 1 && ws && !((uintptr_t)ws & 15)) {
+        iris_gemm_problem_t parts[2];
+        const int pieces = tail_plan(probs[0], ws_bytes, parts);
+        if (pieces > 1) {
+            if (check_problem(probs[0])) return -1;
+            const int want[2] = {1, pieces};
+            return launch_gemm(parts, 2, want, ws, ws_bytes, 1, BN);
         }
     }
     return launch_gemm(probs, n, nullptr, nullptr, 0);

@@ -328,6 +328,82 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
     print(f"fill_n {rows} x {N} x {K}: {splits} chunks")
 
 
+def launched_kernels(lib, fn):
+    """Names of the kernels fn() launches (the per-kernel profile)."""
+    assert lib.iris_hip_profile_enable(1) == 0
+    fn()
+    recs = (tl.KernelTime * 64)()
+    n = lib.iris_hip_profile_read(recs, 64)
+    assert lib.iris_hip_profile_enable(0) == 0
+    return [r.kernel.decode() for r in recs[:max(n, 0)]]
+
+
+@pytest.mark.parametrize("M,N,K,epi,split", [(4608, 3840, 3840, EPI_F32, True), (4608, 3840, 10240, EPI_GATED_ADD, True),
+                                             (2048, 9216, 2048, EPI_SWIGLU, True), (4500, 3800, 3840, EPI_F32_T, True),
+                                             (4608, 11520, 3840, EPI_BF16, False)])
+def test_gemm_fill_tail_split(lib, M, N, K, epi, split):
+    """iris_hip_gemm_fill on products with whole rounds of 256-wide tiles and
+    a part-empty last round (on 256 CUs): Z-Image's attention output and FFN
+    down projections (4608 x 3840; 270 tiles = 256 + 14, the leftover tile
+    row split over K across the CUs the first round frees), a SwiGLU product
+    whose leftover is a set of tile columns (2048 x 9216: 288 tiles), ragged
+    rows and columns with the transposed store; and Z-Image's QKV product
+    (810 tiles), where the estimate keeps the plain launch. Against the
+    plain launch (same products, other summation order over K) and float64
+    on sampled rows, including every leftover row."""
+    if cu_count(lib) != 256:
+        split = None            # which launch the estimate takes depends on the CU count
+    rng = np.random.default_rng(M + N + K + epi)
+    a = bf(rng.standard_normal((M, K), np.float32))
+    w = bf(rng.standard_normal((N, K), np.float32) * 0.02)
+    vec = rng.standard_normal(N).astype(np.float32)
+    nout = N // 2 if epi == EPI_SWIGLU else N
+    ldo = M if epi == EPI_F32_T else nout
+    shape = (N, M) if epi == EPI_F32_T else (M, nout)
+    x0 = rng.standard_normal(shape, np.float32)
+    A, W, V = tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w)), tl.Dev.of(vec)
+    ws_bytes = 64 << 20
+    ws = tl.Dev(ws_bytes)
+    lib.iris_hip_gemm_fill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    outs = []
+    for mode in ("fill", "fill", "plain"):
+        o = tl.Dev(M * nout * 2) if epi in (EPI_BF16, EPI_SWIGLU) else tl.Dev.of(x0)
+        pr = tl.GemmProblem(A.ptr, W.ptr, o.ptr, None if epi == EPI_SWIGLU else V.ptr, M, N, K, K, K, ldo, epi)
+        if mode == "fill":
+            rc = []
+            names = launched_kernels(lib, lambda: rc.append(lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr,
+                                                                                   ws_bytes)))
+            assert rc == [0], lib.iris_hip_last_error()
+            if split is not None:
+                assert ("splitk_reduce_kernel" in names) == split, names
+        else:
+            run_gemm(lib, [pr])
+        assert lib.iris_hip_sync() == 0
+        outs.append(tl.bf16_to_f32(o.get(np.uint16, shape)) if epi in (EPI_BF16, EPI_SWIGLU) else
+                    o.get(np.float32, shape))
+        o.close()
+    assert np.array_equal(outs[0], outs[1]), "not repeatable"
+    got = outs[0].T if epi == EPI_F32_T else outs[0]
+    plain = outs[2].T if epi == EPI_F32_T else outs[2]
+    x0r = x0.T if epi == EPI_F32_T else x0
+    tol = 4e-3 if epi in (EPI_BF16, EPI_SWIGLU) else 1e-5
+    assert tl.rel_l2(got, plain) < tol
+    rows = np.unique(np.concatenate([np.arange(0, 64), np.arange(M - 300, M), rng.integers(0, M, 64)]))
+    y = a[rows].astype(np.float64) @ w.astype(np.float64).T
+    if epi == EPI_SWIGLU:
+        g = np.concatenate([y[:, c * 64:c * 64 + 32] for c in range(N // 64)], 1)
+        u = np.concatenate([y[:, c * 64 + 32:c * 64 + 64] for c in range(N // 64)], 1)
+        ref = g / (1 + np.exp(-g)) * u
+    elif epi == EPI_GATED_ADD:
+        ref = x0r[rows] + vec * y
+    elif epi == EPI_BF16:
+        ref = y + vec
+    else:
+        ref = y + vec
+    assert tl.rel_l2(got[rows], ref) < tol
+    print(f"fill {M}x{N}x{K} epi {epi}: {'tail split' if split else 'plain'}, rel_l2 {tl.rel_l2(got[rows], ref):.2e}")
+
+
 @pytest.mark.parametrize("shapes,K", [([(4608, 3072)], 1024), ([(512, 9216), (4096, 9216)], 192),
                                       ([(4608, 3840)], 320), ([(700, 3000)], 128)])
 def test_gemm_narrow_tiles(lib, shapes, K):
