@@ -71,6 +71,19 @@ float *iris_sample_euler_cfg_with_multi_refs(void *transformer, void *text_encod
 float *iris_sample_euler_zimage(void *transformer, float *z, int batch, int channels, int h, int w, int patch_size,
                                 const float *cap_feats, int cap_seq, const float *schedule, int num_steps,
                                 void (*progress_callback)(int step, int total));
+/* Euler with noise injection (iris_sample.c:990-1062): after every step but
+ * the last, eta * sqrt|dt| times normals from the global generator
+ * (iris_rng_seed / iris_randn, drawn in the reference's order) are added to
+ * the latent; eta <= 0 is the plain Euler sampler. */
+float *iris_sample_euler_ancestral(void *transformer, float *z, int batch, int channels, int h, int w,
+                                   const float *text_emb, int text_seq, const float *schedule, int num_steps,
+                                   float eta, void (*progress_callback)(int step, int total));
+/* Heun's second-order method (iris_sample.c:1063-1145): z_pred = z + dt v(z, t),
+ * then z += dt / 2 (v(z, t) + v(z_pred, t_next)); the last step is plain
+ * Euler. Two forwards per step. */
+float *iris_sample_heun(void *transformer, float *z, int batch, int channels, int h, int w, const float *text_emb,
+                        int text_seq, const float *schedule, int num_steps,
+                        void (*progress_callback)(int step, int total));
 
 #ifdef __cplusplus
 }

@@ -4,9 +4,10 @@
  * Noise follows iris_sample.c:1146-1188 and the xoshiro256** RNG of
  * iris_kernels.c:50-107 (same seeds give the same noise); the schedules are
  * in iris_schedule.c.
- * The Euler loops (iris_sample.c:313-405, :412-536, :543-702, :717-989) keep
- * the latent resident on the device: one upload, one graph replay and one
- * update kernel per step, one download at the end.
+ * The Euler loops (iris_sample.c:313-405, :412-536, :543-702, :717-989), the
+ * ancestral Euler loop (:990-1062) and Heun's (:1063-1145) keep the latent
+ * resident on the device: one upload, one graph replay and one update kernel
+ * per forward, one download at the end.
  */
 #include "../../include/iris_sample.h"
 #include "../../include/iris_hip.h"
@@ -253,5 +254,85 @@ float *iris_sample_euler_zimage(void *transformer, float *z, int batch, int chan
     size_t n = (size_t)channels * h * w;
     float *out = (float *)malloc(n * sizeof(float));
     if (!out || zi_download_latent(tf, out)) { free(out); return NULL; }
+    return out;
+}
+
+/* iris_sample_euler_ancestral (iris_sample.c:990-1062): the Euler step on the
+ * device, then for eta > 0 and every step but the last sigma = eta sqrt|dt|
+ * times a latent of normals drawn on the host from the global generator
+ * (iris_randn: same generator, same order as the reference's), uploaded and
+ * added by the update kernel. The reference checks for cancellation before
+ * each step and calls no step callback. */
+float *iris_sample_euler_ancestral(void *transformer, float *z, int batch, int channels, int h, int w,
+                                   const float *text_emb, int text_seq, const float *schedule, int num_steps,
+                                   float eta, void (*progress_callback)(int, int)) {
+    iris_transformer_t *tf = (iris_transformer_t *)transformer;
+    (void)batch;
+    if (num_steps > IRIS_MAX_STEPS) {
+        fprintf(stderr, "iris_sample: num_steps %d exceeds IRIS_MAX_STEPS %d\n", num_steps, IRIS_MAX_STEPS);
+        return NULL;
+    }
+    if (iris_flux_prepare(tf, h, w, NULL, 0, text_seq, 1) || iris_flux_upload(tf, z, NULL, text_emb)) return NULL;
+    const size_t n = (size_t)channels * h * w;
+    float *lat = (float *)iris_flux_device_buffer(tf, "latent"), *vel = (float *)iris_flux_device_buffer(tf, "velocity");
+    float *noise = (float *)malloc(n * sizeof(float)), *out = (float *)malloc(n * sizeof(float));
+    int ok = noise && out && lat && vel;
+    for (int i = 0; ok && i < num_steps; i++) {
+        if (iris_cancel_requested) { ok = 0; break; }
+        const float dt = schedule[i + 1] - schedule[i];
+        ok = !iris_flux_step(tf, schedule[i], schedule[i + 1], 0.0f);
+        if (ok && eta > 0.0f && i < num_steps - 1) {
+            /* the velocity buffer is free until the next forward */
+            iris_randn(noise, (int)n);
+            ok = !iris_hip_memcpy_h2d(vel, noise, n * sizeof(float)) &&
+                 !iris_hip_euler(lat, vel, NULL, 0.0f, eta * sqrtf(fabsf(dt)), 1.0f, n);
+        }
+        if (ok && progress_callback) progress_callback(i + 1, num_steps);
+    }
+    free(noise);
+    if (ok && iris_flux_download_latent(tf, out)) ok = 0;
+    if (!ok) {
+        free(out);
+        return NULL;
+    }
+    return out;
+}
+
+/* iris_sample_heun (iris_sample.c:1063-1145): v1 = v(z, t); except on the last
+ * step, z_pred = z + dt v1 in the latent buffer, v2 = v(z_pred, t_next), then
+ * z (kept aside with v1) += dt (v1 + (v2 - v1) / 2), the update kernel's
+ * guided form of dt / 2 (v1 + v2). */
+float *iris_sample_heun(void *transformer, float *z, int batch, int channels, int h, int w, const float *text_emb,
+                        int text_seq, const float *schedule, int num_steps, void (*progress_callback)(int, int)) {
+    iris_transformer_t *tf = (iris_transformer_t *)transformer;
+    (void)batch;
+    if (num_steps > IRIS_MAX_STEPS) {
+        fprintf(stderr, "iris_sample: num_steps %d exceeds IRIS_MAX_STEPS %d\n", num_steps, IRIS_MAX_STEPS);
+        return NULL;
+    }
+    if (iris_flux_prepare(tf, h, w, NULL, 0, text_seq, 1) || iris_flux_upload(tf, z, NULL, text_emb)) return NULL;
+    const size_t n = (size_t)channels * h * w, nb = n * sizeof(float);
+    float *lat = (float *)iris_flux_device_buffer(tf, "latent"), *vel = (float *)iris_flux_device_buffer(tf, "velocity");
+    float *keep = (float *)iris_hip_malloc(2 * nb);   /* z of the step, then v1 */
+    float *out = (float *)malloc(nb);
+    int ok = keep && out && lat && vel;
+    for (int i = 0; ok && i < num_steps; i++) {
+        const float dt = schedule[i + 1] - schedule[i];
+        ok = !iris_flux_velocity(tf, schedule[i]);
+        if (ok && i < num_steps - 1) {
+            ok = !iris_hip_memcpy_d2d(keep, lat, nb) && !iris_hip_memcpy_d2d(keep + n, vel, nb) &&
+                 !iris_hip_euler(lat, vel, NULL, 0.0f, dt, 1.0f, n) && !iris_flux_velocity(tf, schedule[i + 1]) &&
+                 !iris_hip_memcpy_d2d(lat, keep, nb) && !iris_hip_euler(lat, keep + n, vel, 0.5f, dt, 1.0f, n);
+        } else if (ok) {
+            ok = !iris_hip_euler(lat, vel, NULL, 0.0f, dt, 1.0f, n);
+        }
+        if (ok && progress_callback) progress_callback(i + 1, num_steps);
+    }
+    if (ok && iris_flux_download_latent(tf, out)) ok = 0;
+    iris_hip_free(keep);
+    if (!ok) {
+        free(out);
+        return NULL;
+    }
     return out;
 }

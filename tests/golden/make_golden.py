@@ -161,6 +161,22 @@ def flux_goldens(r, d, res):
                                           tl.fptr(temb_txt), T, tl.fptr(txt_u20), 20, 3.0, tl.fptr(sched_arr), 2,
                                           None)
     res["flux_sample2_cfg_ref1_t20"] = tl.take_f32(r, p, 128 * 64)
+    # the ancestral (eta 0.6, noise from the global generator seeded with
+    # 1234) and Heun samplers, iris_sample.c:990-1145, over 3 steps
+    sched3 = r.iris_official_schedule(3, 64)
+    sched3_arr = np.ctypeslib.as_array(ctypes.cast(sched3, tl.FP), shape=(4,)).copy()
+    r.iris_sample_euler_ancestral.argtypes = [V, tl.FP, I_, I_, I_, I_, tl.FP, I_, tl.FP, I_, ctypes.c_float, V]
+    r.iris_sample_heun.argtypes = [V, tl.FP, I_, I_, I_, I_, tl.FP, I_, tl.FP, I_, V]
+    r.iris_sample_euler_ancestral.restype = V
+    r.iris_sample_heun.restype = V
+    r.iris_rng_seed.argtypes = [ctypes.c_uint64]
+    r.iris_rng_seed(1234)
+    p = r.iris_sample_euler_ancestral(tf, tl.fptr(noise_arr), 1, 128, 8, 8, tl.fptr(temb_txt), T,
+                                      tl.fptr(sched3_arr), 3, 0.6, None)
+    res["flux_sample3_ancestral"] = tl.take_f32(r, p, 128 * 64)
+    p = r.iris_sample_heun(tf, tl.fptr(noise_arr), 1, 128, 8, 8, tl.fptr(temb_txt), T, tl.fptr(sched3_arr), 3, None)
+    res["flux_sample3_heun"] = tl.take_f32(r, p, 128 * 64)
+    res["flux_sample3_sched"] = sched3_arr
     r.iris_transformer_free(tf)
 
 

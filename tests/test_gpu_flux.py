@@ -198,6 +198,55 @@ def test_two_step_sample_vs_reference(lib, tiny):
     assert tl.cosine(got, G["flux_sample2"]) > 0.999 and tl.rel_l2(got, G["flux_sample2"]) < 1e-2
 
 
+def test_ancestral_and_heun_samplers_vs_reference(lib, tiny):
+    """iris_sample_euler_ancestral (eta 0.6, the global generator seeded with
+    1234 as for the reference's run) and iris_sample_heun over the reference's
+    3-step schedule from its noise, against the reference build's own samples
+    (iris_sample.c:990-1145); the ancestral sample also against the same loop
+    written out over the product's forward and iris_randn (the noise is the
+    generator's, in the reference's order), and with eta 0 against
+    iris_sample_euler."""
+    sched = G["flux_sample3_sched"].copy()
+    z0 = G["flux_noise42"].copy()
+    txt = tl.synth_f32((32, 256), 22)
+    V, I_ = ctypes.c_void_p, ctypes.c_int
+    lib.iris_sample_euler_ancestral.argtypes = [V, tl.FP, I_, I_, I_, I_, tl.FP, I_, tl.FP, I_, F, V]
+    lib.iris_sample_heun.argtypes = [V, tl.FP, I_, I_, I_, I_, tl.FP, I_, tl.FP, I_, V]
+    lib.iris_sample_euler_ancestral.restype = V
+    lib.iris_sample_heun.restype = V
+    lib.iris_rng_seed.argtypes = [ctypes.c_uint64]
+    lib.iris_randn.argtypes = [tl.FP, I_]
+    lib.iris_rng_seed(1234)
+    z = z0.copy()
+    anc = take(lib, lib.iris_sample_euler_ancestral(tiny, tl.fptr(z), 1, 128, 8, 8, tl.fptr(txt), 32, tl.fptr(sched), 3,
+                                                    F(0.6), None), 8192)
+    want = G["flux_sample3_ancestral"]
+    print(f"ancestral: rel_l2 {tl.rel_l2(anc, want):.3e} cosine {tl.cosine(anc, want):.6f}")
+    assert tl.cosine(anc, want) > 0.999 and tl.rel_l2(anc, want) < 1e-2
+    lib.iris_rng_seed(1234)
+    zl = z0.copy()
+    for i in range(3):
+        v = take(lib, lib.iris_transformer_forward(tiny, tl.fptr(zl), 8, 8, tl.fptr(txt), 32, F(sched[i])), 8192)
+        dt = np.float32(sched[i + 1] - sched[i])
+        zl = zl + dt * v
+        if i < 2:
+            noise = np.empty(8192, np.float32)
+            lib.iris_randn(tl.fptr(noise), 8192)
+            zl = zl + np.float32(0.6) * np.sqrt(np.abs(dt)) * noise
+    assert tl.rel_l2(anc, zl) < 1e-5, tl.rel_l2(anc, zl)
+    plain = take(lib, lib.iris_sample_euler_ancestral(tiny, tl.fptr(z0.copy()), 1, 128, 8, 8, tl.fptr(txt), 32,
+                                                      tl.fptr(sched), 3, F(0.0), None), 8192)
+    lib.iris_sample_euler.argtypes = [V, V, tl.FP, I_, I_, I_, I_, tl.FP, I_, tl.FP, I_, V]
+    euler = take(lib, lib.iris_sample_euler(tiny, None, tl.fptr(z0.copy()), 1, 128, 8, 8, tl.fptr(txt), 32,
+                                            tl.fptr(sched), 3, None), 8192)
+    np.testing.assert_array_equal(plain, euler)
+    heun = take(lib, lib.iris_sample_heun(tiny, tl.fptr(z0.copy()), 1, 128, 8, 8, tl.fptr(txt), 32, tl.fptr(sched), 3,
+                                          None), 8192)
+    want = G["flux_sample3_heun"]
+    print(f"heun: rel_l2 {tl.rel_l2(heun, want):.3e} cosine {tl.cosine(heun, want):.6f}")
+    assert tl.cosine(heun, want) > 0.999 and tl.rel_l2(heun, want) < 1e-2
+
+
 def euler_with_forwards(lib, tiny, z0, sched, refs, nrefs, tc, Tc, tu=None, Tu=0, g=1.0):
     """The Euler loop written out over the product's forward entry points."""
     z = z0.copy()
