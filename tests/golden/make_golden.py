@@ -308,11 +308,20 @@ def main():
         with tempfile.TemporaryDirectory() as d:
             c1_golden(r, d, c1)
         np.savez_compressed(os.path.join(tl.GOLDEN, "reference_c1_single_block.npz"), **c1)
+    def schedule_lanes():
+        """the vector lane plan of this host's -march=native reference build
+        (16-wide with AVX-512 F + VL, else 8-wide with AVX2 + FMA)"""
+        flags = next((ln.split(":", 1)[1].split() for ln in open("/proc/cpuinfo") if ln.startswith("flags")), [])
+        if "avx512f" in flags and "avx512vl" in flags:
+            return "avx512"
+        return "avx2" if "avx2" in flags and "fma" in flags else "scalar"
+
     manifest = {
         "generator": "tests/golden/make_golden.py",
         "reference_build": "oracle/Makefile `ref`: gcc -O3 -march=native -ffast-math -DGENERIC_BUILD",
         "flux_tiny": FLUX_TINY, "zimage_tiny": ZI_TINY, "zimage_triu_cases": ZI_TRIU_CASES, "c1": C1,
         "inputs": "iris_synth f32 N(0,1) by seed (see make_golden.py); weights bf16 via iris_synth_seed(name)",
+        "schedule_lanes": schedule_lanes(),
         "sha256": hashes,
     }
     with open(os.path.join(tl.GOLDEN, "manifest.json"), "w") as f:

@@ -11,8 +11,12 @@ schedules, seeded noise and the timestep sinusoid, bit for bit.
   which pin the schedules without the reference build.
 
 The reference build's vectorized schedule lanes divide through the CPU's
-reciprocal estimate (rcpps) and one Newton step; the product uses the same
-instructions, so these equalities hold on the host that made the goldens.
+reciprocal estimate (rcpps, or vrcp14ps in 16-wide AVX-512 blocks) and one
+Newton step, in blocks whose widths follow the host's vector ISA; the product
+uses the same instructions and the same blocks, so these equalities hold on a
+host of the model that made the goldens (run with that host's lane plan,
+recorded in manifest.json) and against the reference build on the host that
+runs the tests.
 """
 import ctypes
 import json
@@ -53,13 +57,27 @@ def bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
+@pytest.fixture
+def golden_lanes(monkeypatch):
+    """the schedule lane plan of the host that made the goldens (the product
+    can narrow its plan to it; a wider one than this CPU runs is skipped)"""
+    plan = MAN.get("schedule_lanes", "avx2")
+    flags = next((ln.split(":", 1)[1].split() for ln in open("/proc/cpuinfo") if ln.startswith("flags")), [])
+    have = {"scalar": True, "avx2": "avx2" in flags and "fma" in flags,
+            "avx512": "avx512f" in flags and "avx512vl" in flags}
+    if not have[plan]:
+        pytest.skip(f"the goldens' schedules come from {plan} lanes, which this CPU lacks")
+    monkeypatch.setenv("IRIS_SCHEDULE_ISA", plan)
+    return plan
+
+
 @pytest.mark.parametrize("n,seq", [(4, 1024), (4, 4096), (50, 4096)])
-def test_official_schedule_equals_reference_golden(prod, n, seq):
+def test_official_schedule_equals_reference_golden(prod, golden_lanes, n, seq):
     got = take(prod.iris_official_schedule(n, seq), n + 1)
     np.testing.assert_array_equal(bits(got), bits(G[f"sched_official_{n}_{seq}"]))
 
 
-def test_zimage_schedule_equals_reference_golden(prod, monkeypatch):
+def test_zimage_schedule_equals_reference_golden(prod, golden_lanes, monkeypatch):
     monkeypatch.delenv("IRIS_ZIMAGE_SHIFT", raising=False)
     got = take(prod.iris_zimage_schedule(8, 4096), 9)
     np.testing.assert_array_equal(bits(got), bits(G["sched_zimage_8"]))

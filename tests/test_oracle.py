@@ -373,6 +373,7 @@ def test_zimage_forward(lib, zi, hw, cap_len, t, key, seeds):
 def zi_triu(lib):
     cfg = MAN["zimage_tiny"]
     axes = (ctypes.c_int * 3)(*cfg["axes"])
+    lib.orc_zi_load.argtypes = [ctypes.c_char_p] + [ctypes.c_int] * 7 + [ctypes.c_float, ctypes.c_void_p]
     with tempfile.TemporaryDirectory() as d:
         tl.write_zimage_model(d, cfg, cfg["seed"], triu_out=True)
         m = lib.orc_zi_load(d.encode(), cfg["dim"], cfg["heads"], cfg["layers"], cfg["refiners"], cfg["cap_dim"],
