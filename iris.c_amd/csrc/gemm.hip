@@ -8,7 +8,9 @@
  *
  * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
  * a 4x2 arrangement; each wave owns 64x128 as 4x8 v_mfma_f32_16x16x32_bf16
- * tiles. The 16x16x32 form does the same work per LDS byte as 32x32x16 and,
+ * tiles (narrower block tiles: 256x224 for plain GEMMs whose last round of
+ * 256-wide tiles would be part-empty, 256x128 for convolutions of at most
+ * 128 output channels). The 16x16x32 form does the same work per LDS byte as 32x32x16 and,
  * with the chip at its power limit on random data, sustains about 10 % more
  * MFMA throughput.
  *
@@ -162,10 +164,13 @@ __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_
 template <int MODE, int BNT = BN>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3;
-    /* BNT: block tile width, 256 or (MODE 0, no SwiGLU) 224 = 2 waves x 7
+    /* BNT: block tile width, 256, or (MODE 0, no SwiGLU) 224 = 2 waves x 7
      * MFMA tiles, for launches whose 256-wide tiles leave the last wave of
-     * blocks part-empty */
-    static_assert(BNT == BN || (BNT == 224 && MODE == 0), "narrow tiles are for plain GEMMs");
+     * blocks part-empty, or (convolutions) 128 = 2 waves x 4 MFMA tiles for
+     * outputs of at most 128 channels, which a 256-wide tile would compute
+     * half empty */
+    static_assert(BNT == BN || (BNT == 224 && MODE == 0) || (BNT == 128 && (MODE == 1 || MODE == 2)),
+                  "narrow tiles are for plain GEMMs and convolutions");
     constexpr int TWN = BNT / WAVES_N, FNT = TWN / 16, W_DMA = BNT / DMA_ROWS / 4;
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
@@ -1036,8 +1041,11 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     memset(&P, 0, sizeof(P));
     P.nprob = 1;
     P.p[0] = p;
+    /* 128-wide tiles for at most 128 output channels (the decoder's
+     * full-resolution convolutions): same per-element accumulation order */
+    const int bnt = p.N <= 128 ? 128 : BN;
     P.tiles_m[0] = (p.M + BM - 1) / BM;
-    P.tiles_n[0] = (p.N + BN - 1) / BN;
+    P.tiles_n[0] = (p.N + bnt - 1) / bnt;
     P.conv_h = c->H;
     P.conv_w = c->W;
     P.conv_up = c->up;
@@ -1064,8 +1072,12 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
         P.ws[0] = c->ws;
         P.ws_stride[0] = stride;
     }
-    if (c->up == 2)
+    if (c->up == 2 && bnt == 128)
+        IRIS_LAUNCH((gemm_bf16_kernel<2, 128>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    else if (c->up == 2)
         IRIS_LAUNCH(gemm_bf16_kernel<2>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
+    else if (bnt == 128)
+        IRIS_LAUNCH((gemm_bf16_kernel<1, 128>), dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     else
         IRIS_LAUNCH(gemm_bf16_kernel<1>, dim3(8 * P.per_xcd), dim3(NT), 0, iris_stream(), P);
     if (iris_launch_check("gemm_bf16_kernel<conv>")) return -1;

@@ -54,13 +54,14 @@ def np_conv3(x, w, b, up):
 
 
 @pytest.mark.parametrize("H,W,cin,cout,up,splits", [
-    (20, 20, 64, 128, 0, 1),      # cout below the 256-wide tile, ragged last tile
-    (16, 24, 128, 256, 1, 1),     # fused nearest upsample
-    (37, 29, 256, 64, 0, 3),      # odd sizes, split-K over 36 K steps
+    (20, 20, 64, 128, 0, 1),      # cout 128: a 128-wide tile, ragged last row tile
+    (16, 24, 128, 256, 1, 1),     # fused nearest upsample, 256-wide tiles
+    (37, 29, 256, 64, 0, 3),      # odd sizes, half-empty 128-wide tile, split-K over 36 K steps
     (8, 64, 512, 512, 1, 4),      # 512 channels (8 K steps per tap), upsampled, split
-    (16, 96, 128, 128, 0, 1),     # cout <= 128 and rows >= 80 pixels: 512x128 tiles
-    (9, 200, 256, 64, 0, 2),      # 512x128 tiles, half-empty N, ragged M, split-K
-    (8, 160, 128, 128, 1, 1),     # 512x128 tiles through the upsample
+    (16, 96, 128, 128, 0, 1),     # cout 128 over several row tiles
+    (9, 200, 256, 64, 0, 2),      # half-empty 128-wide tiles, ragged M, split-K
+    (8, 160, 128, 128, 1, 1),     # 128-wide tiles through the upsample
+    (12, 20, 128, 192, 0, 1),     # cout between the tile widths: one part-empty 256-wide tile
 ])
 def test_conv3x3(lib, H, W, cin, cout, up, splits):
     rng = np.random.default_rng(H * W + cin)
