@@ -343,6 +343,65 @@ __global__ __launch_bounds__(NT) void conv_out_kernel(const uint16_t *g, int H, 
     }
 }
 
+/* The same convolution over 16 x 16 output tiles: the tile's input pixels
+ * and their one-pixel halo are staged in LDS 32 channels at a time (each
+ * input row read once per tile instead of once per tap and neighbour), the
+ * chunk's weights beside them; one thread per output pixel. The sums run
+ * chunk by chunk, tap by tap within a chunk. Rows of 32 channels are padded
+ * to 40 elements, so the 16 pixels of a half wave read 16 distinct 4-bank
+ * groups. */
+constexpr int CO_T = 16, CO_H = CO_T + 2, CO_C = 32, CO_STR = CO_C + 8;
+__global__ __launch_bounds__(NT) void conv_out_tiled_kernel(const uint16_t *g, int H, int W, int cin, const float *wt,
+                                                            const float *bias, uint8_t *rgb, float *f32) {
+    __shared__ __attribute__((aligned(16))) uint16_t xs[CO_H * CO_H * CO_STR];
+    __shared__ float4 wl[9 * CO_C];
+    const int tx = threadIdx.x & (CO_T - 1), ty = threadIdx.x / CO_T;
+    const int x0 = blockIdx.x * CO_T, y0 = blockIdx.y * CO_T;
+    float a0 = bias[0], a1 = bias[1], a2 = bias[2];
+    for (int c0 = 0; c0 < cin; c0 += CO_C) {
+        __syncthreads();   /* the previous chunk's reads are done */
+        for (int i = threadIdx.x; i < CO_H * CO_H * (CO_C / 8); i += NT) {
+            const int pix = i >> 2, part = i & 3;
+            const int gy = y0 + pix / CO_H - 1, gx = x0 + pix % CO_H - 1;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if ((unsigned)gy < (unsigned)H && (unsigned)gx < (unsigned)W)
+                v = *(const uint4 *)(g + ((size_t)gy * W + gx) * cin + c0 + part * 8);
+            *(uint4 *)(xs + pix * CO_STR + part * 8) = v;
+        }
+        for (int i = threadIdx.x; i < 9 * CO_C; i += NT) wl[i] = ((const float4 *)wt)[(i / CO_C) * cin + c0 + i % CO_C];
+        __syncthreads();
+        for (int tap = 0; tap < 9; tap++) {
+            const uint16_t *src = xs + ((ty + tap / 3) * CO_H + tx + tap % 3) * CO_STR;
+            const float4 *wr = wl + tap * CO_C;
+#pragma unroll
+            for (int c = 0; c < CO_C; c += 8) {
+                const u16x8 r = *(const u16x8 *)(src + c);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float v = bf2f(r[j]);
+                    const float4 k = wr[c + j];
+                    a0 += v * k.x;
+                    a1 += v * k.y;
+                    a2 += v * k.z;
+                }
+            }
+        }
+    }
+    const int y = y0 + ty, x = x0 + tx;
+    if (y >= H || x >= W) return;
+    const int p = y * W + x;
+    const float o[3] = {a0, a1, a2};
+#pragma unroll
+    for (int ch = 0; ch < 3; ch++) {
+        if (f32) f32[(size_t)ch * H * W + p] = o[ch];
+        float val = (o[ch] + 1.0f) * 0.5f;
+        val = val * 255.0f;
+        if (val < 0) val = 0;
+        if (val > 255) val = 255;
+        rgb[(size_t)p * 3 + ch] = (uint8_t)(val + 0.5f);
+    }
+}
+
 unsigned blocks_for(size_t n) {
     const size_t b = (n + NT - 1) / NT;
     return (unsigned)(b < 65536 ? b : 65536);
@@ -424,9 +483,15 @@ extern "C" int iris_hip_transpose_bf16(uint16_t *dst, int ld_dst, int rows_pad, 
 
 extern "C" int iris_hip_vae_conv_out(uint8_t *rgb, float *f32, const uint16_t *g, int H, int W, int cin,
                                      const float *wt, const float *bias) {
-    if (!rgb || !g || !wt || !bias || H <= 0 || W <= 0 || cin <= 0 || cin > 256 || cin % 8 || ((uintptr_t)g & 15) ||
+    if (!rgb || !g || !wt || !bias || H <= 0 || W <= 0 || H > 32768 || W > 32768 || cin <= 0 || cin > 256 || cin % 8 ||
+        ((uintptr_t)g & 15) ||
         ((uintptr_t)wt & 15))
         return iris_set_error("vae_conv_out: bad arguments");
+    if (cin % CO_C == 0) {
+        IRIS_LAUNCH(conv_out_tiled_kernel, dim3((W + CO_T - 1) / CO_T, (H + CO_T - 1) / CO_T), dim3(NT), 0,
+                    iris_stream(), g, H, W, cin, wt, bias, rgb, f32);
+        return iris_launch_check("conv_out_tiled_kernel");
+    }
     const int npix = H * W;
     IRIS_LAUNCH(conv_out_kernel, dim3((npix + NT - 1) / NT), dim3(NT), 9 * cin * sizeof(float4), iris_stream(),
                        g, H, W, cin, wt, bias, rgb, f32);

@@ -208,9 +208,13 @@ def test_vae_front(lib, z, divide, pq):
     assert not got[..., z:].any()
 
 
-def test_conv_out(lib):
-    rng = np.random.default_rng(1)
-    H, W, cin = 33, 47, 128       # W % 4 != 0: a partial quad per row
+@pytest.mark.parametrize("H,W,cin", [
+    (33, 47, 128),   # the decoder's 128 channels over ragged 16 x 16 output tiles (LDS-tiled kernel)
+    (17, 16, 64),    # two 32-channel chunks, one ragged tile row
+    (9, 21, 24),     # channels not a multiple of 32: the one-thread-per-pixel kernel
+])
+def test_conv_out(lib, H, W, cin):
+    rng = np.random.default_rng(H * W + cin)
     g = rng.standard_normal((H, W, cin)).astype(np.float32)
     w = (0.5 * rng.standard_normal((3, cin, 3, 3)) / np.sqrt(9 * cin)).astype(np.float32)
     b = (0.1 * rng.standard_normal(3)).astype(np.float32)
