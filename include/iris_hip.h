@@ -178,6 +178,17 @@ typedef struct {
     int splits;
     float *ws;
     size_t ws_bytes;
+    /* GroupNorm statistics of the output (iris_group_norm's sums,
+     * iris_kernels.c:542), computed in the epilogue; gn_part NULL: none.
+     * Without split-K only. For each row tile t of 256 output pixels and
+     * each of gn_groups groups of cout / gn_groups channels (a multiple of
+     * 4), the sum and the sum of squares of the f32 values written (with
+     * IRIS_EPI_ADD the updated stream, with IRIS_EPI_BF16 the values before
+     * rounding), summed in a fixed order, at gn_part[(t * gn_groups + g) * 2]
+     * and [.. + 1]: the layout and block count (ceil(H * W / 256)) that
+     * iris_hip_gn_finalize takes. */
+    double *gn_part;
+    int gn_groups;
 } iris_conv3x3_t;
 int iris_hip_conv3x3(const iris_conv3x3_t *c);
 

@@ -77,6 +77,10 @@ struct GemmParams {
      * (tap / 3 - 1, tap % 3 - 1) */
     int conv_h, conv_w, conv_up, conv_cpt_shift, conv_cin_bshift;
     unsigned conv_in_bytes;
+    /* GroupNorm statistics of a convolution's output (CONV kernels, no
+     * split-K): per row tile and group, sum and sum of squares in f64 */
+    double *gn_part;
+    int gn_groups;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in a tile */
@@ -462,12 +466,24 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * access per lane and 16x16 tile */
     const bool aligned = (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 && ((uintptr_t)vec & 15) == 0;
     const bool full = m0 + BM <= M && n0 + BNT <= N && aligned;
+    /* GroupNorm statistics of a convolution's output: each lane sums the
+     * values it writes per 4-channel chunk (one group: groups are multiples
+     * of 4 channels), then the tile's sums per group are formed in a fixed
+     * order below (the direct stores: the tile's values stay in registers) */
+    const bool gn = CONV && P.gn_part != nullptr;
+    float gs1[FNT], gs2[FNT];
+#pragma unroll
+    for (int ni = 0; ni < FNT; ni++) gs1[ni] = gs2[ni] = 0.0f;
+    auto gn_add = [&](int ni, float y) {
+        gs1[ni] += y;
+        gs2[ni] += y * y;
+    };
     /* Whole tiles of bf16 output (plain or SwiGLU) go out through LDS: each
      * group writes its 128 rows into one of the stages, now free, and then
      * stores them as 16-byte chunks of whole rows, so one store instruction
      * covers full 128-byte lines instead of 32-byte pieces of 16 rows (the
      * direct stores left the waves stalled on issue). */
-    if (full && (ldo & 7) == 0 && (pr.epi == IRIS_EPI_BF16 || (BNT == BN && pr.epi == IRIS_EPI_SWIGLU))) {
+    if (!gn && full && (ldo & 7) == 0 && (pr.epi == IRIS_EPI_BF16 || (BNT == BN && pr.epi == IRIS_EPI_SWIGLU))) {
         if (pr.epi == IRIS_EPI_SWIGLU) stage_out<BNT / 2, true, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0 >> 1, wm, wn, TWN);
         else stage_out<BNT, false, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0, wm, wn, TWN);
         return;
@@ -497,32 +513,44 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 const f32x4 x = acc[mi][ni];
                 const size_t o = (size_t)row * ldo + col;
                 if (full || (cols4 && row < M)) {
+                    float4 y;
                     if (pr.epi == IRIS_EPI_F32) {
-                        *(float4 *)((float *)pr.out + o) = make_float4(x[0] + v[0], x[1] + v[1], x[2] + v[2], x[3] + v[3]);
+                        y = make_float4(x[0] + v[0], x[1] + v[1], x[2] + v[2], x[3] + v[3]);
+                        *(float4 *)((float *)pr.out + o) = y;
                     } else if (pr.epi == IRIS_EPI_BF16) {
+                        y = make_float4(x[0] + v[0], x[1] + v[1], x[2] + v[2], x[3] + v[3]);
                         uint2 p;
-                        p.x = (uint32_t)f2bf_hw(x[0] + v[0]) | ((uint32_t)f2bf_hw(x[1] + v[1]) << 16);
-                        p.y = (uint32_t)f2bf_hw(x[2] + v[2]) | ((uint32_t)f2bf_hw(x[3] + v[3]) << 16);
+                        p.x = (uint32_t)f2bf_hw(y.x) | ((uint32_t)f2bf_hw(y.y) << 16);
+                        p.y = (uint32_t)f2bf_hw(y.z) | ((uint32_t)f2bf_hw(y.w) << 16);
                         *(uint2 *)((uint16_t *)pr.out + o) = p;
                     } else if (pr.epi == IRIS_EPI_GATED_ADD) {
                         float4 *dst = (float4 *)((float *)pr.out + o);
-                        float4 y = *dst;
+                        y = *dst;
                         y.x += v[0] * x[0]; y.y += v[1] * x[1]; y.z += v[2] * x[2]; y.w += v[3] * x[3];
                         *dst = y;
                     } else {
                         float4 *dst = (float4 *)((float *)pr.out + o);
-                        float4 y = *dst;
+                        y = *dst;
                         y.x += x[0] + v[0]; y.y += x[1] + v[1]; y.z += x[2] + v[2]; y.w += x[3] + v[3];
                         *dst = y;
+                    }
+                    if (gn) {
+                        gn_add(ni, y.x);
+                        gn_add(ni, y.y);
+                        gn_add(ni, y.z);
+                        gn_add(ni, y.w);
                     }
                 } else if (row < M) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         if (col + r >= N) continue;
-                        if (pr.epi == IRIS_EPI_F32) ((float *)pr.out)[o + r] = x[r] + v[r];
-                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o + r] = f2bf_hw(x[r] + v[r]);
-                        else if (pr.epi == IRIS_EPI_GATED_ADD) ((float *)pr.out)[o + r] += v[r] * x[r];
-                        else ((float *)pr.out)[o + r] += x[r] + v[r];
+                        float *const f = (float *)pr.out + o + r;
+                        float y = x[r] + v[r];
+                        if (pr.epi == IRIS_EPI_F32) *f = y;
+                        else if (pr.epi == IRIS_EPI_BF16) ((uint16_t *)pr.out)[o + r] = f2bf_hw(y);
+                        else if (pr.epi == IRIS_EPI_GATED_ADD) *f = y = *f + v[r] * x[r];
+                        else *f = y = *f + (x[r] + v[r]);
+                        if (gn) gn_add(ni, y);
                     }
                 }
             }
@@ -577,6 +605,40 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
     default:
         break;
+    }
+    if constexpr (CONV) {
+        if (gn) {
+            /* per wave, the 16 lanes of a row hold one 4-channel chunk's 16
+             * rows of each of the wave's 4 row blocks: the chunk's sums over
+             * the wave's 64 rows, then over the tile's 4 waves in M and the
+             * group's chunks in order, in f64 */
+            __shared__ float gnl[WAVES_M * WAVES_N * FNT * 4 * 2];
+#pragma unroll
+            for (int ni = 0; ni < FNT; ni++) {
+                const float s = row16_sum(gs1[ni]), q = row16_sum(gs2[ni]);
+                if (lr == 0) {
+                    float *d = gnl + (((wm * WAVES_N + wn) * FNT + ni) * 4 + lg) * 2;
+                    d[0] = s;
+                    d[1] = q;
+                }
+            }
+            __syncthreads();
+            const int G = P.gn_groups, cpg = N / G, t = threadIdx.x;
+            if (t < BNT / cpg && n0 + t * cpg < N) {
+                double s = 0.0, q = 0.0;
+                for (int c = t * cpg; c < (t + 1) * cpg; c += 4) {
+                    const int w = c % TWN;
+                    for (int wm_ = 0; wm_ < WAVES_M; wm_++) {
+                        const float *d = gnl + (((wm_ * WAVES_N + c / TWN) * FNT + w / 16) * 4 + (w % 16) / 4) * 2;
+                        s += (double)d[0];
+                        q += (double)d[1];
+                    }
+                }
+                double *dst = P.gn_part + ((size_t)(m0 / BM) * G + n0 / cpg + t) * 2;
+                dst[0] = s;
+                dst[1] = q;
+            }
+        }
     }
 }
 
@@ -1052,6 +1114,15 @@ extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {
     P.conv_cpt_shift = __builtin_ctz((unsigned)c->cin) - 6;
     P.conv_cin_bshift = __builtin_ctz((unsigned)c->cin) + 1;
     P.conv_in_bytes = (unsigned)in_bytes;
+    if (c->gn_part) {
+        const int G = c->gn_groups, cpg = G > 0 && p.N % G == 0 ? p.N / G : 0;
+        if (cpg == 0 || cpg % 4 || bnt % cpg || c->splits > 1 || ((uintptr_t)c->gn_part & 7))
+            return iris_set_error("conv3x3: GroupNorm statistics need groups of a multiple of 4 channels dividing the "
+                                  "%d-wide tile, no split-K and an 8-byte aligned buffer (cout %d, groups %d, splits %d)",
+                                  bnt, p.N, G, c->splits);
+        P.gn_part = c->gn_part;
+        P.gn_groups = G;
+    }
     int chunks = 1;
     long long stride = 0;
     P.chunks[0] = 1;

@@ -73,6 +73,10 @@ struct iris_vae_gpu {
     float *dimg;
     double *part;
     size_t ws_bytes;
+    /* part holds the GroupNorm sums of st_buf (st_nblk row tiles), written
+     * by the convolution that produced it; NULL: none pending */
+    const void *st_buf;
+    int st_nblk;
 };
 
 static int fail(const char *what) {
@@ -476,7 +480,10 @@ static int ensure_work(iris_vae_gpu_t *v, int lh, int lw) {
     ALLOC(v->t, P * 256 * 2);
     ALLOC(v->h, P * 256 * 2);
     ALLOC(v->raw, P * 256 * 2);
-    ALLOC(v->part, (size_t)GN_BLOCKS * VAE_GROUPS * 2 * sizeof(double));
+    /* the statistics pass's blocks, or one per 256-pixel row tile of a
+     * convolution that forms the sums in its epilogue */
+    ALLOC(v->part, (size_t)(GN_BLOCKS > (P + 255) / 256 ? GN_BLOCKS : (P + 255) / 256) * VAE_GROUPS * 2 *
+                       sizeof(double));
     ALLOC(v->ab, 2 * 512 * sizeof(float));
     ALLOC(v->qkv, S * 3 * VAE_MID * 2);
     ALLOC(v->att, S * VAE_MID * 2);
@@ -499,13 +506,17 @@ oom:
 
 static int gn(iris_vae_gpu_t *v, const void *x, int is_bf16, int pix, int C, const float *g, const float *b,
               int swish, uint16_t *y, uint16_t *raw) {
-    const int nblk = iris_hip_gn_stats(x, is_bf16, pix, C, VAE_GROUPS, v->part, GN_BLOCKS);
+    /* the sums from the producing convolution's epilogue, or a statistics pass */
+    const int nblk = v->st_buf == x ? v->st_nblk : iris_hip_gn_stats(x, is_bf16, pix, C, VAE_GROUPS, v->part, GN_BLOCKS);
+    v->st_buf = NULL;
     if (nblk < 0 || iris_hip_gn_finalize(v->part, nblk, pix, C, VAE_GROUPS, g, b, v->eps, v->ab)) return -1;
     return iris_hip_gn_apply(x, is_bf16, v->ab, pix, C, swish, y, raw);
 }
 
+/* stats: the output feeds a GroupNorm, so an unsplit convolution also forms
+ * its GroupNorm sums (cout / VAE_GROUPS channels per group) */
 static int conv(iris_vae_gpu_t *v, const uint16_t *in, const uint16_t *w, const float *b, void *out, int H, int W,
-                int cin, int cout, int up, int epi) {
+                int cin, int cout, int up, int epi, int stats) {
     iris_conv3x3_t c;
     memset(&c, 0, sizeof(c));
     c.in = in;
@@ -528,11 +539,23 @@ static int conv(iris_vae_gpu_t *v, const uint16_t *in, const uint16_t *w, const 
         c.ws = v->ws;
         c.ws_bytes = v->ws_bytes;
     }
-    return iris_hip_conv3x3(&c);
+    stats = stats && c.splits <= 1 && cout % (4 * VAE_GROUPS) == 0;
+    if (stats) {
+        c.gn_part = v->part;
+        c.gn_groups = VAE_GROUPS;
+    }
+    v->st_buf = NULL;
+    if (iris_hip_conv3x3(&c)) return -1;
+    if (stats) {
+        v->st_buf = out;
+        v->st_nblk = (H * W + 255) / 256;
+    }
+    return 0;
 }
 
-static int gemm(const uint16_t *A, int lda, const uint16_t *W, int ldw, void *out, int ldo, const float *bias, int M,
-                int N, int K, int epi) {
+static int gemm(iris_vae_gpu_t *v, const uint16_t *A, int lda, const uint16_t *W, int ldw, void *out, int ldo,
+                const float *bias, int M, int N, int K, int epi) {
+    v->st_buf = NULL;
     iris_gemm_problem_t p;
     memset(&p, 0, sizeof(p));
     p.A = A; p.W = W; p.out = out; p.vec = bias;
@@ -551,17 +574,17 @@ static void swap(float **a, float **b) {
 static int resblock(iris_vae_gpu_t *v, const vres_t *r, int H, int W) {
     const int P = H * W;
     if (gn(v, v->x, 0, P, r->cin, r->n1g, r->n1b, 1, v->t, r->sk ? v->raw : NULL) ||
-        conv(v, v->t, r->c1, r->c1b, v->h, H, W, r->cin, r->cout, 0, IRIS_EPI_BF16) ||
+        conv(v, v->t, r->c1, r->c1b, v->h, H, W, r->cin, r->cout, 0, IRIS_EPI_BF16, 1) ||
         gn(v, v->h, 1, P, r->cout, r->n2g, r->n2b, 1, v->t, NULL))
         return -1;
     if (r->sk) {
-        if (gemm(v->raw, r->cin, r->sk, r->cin, v->y, r->cout, r->skb, P, r->cout, r->cin, IRIS_EPI_F32) ||
-            conv(v, v->t, r->c2, r->c2b, v->y, H, W, r->cout, r->cout, 0, IRIS_EPI_ADD))
+        if (gemm(v, v->raw, r->cin, r->sk, r->cin, v->y, r->cout, r->skb, P, r->cout, r->cin, IRIS_EPI_F32) ||
+            conv(v, v->t, r->c2, r->c2b, v->y, H, W, r->cout, r->cout, 0, IRIS_EPI_ADD, 1))
             return -1;
         swap(&v->x, &v->y);
         return 0;
     }
-    return conv(v, v->t, r->c2, r->c2b, v->x, H, W, r->cout, r->cout, 0, IRIS_EPI_ADD);
+    return conv(v, v->t, r->c2, r->c2b, v->x, H, W, r->cout, r->cout, 0, IRIS_EPI_ADD, 1);
 }
 
 /* attnblock_forward (iris_vae.c:260-357): single head over the S pixels,
@@ -569,17 +592,17 @@ static int resblock(iris_vae_gpu_t *v, const vres_t *r, int H, int W) {
 static int attention(iris_vae_gpu_t *v, const vattn_t *a, int H, int W) {
     const int S = H * W, C = VAE_MID, Kp = (S + 63) / 64 * 64, R = score_rows(S, Kp);
     if (gn(v, v->x, 0, S, C, a->g, a->b, 0, v->t, NULL) ||
-        gemm(v->t, C, a->qkv_w, C, v->qkv, 3 * C, a->qkv_b, S, 3 * C, C, IRIS_EPI_BF16) ||
+        gemm(v, v->t, C, a->qkv_w, C, v->qkv, 3 * C, a->qkv_b, S, 3 * C, C, IRIS_EPI_BF16) ||
         iris_hip_transpose_bf16(v->vt, Kp, Kp, v->qkv + 2 * C, 3 * C, S, C))
         return -1;
     for (int q0 = 0; q0 < S; q0 += R) {
         const int r = S - q0 < R ? S - q0 : R;
-        if (gemm(v->qkv + (size_t)q0 * 3 * C, 3 * C, v->qkv + C, 3 * C, v->sc, Kp, NULL, r, S, C, IRIS_EPI_F32) ||
+        if (gemm(v, v->qkv + (size_t)q0 * 3 * C, 3 * C, v->qkv + C, 3 * C, v->sc, Kp, NULL, r, S, C, IRIS_EPI_F32) ||
             iris_hip_softmax_bf16(v->pm, Kp, Kp, v->sc, Kp, r, S) ||
-            gemm(v->pm, Kp, v->vt, Kp, v->att + (size_t)q0 * C, C, NULL, r, C, Kp, IRIS_EPI_BF16))
+            gemm(v, v->pm, Kp, v->vt, Kp, v->att + (size_t)q0 * C, C, NULL, r, C, Kp, IRIS_EPI_BF16))
             return -1;
     }
-    return gemm(v->att, C, a->o_w, C, v->x, C, a->o_b, S, C, C, IRIS_EPI_ADD);
+    return gemm(v, v->att, C, a->o_w, C, v->x, C, a->o_b, S, C, C, IRIS_EPI_ADD);
 }
 
 int iris_vae_gpu_decode_device(iris_vae_gpu_t *v, const float *d_lat, int lh, int lw, uint8_t *d_rgb, float *d_f32) {
@@ -588,9 +611,10 @@ int iris_vae_gpu_decode_device(iris_vae_gpu_t *v, const float *d_lat, int lh, in
         return -1;
     }
     if (ensure_work(v, lh, lw)) return -1;
+    v->st_buf = NULL;
     int H = 2 * lh, W = 2 * lw;
     if (iris_hip_vae_front(v->front, d_lat, v->z, lh, lw, v->lsc, v->lsh, v->divide, v->pqw, v->pqb) ||
-        conv(v, v->front, v->cin_w, v->cin_b, v->x, H, W, VAE_CIN_PAD, VAE_MID, 0, IRIS_EPI_F32) ||
+        conv(v, v->front, v->cin_w, v->cin_b, v->x, H, W, VAE_CIN_PAD, VAE_MID, 0, IRIS_EPI_F32, 1) ||
         resblock(v, &v->mid1, H, W) || attention(v, &v->attn, H, W) || resblock(v, &v->mid2, H, W))
         return fail("decode (mid block)");
     for (int level = 3, bi = 0; level >= 0; level--) {
@@ -601,7 +625,7 @@ int iris_vae_gpu_decode_device(iris_vae_gpu_t *v, const float *d_lat, int lh, in
             /* nearest 2x + conv: the conv reads the bf16 stream through the upsample */
             if (iris_hip_f32_to_bf16(v->raw, v->x, (size_t)H * W * ch) ||
                 conv(v, v->raw, v->ups_w[3 - level], v->ups_b[3 - level], v->y, 2 * H, 2 * W, ch, ch, 1,
-                     IRIS_EPI_F32))
+                     IRIS_EPI_F32, 1))
                 return fail("decode (upsample)");
             swap(&v->x, &v->y);
             H *= 2;
@@ -664,8 +688,9 @@ int iris_vae_gpu_encode_device(iris_vae_gpu_t *v, const float *d_img, int H, int
         return -1;
     }
     if (ensure_work(v, H / 16, W / 16)) return -1;
+    v->st_buf = NULL;
     if (iris_hip_vae_img_in(v->raw, d_img, H, W) ||
-        conv(v, v->raw, v->e_cin_w, v->e_cin_b, v->x, H, W, VAE_CIN_PAD, VAE_BASE, 0, IRIS_EPI_F32))
+        conv(v, v->raw, v->e_cin_w, v->e_cin_b, v->x, H, W, VAE_CIN_PAD, VAE_BASE, 0, IRIS_EPI_F32, 1))
         return fail("encode (conv_in)");
     int h = H, w = W;
     for (int level = 0, bi = 0; level < 4; level++) {
@@ -675,7 +700,7 @@ int iris_vae_gpu_encode_device(iris_vae_gpu_t *v, const float *d_img, int H, int
         if (level < 3) {
             /* pad right/bottom + 3x3 stride 2, in the conv's loads */
             if (iris_hip_f32_to_bf16(v->raw, v->x, (size_t)h * w * ch) ||
-                conv(v, v->raw, v->e_ds_w[level], v->e_ds_b[level], v->y, h / 2, w / 2, ch, ch, 2, IRIS_EPI_F32))
+                conv(v, v->raw, v->e_ds_w[level], v->e_ds_b[level], v->y, h / 2, w / 2, ch, ch, 2, IRIS_EPI_F32, 1))
                 return fail("encode (downsample)");
             swap(&v->x, &v->y);
             h /= 2;
@@ -684,7 +709,7 @@ int iris_vae_gpu_encode_device(iris_vae_gpu_t *v, const float *d_img, int H, int
     }
     if (resblock(v, &v->e_mid1, h, w) || attention(v, &v->e_attn, h, w) || resblock(v, &v->e_mid2, h, w) ||
         gn(v, v->x, 0, h * w, VAE_MID, v->e_no_g, v->e_no_b, 1, v->t, NULL) ||
-        conv(v, v->t, v->e_co_w, v->e_co_b, v->y, h, w, VAE_MID, 2 * v->z, 0, IRIS_EPI_F32) ||
+        conv(v, v->t, v->e_co_w, v->e_co_b, v->y, h, w, VAE_MID, 2 * v->z, 0, IRIS_EPI_F32, 0) ||
         iris_hip_vae_enc_out(d_lat, v->y, v->z, h, w, v->qw, v->qb, v->esc, v->esh))
         return fail("encode (output)");
     return 0;

@@ -122,7 +122,8 @@ class Conv3x3(ctypes.Structure):
     _fields_ = [("inp", ctypes.c_void_p), ("wt", ctypes.c_void_p), ("out", ctypes.c_void_p),
                 ("bias", ctypes.c_void_p), ("H", ctypes.c_int), ("W", ctypes.c_int), ("cin", ctypes.c_int),
                 ("cout", ctypes.c_int), ("up", ctypes.c_int), ("ldo", ctypes.c_int), ("epi", ctypes.c_int),
-                ("splits", ctypes.c_int), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t)]
+                ("splits", ctypes.c_int), ("ws", ctypes.c_void_p), ("ws_bytes", ctypes.c_size_t),
+                ("gn_part", ctypes.c_void_p), ("gn_groups", ctypes.c_int)]
 
 
 class IrisImage(ctypes.Structure):

@@ -1,7 +1,8 @@
 """The VAE decoder's kernels through the C ABI against float64 numpy
 statements of the same operations on the same bf16-rounded inputs:
 the implicit-GEMM 3x3 convolution (padding, fused nearest upsample, ragged
-pixel counts, cout below the tile width, split-K, each epilogue), GroupNorm
+pixel counts, cout below the tile width, split-K, each epilogue, the
+GroupNorm sums of its epilogue), GroupNorm
 + swish, the bf16 softmax, the transpose, the latent front end and
 conv_out with the uint8 conversion."""
 import ctypes
@@ -115,6 +116,75 @@ def test_conv3x3_stride2(lib, H, W, cin, cout, splits):
     assert lib.iris_hip_conv3x3(ctypes.byref(c)) == 0, lib.iris_hip_last_error()
     assert lib.iris_hip_sync() == 0
     assert tl.rel_l2(o.get(np.float32, (H, W, cout)), ref) < 1e-5
+
+
+@pytest.mark.parametrize("H,W,cin,cout,up,epi", [
+    (20, 30, 64, 128, 0, EPI_BF16),    # 128-wide tile, ragged last row tile, sums before the bf16 rounding
+    (16, 24, 128, 256, 1, EPI_F32),    # 256-wide tile through the upsample
+    (13, 21, 64, 512, 0, EPI_ADD),     # two 256-wide column tiles, the updated stream's sums
+    (9, 34, 128, 128, 2, EPI_F32),     # stride-2 convolution
+])
+def test_conv3x3_groupnorm_sums(lib, H, W, cin, cout, up, epi):
+    """The GroupNorm sums a convolution forms in its epilogue: per row tile of
+    256 output pixels and group of cout / 32 channels, the sum and sum of
+    squares of exactly the f32 values it writes (the updated stream for the
+    residual add, the values before rounding for bf16), in the layout
+    iris_hip_gn_finalize reads, which then gives the statistics pass's scale
+    and shift."""
+    G = 32
+    rng = np.random.default_rng(H * W * cout + up)
+    hi = 2 * H if up == 2 else H >> up
+    wi = 2 * W if up == 2 else W >> up
+    x = rng.standard_normal((hi, wi, cin)).astype(np.float32)
+    wt = (rng.standard_normal((cout, 9, cin)) / np.sqrt(9 * cin)).astype(np.float32)
+    b = (0.3 * rng.standard_normal(cout)).astype(np.float32)
+    dx, dw, db = tl.Dev.of(tl.to_bf16(x)), tl.Dev.of(tl.to_bf16(wt)), tl.Dev.of(b)
+    P, tiles = H * W, (H * W + 255) // 256
+    part = tl.Dev(tiles * G * 2 * 8)
+    x0 = (2.0 + rng.standard_normal((P, cout))).astype(np.float32)
+    out = tl.Dev.of(x0) if epi == EPI_ADD else tl.Dev(P * cout * (2 if epi == EPI_BF16 else 4))
+    c = Conv(dx.ptr, dw.ptr, out.ptr, db.ptr, H, W, cin, cout, up, cout, epi, 1, None, 0, part.ptr, G)
+    assert lib.iris_hip_conv3x3(ctypes.byref(c)) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    sums = part.get(np.float64, (tiles, G, 2))
+    if epi == EPI_BF16:
+        # the rounded output cannot give the pre-rounding values: the same conv with the f32 epilogue can
+        o32 = tl.Dev(P * cout * 4)
+        c32 = Conv(dx.ptr, dw.ptr, o32.ptr, db.ptr, H, W, cin, cout, up, cout, EPI_F32, 1, None, 0, None, 0)
+        assert lib.iris_hip_conv3x3(ctypes.byref(c32)) == 0 and lib.iris_hip_sync() == 0
+        y = o32.get(np.float32, (P, cout)).astype(np.float64)
+    else:
+        y = out.get(np.float32, (P, cout)).astype(np.float64)
+    ypad = np.zeros((tiles * 256, cout))
+    ypad[:P] = y
+    yt = ypad.reshape(tiles, 256, G, cout // G)
+    want = np.stack([yt.sum(axis=(1, 3)), (yt * yt).sum(axis=(1, 3))], axis=-1)
+    np.testing.assert_allclose(sums, want, rtol=1e-5, atol=1e-3)
+    # iris_hip_gn_finalize over these sums == over the statistics pass's
+    gamma, beta = tl.Dev.of((1 + 0.1 * rng.standard_normal(cout)).astype(np.float32)), tl.Dev.of(
+        (0.1 * rng.standard_normal(cout)).astype(np.float32))
+    ab1, ab2 = tl.Dev(2 * cout * 4), tl.Dev(2 * cout * 4)
+    assert lib.iris_hip_gn_finalize(part.ptr, tiles, P, cout, G, gamma.ptr, beta.ptr, ctypes.c_float(1e-6),
+                                    ab1.ptr) == 0
+    sp = tl.Dev(1024 * G * 2 * 8)
+    src = o32 if epi == EPI_BF16 else out
+    nblk = lib.iris_hip_gn_stats(src.ptr, 0, P, cout, G, sp.ptr, 1024)
+    assert nblk > 0
+    assert lib.iris_hip_gn_finalize(sp.ptr, nblk, P, cout, G, gamma.ptr, beta.ptr, ctypes.c_float(1e-6), ab2.ptr) == 0
+    assert lib.iris_hip_sync() == 0
+    np.testing.assert_allclose(ab1.get(np.float32, (2, cout)), ab2.get(np.float32, (2, cout)), rtol=2e-5, atol=2e-5)
+
+
+def test_conv3x3_groupnorm_sums_rejects(lib):
+    """Sums need groups of a multiple of 4 channels that divide the tile, no
+    split-K and an aligned buffer."""
+    d = tl.Dev(1 << 22)
+    bad = [Conv(d.ptr, d.ptr, d.ptr, None, 16, 16, 64, 128, 0, 128, EPI_F32, 1, None, 0, d.ptr, 64),    # 2 per group
+           Conv(d.ptr, d.ptr, d.ptr, None, 16, 16, 64, 96, 0, 96, EPI_F32, 1, None, 0, d.ptr, 32),     # 3 per group
+           Conv(d.ptr, d.ptr, d.ptr, None, 16, 16, 64, 128, 0, 128, EPI_F32, 2, d.ptr, 1 << 20, d.ptr, 32),
+           Conv(d.ptr, d.ptr, d.ptr, None, 16, 16, 64, 128, 0, 128, EPI_F32, 1, None, 0, d.ptr + 4, 32)]
+    for c in bad:
+        assert lib.iris_hip_conv3x3(ctypes.byref(c)) != 0
 
 
 def test_conv3x3_rejects(lib):
