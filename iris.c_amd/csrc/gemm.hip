@@ -483,12 +483,27 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * stores them as 16-byte chunks of whole rows, so one store instruction
      * covers full 128-byte lines instead of 32-byte pieces of 16 rows (the
      * direct stores left the waves stalled on issue). */
-    if (!gn && full && (ldo & 7) == 0 && (pr.epi == IRIS_EPI_BF16 || (BNT == BN && pr.epi == IRIS_EPI_SWIGLU))) {
+    bool staged = false;
+    if (full && (ldo & 7) == 0 && (pr.epi == IRIS_EPI_BF16 || (BNT == BN && pr.epi == IRIS_EPI_SWIGLU))) {
+        if (gn) {   /* a convolution's bf16 tile: the sums of the values before rounding */
+#pragma unroll
+            for (int ni = 0; ni < FNT; ni++) {
+                const float4 t = vec ? *(const float4 *)(vec + colb + ni * 16) : make_float4(0, 0, 0, 0);
+#pragma unroll
+                for (int mi = 0; mi < FM; mi++) {
+                    gn_add(ni, acc[mi][ni][0] + t.x);
+                    gn_add(ni, acc[mi][ni][1] + t.y);
+                    gn_add(ni, acc[mi][ni][2] + t.z);
+                    gn_add(ni, acc[mi][ni][3] + t.w);
+                }
+            }
+        }
         if (pr.epi == IRIS_EPI_SWIGLU) stage_out<BNT / 2, true, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0 >> 1, wm, wn, TWN);
         else stage_out<BNT, false, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0, wm, wn, TWN);
-        return;
+        if (!gn) return;
+        staged = true;
     }
-    switch (pr.epi) {
+    if (!staged) switch (pr.epi) {
     case IRIS_EPI_F32:
     case IRIS_EPI_BF16:
     case IRIS_EPI_GATED_ADD:
