@@ -12,7 +12,7 @@ import pytest
 import iris_testlib as tl
 
 pytestmark = pytest.mark.gpu
-EPI_F32, EPI_BF16, EPI_GATED_ADD, EPI_SWIGLU, EPI_F32_T = range(5)
+EPI_F32, EPI_BF16, EPI_GATED_ADD, EPI_SWIGLU, EPI_F32_T, EPI_ADD = range(6)
 
 
 @pytest.fixture(scope="module")
@@ -255,17 +255,21 @@ def cu_count(lib):
 @pytest.mark.parametrize("rows,N,K,epi", [((512, 1024), 3072, 3072, EPI_GATED_ADD),
                                           ((512, 1024), 3072, 9216, EPI_GATED_ADD),
                                           ((1536,), 3072, 12288, EPI_GATED_ADD), ((300, 77), 640, 1024, EPI_F32),
-                                          ((200, 130), 512, 2048, EPI_SWIGLU), ((4608,), 3072, 3072, EPI_GATED_ADD)])
+                                          ((200, 130), 512, 2048, EPI_SWIGLU), ((4608,), 3072, 3072, EPI_GATED_ADD),
+                                          ((1536,), 4096, 2048, EPI_SWIGLU), ((1536,), 3072, 2048, EPI_BF16),
+                                          ((1000, 700), 2000, 1536, EPI_F32), ((1536,), 3072, 1024, EPI_ADD)])
 def test_gemm_fill_n(lib, rows, N, K, epi):
     """iris_hip_gemm_fill_n: the txt and img streams of a 512x512 double
     block (512 + 1024 rows; out projection K 3072, down projection K 9216)
     and the single block's out projection (1536 x 3072 x 12288), split over
     K in one launch of both problems, against float64; bit for bit equal to
     iris_hip_gemm_splitk of each problem alone with the same chunk count,
-    and repeatable. Also ragged rows with an output row stride that is not a
-    multiple of 4 (the reduce's one-element path), SwiGLU split, and a
-    product that fills the chip (4608 rows: the plain launch, equal to
-    iris_hip_gemm bit for bit)."""
+    and repeatable (also under the per-kernel profile, which asserts one
+    reduce launch for a split). Also ragged rows and columns with an output
+    row stride that is not a multiple of 4 (the reduce's one-element path),
+    SwiGLU, bf16 and residual-add epilogues, and a product that fills the
+    chip (4608 rows: the plain launch, equal to iris_hip_gemm bit for
+    bit)."""
     rng = np.random.default_rng(sum(rows) + N + K)
     cus = cu_count(lib)
     P = tl.GemmProblem
@@ -285,16 +289,20 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
     lib.iris_hip_gemm_fill_n.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
     lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
 
+    bf16_out = epi in (EPI_SWIGLU, EPI_BF16)
+    kernels = []
+
     def run(mode):
         outs, probs = [], []
         for m, a, w, vec, x0, ldo, dA, dW, dV in ins:
-            bf16_out = epi == EPI_SWIGLU
             o = tl.Dev(m * ldo * 2) if bf16_out else tl.Dev.of(x0)
             probs.append(P(dA.ptr, dW.ptr, o.ptr, dV.ptr if epi != EPI_SWIGLU else None, m, N, K, K, K, ldo, epi))
             outs.append(o)
         arr = (P * len(probs))(*probs)
         if mode == "fill":
             assert lib.iris_hip_gemm_fill_n(arr, len(probs), ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+        elif mode == "fill_profiled":
+            kernels.extend(launched_kernels(lib, lambda: lib.iris_hip_gemm_fill_n(arr, len(probs), ws.ptr, ws_bytes)))
         elif mode == "alone":
             for pr in probs:
                 assert lib.iris_hip_gemm_splitk(ctypes.byref(pr), splits, ws.ptr, ws_bytes) == 0, \
@@ -304,14 +312,13 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
         assert lib.iris_hip_sync() == 0
         res = []
         for o, (m, a, w, vec, x0, ldo, *_) in zip(outs, ins):
-            res.append(tl.bf16_to_f32(o.get(np.uint16, (m, ldo))) if epi == EPI_SWIGLU else
-                       o.get(np.float32, (m, ldo)))
+            res.append(tl.bf16_to_f32(o.get(np.uint16, (m, ldo))) if bf16_out else o.get(np.float32, (m, ldo)))
             o.close()
         return res
 
-    got, again = run("fill"), run("fill")
-    for g, g2, (m, a, w, vec, x0, ldo, *_) in zip(got, again, ins):
-        assert np.array_equal(g, g2), "not repeatable"
+    got, again, third = run("fill"), run("fill"), run("fill_profiled")
+    for g, g2, g3, (m, a, w, vec, x0, ldo, *_) in zip(got, again, third, ins):
+        assert np.array_equal(g, g2) and np.array_equal(g, g3), "not repeatable"
         y = a.astype(np.float64) @ w.astype(np.float64).T
         if epi == EPI_SWIGLU:
             gt = np.concatenate([y[:, c * 64:c * 64 + 32] for c in range(N // 64)], 1)
@@ -319,13 +326,61 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
             assert tl.rel_l2(g, gt / (1 + np.exp(-gt)) * up) < 4e-3
         elif epi == EPI_GATED_ADD:
             assert tl.rel_l2(g, x0 + vec * y) < 1e-5
+        elif epi == EPI_ADD:
+            assert tl.rel_l2(g, x0 + y + vec) < 1e-5
+        elif epi == EPI_BF16:
+            assert tl.rel_l2(g, y + vec) < 4e-3
         else:
             assert tl.rel_l2(g[:, :N], y + vec) < 1e-5
             assert np.array_equal(g[:, N:], x0[:, N:]), "wrote past N"
+    reduce_pass = any("splitk_reduce_kernel" in k for k in kernels)
+    assert reduce_pass == (splits > 1), (splits, kernels)
     want = run("alone" if splits > 1 else "plain")
     for g, w_ in zip(got, want):
         assert np.array_equal(g, w_), f"differs from the {'split-K' if splits > 1 else 'plain'} launch"
     print(f"fill_n {rows} x {N} x {K}: {splits} chunks")
+
+
+def test_gemm_fill_split_in_graph(lib):
+    """A product split over K into 3 chunks (1536 x 3072 x 3072, gated
+    residual add; the 512x512 single block's shape class) captured into a
+    graph with its reduce launch: each replay, with an eager launch of the
+    same product between replays, equals the eager result bit for bit."""
+    M, N, K = 1536, 3072, 3072
+    rng = np.random.default_rng(77)
+    A = tl.Dev.of(tl.to_bf16(bf(rng.standard_normal((M, K), np.float32))))
+    W = tl.Dev.of(tl.to_bf16(bf(rng.standard_normal((N, K), np.float32) * 0.02)))
+    V = tl.Dev.of(rng.standard_normal(N).astype(np.float32))
+    x0 = rng.standard_normal((M, N), np.float32)
+    o = tl.Dev.of(x0)
+    ws_bytes = 64 << 20
+    ws = tl.Dev(ws_bytes)
+    lib.iris_hip_gemm_fill.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t]
+    lib.iris_hip_graph_end.restype = ctypes.c_void_p
+    lib.iris_hip_graph_launch.argtypes = [ctypes.c_void_p]
+    lib.iris_hip_graph_destroy.argtypes = [ctypes.c_void_p]
+    pr = tl.GemmProblem(A.ptr, W.ptr, o.ptr, V.ptr, M, N, K, K, K, N, EPI_GATED_ADD)
+    assert "splitk_reduce_kernel" in launched_kernels(lib, lambda: lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr,
+                                                                                          ws_bytes))
+    o.put(x0)
+    assert lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr, ws_bytes) == 0, lib.iris_hip_last_error()
+    assert lib.iris_hip_sync() == 0
+    ref = o.get(np.float32, (M, N))
+    assert lib.iris_hip_graph_begin() == 0, lib.iris_hip_last_error()
+    rc = lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr, ws_bytes)
+    g = lib.iris_hip_graph_end()
+    assert rc == 0 and g, lib.iris_hip_last_error()
+    try:
+        for _ in range(3):
+            o.put(x0)
+            assert lib.iris_hip_graph_launch(g) == 0 and lib.iris_hip_sync() == 0, lib.iris_hip_last_error()
+            assert np.array_equal(o.get(np.float32, (M, N)), ref), "graph replay differs"
+            o.put(x0)
+            assert lib.iris_hip_gemm_fill(ctypes.byref(pr), ws.ptr, ws_bytes) == 0
+            assert lib.iris_hip_sync() == 0
+            assert np.array_equal(o.get(np.float32, (M, N)), ref), "eager launch after a replay differs"
+    finally:
+        lib.iris_hip_graph_destroy(g)
 
 
 def launched_kernels(lib, fn):
