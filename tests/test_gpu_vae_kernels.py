@@ -225,8 +225,12 @@ def test_group_norm(lib, pixels, C, is_bf16, swish):
     assert np.array_equal(raw.get(np.uint16, (pixels, C)), tl.to_bf16(xin.astype(np.float32)))
 
 
-@pytest.mark.parametrize("rows,cols,pad", [(3, 1024, 1024), (70, 60, 64), (5, 16384, 16384)])
+@pytest.mark.parametrize("rows,cols,pad", [(3, 1024, 1024), (70, 60, 64), (5, 16384, 16384), (4, 6000, 6016),
+                                           (3, 4096, 4160), (2, 20000, 20032)])
 def test_softmax_bf16(lib, rows, cols, pad):
+    """Row softmax to bf16 against float64, up to the 1024x1024 bottleneck's
+    16384 columns and beyond, with ragged and padded rows (padding columns
+    written as zero)."""
     rng = np.random.default_rng(cols)
     s = (rng.standard_normal((rows, pad)) * 4).astype(np.float32)
     ds, dp = tl.Dev.of(s), tl.Dev(rows * pad * 2)
