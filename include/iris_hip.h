@@ -220,6 +220,16 @@ int iris_hip_vae_enc_out(float *d_latent, const float *d_moments, int z, int h, 
 /* Row softmax, f32 scores [rows][ld_s] -> bf16 [rows][ld_p], columns
  * cols..cols_pad-1 zeroed (iris_softmax in attnblock_forward, iris_vae.c:335). */
 int iris_hip_softmax_bf16(uint16_t *d_p, int ld_p, int cols_pad, const float *d_s, int ld_s, int rows, int cols);
+/* The same softmax over the scaled products of one attention head, with no
+ * f32 score matrix (the scores of attnblock_forward, iris_vae.c:320-335):
+ * s[m][n] = scale * q[m] . k[n] over d (q [M][ld_q], k [N][ld_k] bf16,
+ * d % 64 == 0), p[m][n] = exp(s - max_n s) / sum_n exp(s - max_n s) in bf16
+ * into p [M][ld_p], columns N..pad_n-1 zeroed (pad_n <= N rounded up to 256).
+ * Two passes over the products: the first writes each 256-column tile's row
+ * (max, sum) into stat (M * ceil(N / 256) float pairs) and merges them per
+ * row into row (M float pairs), the second writes p. */
+int iris_hip_softmax_scores(const uint16_t *d_q, int ld_q, const uint16_t *d_k, int ld_k, int M, int N, int d,
+                            float scale, uint16_t *d_p, int ld_p, int pad_n, float *d_stat, float *d_row);
 /* dst[c][r] = src[r][c] (bf16), rows..rows_pad-1 zero-filled; rows_pad % 64 == 0 */
 int iris_hip_transpose_bf16(uint16_t *d_dst, int ld_dst, int rows_pad, const uint16_t *d_src, int ld_src, int rows,
                             int cols);

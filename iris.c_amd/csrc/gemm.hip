@@ -81,6 +81,15 @@ struct GemmParams {
      * split-K): per row tile and group, sum and sum of squares in f64 */
     double *gn_part;
     int gn_groups;
+    /* row softmax of scaled products (MODES 4, 5; one problem): s = sm_scale
+     * * acc in log2 units, columns past N excluded. MODE 4: per row and tile,
+     * (max s, sum 2^(s - max)) into sm_stat[row * tiles_n + tile column];
+     * MODE 5: bf16 2^(s - sm_row[row].x) * sm_row[row].y into out, and zeros
+     * in columns N .. sm_pad - 1 */
+    float sm_scale;
+    float2 *sm_stat;
+    const float2 *sm_row;
+    int sm_pad;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) {   /* element offset in a tile */
@@ -160,14 +169,102 @@ __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_
     }
 }
 
+/* The two epilogues of MODE 4 (the products of one query block against the
+ * keys of one 256-wide tile): per-row statistics of the tile, or the
+ * probabilities. Lane l holds row lr of each 16x16 tile at columns
+ * lg*4 .. lg*4+3; a row's 256 columns are spread over the 4 lanes lr + 16j of
+ * a wave and the 2 waves across N. */
+template <bool STATS, int FNT_>
+__device__ __forceinline__ void softmax_epilogue(f32x4 (&acc)[FM][FNT_], const GemmParams &P,
+                                                 const iris_gemm_problem_t &pr, int m0, int n0, int tn, int wm, int wn,
+                                                 uint16_t *lds0, uint16_t *lds1) {
+    constexpr int TWN_ = FNT_ * 16, BNT_ = TWN_ * WAVES_N;
+    const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int M = pr.M, N = pr.N;
+    const int rowb = m0 + wm * TW_M + lr, colb = n0 + wn * TWN_ + lg * 4;
+    /* scaled scores in place; columns past N hold -inf (2^-inf = 0) */
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++)
+#pragma unroll
+        for (int ni = 0; ni < FNT_; ni++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                acc[mi][ni][r] = colb + ni * 16 + r < N ? acc[mi][ni][r] * P.sm_scale : -INFINITY;
+    if constexpr (STATS) {
+        /* the tile's row max, then its row sum of 2^(s - max): lane, the
+         * row's 4 lanes (xor 16, 32), the 2 waves across N (in LDS) */
+        __shared__ float red[2][WAVES_N][BM];
+#pragma unroll
+        for (int mi = 0; mi < FM; mi++) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int ni = 0; ni < FNT_; ni++)
+                m = fmaxf(m, fmaxf(fmaxf(acc[mi][ni][0], acc[mi][ni][1]), fmaxf(acc[mi][ni][2], acc[mi][ni][3])));
+            m = fmaxf(m, __shfl_xor(m, 16, 64));
+            m = fmaxf(m, __shfl_xor(m, 32, 64));
+            if (lg == 0) red[0][wn][wm * TW_M + mi * 16 + lr] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mi = 0; mi < FM; mi++) {
+            const int rr = wm * TW_M + mi * 16 + lr;
+            const float mt = fmaxf(red[0][0][rr], red[0][1][rr]);
+            float l = 0.0f;
+#pragma unroll
+            for (int ni = 0; ni < FNT_; ni++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) l += __builtin_amdgcn_exp2f(acc[mi][ni][r] - mt);
+            l += __shfl_xor(l, 16, 64);
+            l += __shfl_xor(l, 32, 64);
+            if (lg == 0) red[1][wn][rr] = l;
+        }
+        __syncthreads();
+        if (tid < BM && m0 + tid < M)
+            P.sm_stat[(size_t)(m0 + tid) * P.tiles_n[0] + tn] =
+                make_float2(fmaxf(red[0][0][tid], red[0][1][tid]), red[1][0][tid] + red[1][1][tid]);
+        return;
+    } else {
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++) {
+        const int row = rowb + mi * 16;
+        const float2 rs = row < M ? P.sm_row[row] : make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int ni = 0; ni < FNT_; ni++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[mi][ni][r] = __builtin_amdgcn_exp2f(acc[mi][ni][r] - rs.x) * rs.y;
+    }
+    const int ldo = pr.ldo;
+    if (m0 + BM <= M && n0 + BNT_ <= N && (ldo & 7) == 0 && ((uintptr_t)pr.out & 15) == 0) {
+        stage_out<BNT_, false, FM, FNT_>(acc, lds0, lds1, pr, nullptr, m0, n0, wm, wn, TWN_);
+        return;
+    }
+    /* edge tiles element by element, zeros in the padding columns */
+#pragma unroll
+    for (int mi = 0; mi < FM; mi++) {
+        const int row = rowb + mi * 16;
+        if (row >= M) continue;
+#pragma unroll
+        for (int ni = 0; ni < FNT_; ni++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int col = colb + ni * 16 + r;
+                if (col < P.sm_pad)
+                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = col < N ? f2bf_hw(acc[mi][ni][r]) : (uint16_t)0;
+            }
+    }
+    }
+}
+
 /* MODE 0: GEMM; 1: 3x3 convolution, stride 1, input optionally read through
  * a nearest 2x upsample; 2: 3x3 convolution, stride 2, right/bottom padding;
- * 3: GEMM with a second K segment (A2, W2) after the first. The modes are
+ * 3: GEMM with a second K segment (A2, W2) after the first; 4, 5: GEMMs
+ * whose epilogue is a row softmax pass (softmax_epilogue: row statistics,
+ * probabilities). The modes are
  * separate kernels: the load-issue phase has no cycles to spare for the
  * address arithmetic of the modes it does not run. */
 template <int MODE, int BNT = BN>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
-    constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3;
+    constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3, SMX = MODE == 4 || MODE == 5;
     /* BNT: block tile width, 256, or (MODE 0, no SwiGLU) 224 = 2 waves x 7
      * MFMA tiles, for launches whose 256-wide tiles leave the last wave of
      * blocks part-empty, or (convolutions) 128 = 2 waves x 4 MFMA tiles for
@@ -455,6 +552,10 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
     WAIT(0, 0);   /* no DMA outstanding at exit */
 #undef WAIT
+    if constexpr (SMX) {
+        softmax_epilogue<MODE == 4, FNT>(acc, P, pr, m0, n0, tn, wm, wn, lds0, lds1);
+        return;
+    }
 
     /* ---- epilogue: W is the MFMAs' first operand, so lane l holds row lr of
      *      each 16x16 tile at the 4 consecutive columns lg*4 .. lg*4+3 ---- */
@@ -1084,6 +1185,63 @@ extern "C" int iris_hip_gemm_fill_n(const iris_gemm_problem_t *probs, int n, flo
 extern "C" int iris_hip_gemm_fill(const iris_gemm_problem_t *p, float *ws, size_t ws_bytes) {
     if (!p) return iris_set_error("gemm_fill: null problem");
     return iris_hip_gemm_fill_n(p, 1, ws, ws_bytes);
+}
+
+namespace {
+
+/* per row, one wave: the tiles' (max, sum) pairs merged into (max, 1 / sum);
+ * lane j takes tiles j, j + 64, ..., then the wave's butterfly (a fixed
+ * order) */
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const float2 *stat, int tiles, int rows,
+                                                           float2 *row_out) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const float2 *s = stat + (size_t)r * tiles;
+    float m = -INFINITY;
+    for (int t = lane; t < tiles; t += 64) m = fmaxf(m, s[t].x);
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float l = 0.0f;
+    for (int t = lane; t < tiles; t += 64) l += s[t].y * __builtin_amdgcn_exp2f(s[t].x - m);
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) row_out[r] = make_float2(m, 1.0f / l);
+}
+
+}  // namespace
+
+extern "C" int iris_hip_softmax_scores(const uint16_t *q, int ld_q, const uint16_t *k, int ld_k, int M, int N, int d,
+                                       float scale, uint16_t *p, int ld_p, int pad_n, float *stat, float *row) {
+    if (!q || !k || !p || !stat || !row || M <= 0 || N <= 0)
+        return iris_set_error("softmax_scores: null buffer or empty shape (%d x %d)", M, N);
+    const int tiles_n = (N + BN - 1) / BN;
+    if (pad_n < N || pad_n > tiles_n * BN || ld_p < pad_n)
+        return iris_set_error("softmax_scores: pad %d for %d columns (ld %d)", pad_n, N, ld_p);
+    if (((uintptr_t)stat | (uintptr_t)row) & 7) return iris_set_error("softmax_scores: statistics not 8-byte aligned");
+    if ((long long)M * tiles_n >= (1LL << 31)) return iris_set_error("softmax_scores: too many rows");
+    GemmParams P;
+    memset(&P, 0, sizeof(P));
+    iris_gemm_problem_t &pr = P.p[0];
+    pr.A = q; pr.lda = ld_q; pr.W = k; pr.ldw = ld_k; pr.out = p; pr.ldo = ld_p;
+    pr.M = M; pr.N = N; pr.K = d; pr.epi = IRIS_EPI_BF16;
+    if (check_problem(pr)) return -1;
+    P.nprob = 1;
+    P.chunks[0] = 1;
+    P.tiles_m[0] = (M + BM - 1) / BM;
+    P.tiles_n[0] = tiles_n;
+    P.total = P.tiles_m[0] * tiles_n;
+    for (int i = 1; i <= MAXP; i++) P.tile_start[i] = P.total;
+    P.per_xcd = (P.total + 7) / 8;
+    P.sm_scale = scale * 1.44269504088896341f;   /* log2(e): scores in log2 units */
+    P.sm_stat = (float2 *)stat;
+    P.sm_pad = pad_n;
+    const dim3 grid(8 * P.per_xcd);
+    IRIS_LAUNCH(gemm_bf16_kernel<4>, grid, dim3(NT), 0, iris_stream(), P);
+    if (iris_launch_check("gemm_bf16_kernel<4> (row statistics)")) return -1;
+    IRIS_LAUNCH(softmax_rows_kernel, dim3((M + 3) / 4), dim3(256), 0, iris_stream(), (const float2 *)stat, tiles_n, M,
+                (float2 *)row);
+    if (iris_launch_check("softmax_rows_kernel")) return -1;
+    P.sm_row = (const float2 *)row;
+    IRIS_LAUNCH(gemm_bf16_kernel<5>, grid, dim3(NT), 0, iris_stream(), P);
+    return iris_launch_check("gemm_bf16_kernel<5> (probabilities)");
 }
 
 extern "C" int iris_hip_conv3x3(const iris_conv3x3_t *c) {

@@ -29,7 +29,7 @@
 #define VAE_GROUPS 32
 #define VAE_CIN_PAD 64         /* conv_in's input channels, zero-padded */
 #define GN_BLOCKS 1024         /* blocks of the GroupNorm statistics pass */
-#define SCORE_ELEMS (1u << 28) /* attention scores held at once (f32) */
+#define SCORE_ELEMS (1u << 28) /* attention probabilities held at once (bf16) */
 
 static const int ch_mult[4] = {1, 2, 4, 4};
 
@@ -67,7 +67,7 @@ struct iris_vae_gpu {
     float *esc, *esh;                          /* latent normalization: (x - esh) * esc */
     /* work buffers, sized for cap_pix output pixels */
     size_t cap_pix;
-    float *x, *y, *sc, *ws, *ab, *dlat, *df32;
+    float *x, *y, *sst, *srow, *ws, *ab, *dlat, *df32;   /* sst, srow: the softmax's row statistics */
     uint16_t *t, *h, *raw, *qkv, *vt, *att, *pm, *front;
     uint8_t *drgb;
     float *dimg;
@@ -262,10 +262,10 @@ static int load_encoder(vsrc_t *s, iris_vae_gpu_t *v) {
 }
 
 static void free_work(iris_vae_gpu_t *v) {
-    void *p[] = {v->x, v->y, v->sc, v->ws, v->ab, v->dlat, v->df32, v->t, v->h, v->raw, v->qkv, v->vt,
+    void *p[] = {v->x, v->y, v->sst, v->srow, v->ws, v->ab, v->dlat, v->df32, v->t, v->h, v->raw, v->qkv, v->vt,
                  v->att, v->pm, v->front, v->drgb, v->part, v->dimg};
     for (size_t i = 0; i < sizeof(p) / sizeof(p[0]); i++) iris_hip_free(p[i]);
-    v->x = v->y = v->sc = v->ws = v->ab = v->dlat = v->df32 = NULL;
+    v->x = v->y = v->sst = v->srow = v->ws = v->ab = v->dlat = v->df32 = NULL;
     v->t = v->h = v->raw = v->qkv = v->vt = v->att = v->pm = v->front = NULL;
     v->drgb = NULL;
     v->dimg = NULL;
@@ -488,7 +488,9 @@ static int ensure_work(iris_vae_gpu_t *v, int lh, int lw) {
     ALLOC(v->qkv, S * 3 * VAE_MID * 2);
     ALLOC(v->att, S * VAE_MID * 2);
     ALLOC(v->vt, (size_t)VAE_MID * Kp * 2);
-    ALLOC(v->sc, n_sc * sizeof(float));
+    /* per row chunk: (max, sum) per row and 256-column tile, (max, 1 / sum) per row */
+    ALLOC(v->sst, (n_sc / 256 + S) * 2 * sizeof(float));
+    ALLOC(v->srow, S * 2 * sizeof(float));
     ALLOC(v->pm, n_sc * 2);
     ALLOC(v->front, S * VAE_CIN_PAD * 2);
     v->ws_bytes = 4 * S * VAE_MID * sizeof(float);   /* split-K at the bottleneck */
@@ -588,7 +590,8 @@ static int resblock(iris_vae_gpu_t *v, const vres_t *r, int H, int W) {
 }
 
 /* attnblock_forward (iris_vae.c:260-357): single head over the S pixels,
- * x += out_proj(softmax(q k^T / sqrt(C)) v); scores in f32, in row chunks */
+ * x += out_proj(softmax(q k^T / sqrt(C)) v) in row chunks; the softmax runs
+ * in the epilogues of two passes over the products (no f32 score matrix) */
 static int attention(iris_vae_gpu_t *v, const vattn_t *a, int H, int W) {
     const int S = H * W, C = VAE_MID, Kp = (S + 63) / 64 * 64, R = score_rows(S, Kp);
     if (gn(v, v->x, 0, S, C, a->g, a->b, 0, v->t, NULL) ||
@@ -597,10 +600,18 @@ static int attention(iris_vae_gpu_t *v, const vattn_t *a, int H, int W) {
         return -1;
     for (int q0 = 0; q0 < S; q0 += R) {
         const int r = S - q0 < R ? S - q0 : R;
-        if (gemm(v, v->qkv + (size_t)q0 * 3 * C, 3 * C, v->qkv + C, 3 * C, v->sc, Kp, NULL, r, S, C, IRIS_EPI_F32) ||
-            iris_hip_softmax_bf16(v->pm, Kp, Kp, v->sc, Kp, r, S) ||
-            gemm(v, v->pm, Kp, v->vt, Kp, v->att + (size_t)q0 * C, C, NULL, r, C, Kp, IRIS_EPI_BF16))
+        /* q rows carry the 1/sqrt(C) scale (load_attn) */
+        if (iris_hip_softmax_scores(v->qkv + (size_t)q0 * 3 * C, 3 * C, v->qkv + C, 3 * C, r, S, C, 1.0f, v->pm, Kp,
+                                    Kp, v->sst, v->srow))
             return -1;
+        /* P V: 512 output columns leave most CUs idle at one chunk of K; split
+         * over K through the convolutions' workspace where that fills them */
+        iris_gemm_problem_t p;
+        memset(&p, 0, sizeof(p));
+        p.A = v->pm; p.lda = Kp; p.W = v->vt; p.ldw = Kp; p.out = v->att + (size_t)q0 * C; p.ldo = C;
+        p.M = r; p.N = C; p.K = Kp; p.epi = IRIS_EPI_BF16;
+        v->st_buf = NULL;
+        if (iris_hip_gemm_fill(&p, v->ws, v->ws_bytes)) return -1;
     }
     return gemm(v, v->att, C, a->o_w, C, v->x, C, a->o_b, S, C, C, IRIS_EPI_ADD);
 }

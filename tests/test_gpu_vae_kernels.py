@@ -33,6 +33,8 @@ def lib():
                                           ctypes.c_int]
     lib.iris_hip_transpose_bf16.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
+    lib.iris_hip_softmax_scores.argtypes = [vp, ctypes.c_int, vp, ctypes.c_int] + [ctypes.c_int] * 3 + [
+        ctypes.c_float, vp, ctypes.c_int, ctypes.c_int, vp, vp]
     lib.iris_hip_vae_conv_out.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
     return lib
 
@@ -241,6 +243,51 @@ def test_softmax_bf16(lib, rows, cols, pad):
     ref = e / e.sum(1, keepdims=True)
     assert tl.rel_l2(got[:, :cols], ref) < 4e-3
     assert not got[:, cols:].any()
+
+
+@pytest.mark.parametrize("M,N,d,scale", [(300, 1000, 512, 1.0), (512, 512, 128, 0.125), (1024, 16384, 512, 1.0),
+                                         (77, 40, 64, 0.3)])
+def test_softmax_scores(lib, M, N, d, scale):
+    """Softmax over scaled products in two passes (tile row statistics, then
+    probabilities): against float64 softmax(scale q k^T) within bf16
+    rounding, rows summing to 1, zeros in the padding columns; ragged rows
+    and columns (edge tiles), the 1024x1024 bottleneck's 16384 keys, and
+    fewer keys than one tile. Repeats bit for bit."""
+    rng = np.random.default_rng(M + N + d)
+    ldq, ldk = 3 * d, 3 * d
+    qkv = bf(rng.standard_normal((max(M, N), ldq), np.float32) * (2.0 / np.sqrt(d)) ** 0.5)
+    q, k = qkv[:M, :d], qkv[:N, d:2 * d]
+    pad = (N + 63) // 64 * 64
+    tiles = (N + 255) // 256
+    dqkv = tl.Dev.of(tl.to_bf16(qkv))
+    dp, dst, drow = tl.Dev(M * pad * 2), tl.Dev(M * tiles * 8), tl.Dev(M * 8)
+    outs = []
+    for _ in range(2):
+        assert lib.iris_hip_memset(dp.ptr, 0xff, M * pad * 2) == 0
+        assert lib.iris_hip_softmax_scores(dqkv.ptr, ldq, dqkv.ptr + d * 2, ldk, M, N, d, scale, dp.ptr, pad, pad,
+                                           dst.ptr, drow.ptr) == 0, lib.iris_hip_last_error()
+        assert lib.iris_hip_sync() == 0
+        outs.append(dp.get(np.uint16, (M, pad)))
+    assert np.array_equal(outs[0], outs[1]), "not repeatable"
+    got = tl.bf16_to_f32(outs[0])
+    s = scale * (q.astype(np.float64) @ k.astype(np.float64).T)
+    e = np.exp(s - s.max(1, keepdims=True))
+    ref = e / e.sum(1, keepdims=True)
+    assert tl.rel_l2(got[:, :N], ref) < 4e-3
+    assert np.abs(got[:, :N].sum(1) - 1.0).max() < 2e-2
+    assert not got[:, N:].any()
+    print(f"softmax_scores {M}x{N}x{d}: rel_l2 {tl.rel_l2(got[:, :N], ref):.2e}")
+
+
+def test_softmax_scores_rejects(lib):
+    """Shapes the two passes do not take: padding past the last tile, d not
+    a multiple of 64, misaligned statistics."""
+    buf, st = tl.Dev(1 << 20), tl.Dev(4096)
+    call = lib.iris_hip_softmax_scores
+    assert call(buf.ptr, 192, buf.ptr, 192, 8, 100, 64, 1.0, buf.ptr, 512, 512, st.ptr, st.ptr) != 0
+    assert call(buf.ptr, 192, buf.ptr, 192, 8, 100, 48, 1.0, buf.ptr, 128, 128, st.ptr, st.ptr) != 0
+    assert call(buf.ptr, 192, buf.ptr, 192, 8, 100, 64, 1.0, buf.ptr, 128, 128, st.ptr + 4, st.ptr) != 0
+    assert call(buf.ptr, 192, buf.ptr, 192, 8, 100, 64, 1.0, buf.ptr, 128, 90, st.ptr, st.ptr) != 0
 
 
 def test_transpose_bf16(lib):
