@@ -5,6 +5,9 @@
  * cblas_sgemm, iris_transformer_flux.c:121-131, iris_kernels.c:220-290) and the
  * elementwise passes that follow them (gated_add :136-143, iris_silu_mul
  * iris_kernels.c:626-638, the split/concat copies :3833-3840, :3897-3902).
+ * The same kernel body also runs the VAE's implicit-GEMM 3x3 convolutions
+ * (iris_vae.c:203-251) and the row softmax of its bottleneck attention in the
+ * epilogues of two passes over the score product (iris_vae.c:320-335).
  *
  * out = A[M,K] . W[N,K]^T. Block tile 256x256x64 with 512 threads = 8 waves in
  * a 4x2 arrangement; each wave owns 64x128 as 4x8 v_mfma_f32_16x16x32_bf16
