@@ -52,7 +52,6 @@ constexpr int WAVES_M = 4, WAVES_N = 2, TW_M = BM / WAVES_M;
 constexpr int FM = TW_M / 16;
 constexpr int TILE_ELEMS = BM * BK;                 /* A tile = W tile = 16384 bf16 */
 constexpr int DMA_ROWS = 8;                         /* rows of one 64-lane x 16-byte LDS-DMA load */
-constexpr int DMA_PER_WAVE = BM / DMA_ROWS / 4;     /* loads per wave for one operand tile = 8 */
 constexpr int GROUP_M = 8;
 constexpr int MAXP = 4;
 
@@ -115,7 +114,8 @@ template <int OC> __device__ __forceinline__ int opos(int row, int col) {
 
 /* bf16 epilogue of a whole tile through LDS (the caller has checked that the
  * tile is in range and the output rows 16-byte aligned). Group g (rows
- * 128 g .. 128 g + 127) stages its rows in stage g. SWIGLU: accumulator
+ * GR g .. GR g + GR - 1, GR = 128 for 256-row tiles) stages its rows in
+ * stage g. SWIGLU: accumulator
  * columns are 32-row gate / up groups, OC = half the tile width. */
 template <int OC, bool SWIGLU, int FM_, int FNT_>
 __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_t *lds0, uint16_t *lds1,
@@ -123,10 +123,11 @@ __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_
                                           int wn, int twn) {
     static_assert(128 * (OC == 256 ? 256 : OC + 8) * 2 <= 2 * TILE_ELEMS * 2, "a staged half fits one stage");
     constexpr int CPR = OC / 8; /* 16-byte chunks per row */
+    constexpr int GR = 32 * FM_; /* rows of a wave group: 2 waves of 16 FM_ rows */
     const int tid = threadIdx.x, lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int grp = (tid >> 6) >> 2;
     uint16_t *const st = grp ? lds1 : lds0;
-    const int hrow = (wm & 1) * 64 + lr;
+    const int hrow = (wm & 1) * (16 * FM_) + lr;
     __syncthreads(); /* every wave is done with the K loop's stages */
     if constexpr (SWIGLU) {
 #pragma unroll
@@ -163,10 +164,10 @@ __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_
         }
     }
     __syncthreads();
-    uint16_t *const out = (uint16_t *)pr.out + (size_t)(m0 + 128 * grp) * pr.ldo + oc0;
+    uint16_t *const out = (uint16_t *)pr.out + (size_t)(m0 + GR * grp) * pr.ldo + oc0;
     const int gt = tid & 255;
 #pragma unroll
-    for (int i = 0; i < 128 * CPR / 256; i++) {
+    for (int i = 0; i < GR * CPR / 256; i++) {
         const int c = gt + 256 * i, row = c / CPR, ch = c - row * CPR;
         *(uint4 *)(out + (size_t)row * pr.ldo + ch * 8) = *(const uint4 *)(st + opos<OC>(row, ch * 8));
     }
@@ -265,7 +266,7 @@ __device__ __forceinline__ void softmax_epilogue(f32x4 (&acc)[FM][FNT_], const G
  * probabilities). The modes are
  * separate kernels: the load-issue phase has no cycles to spare for the
  * address arithmetic of the modes it does not run. */
-template <int MODE, int BNT = BN>
+template <int MODE, int BNT = BN, int BMT = BM>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     constexpr bool CONV = MODE == 1 || MODE == 2, SEG2 = MODE == 3, SMX = MODE == 4 || MODE == 5;
     /* BNT: block tile width, 256, or (MODE 0, no SwiGLU) 224 = 2 waves x 7
@@ -275,7 +276,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * half empty */
     static_assert(BNT == BN || (BNT == 224 && MODE == 0) || (BNT == 128 && (MODE == 1 || MODE == 2)),
                   "narrow tiles are for plain GEMMs and convolutions");
+    /* BMT: block tile height, 256, or 128 (plain GEMMs on few rows: twice
+     * the tiles of a 256-row tile; wave tile 32 x 128) */
+    static_assert(BMT == BM || (BMT == 128 && MODE == 0 && BNT == BN), "128-row tiles are for plain GEMMs");
     constexpr int TWN = BNT / WAVES_N, FNT = TWN / 16, W_DMA = BNT / DMA_ROWS / 4;
+    constexpr int TWM = BMT / WAVES_M, FMT = TWM / 16, A_DMA = BMT / DMA_ROWS / 4;
     /* two stages, each an A tile then a W tile; separate objects so the
      * compiler tracks the LDS-DMA writes of one stage apart from reads of
      * the other */
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     const int gsz = min(tmc - first_m, GROUP_M);
     const int tm = first_m + (t % (GROUP_M * tnc)) % gsz;
     const int tn = (t % (GROUP_M * tnc)) / gsz;
-    const int m0 = tm * BM, n0 = tn * BNT;
+    const int m0 = tm * BMT, n0 = tn * BNT;
 
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * gw + i). */
     const uint16_t *a_base = pr.A + (size_t)m0 * pr.lda;
     const uint16_t *w_base = pr.W + (size_t)n0 * pr.ldw;
-    const int a_rows = min(BM, pr.M - m0), w_rows = min(BNT, pr.N - n0);
+    const int a_rows = min(BMT, pr.M - m0), w_rows = min(BNT, pr.N - n0);
     const __amdgpu_buffer_rsrc_t a_rsrc =
         CONV ? __builtin_amdgcn_make_buffer_rsrc((void *)pr.A, (short)0, (int)P.conv_in_bytes, 0x00020000)
              : __builtin_amdgcn_make_buffer_rsrc((void *)a_base, (short)0, a_rows * pr.lda * 2, 0x00020000);
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 #pragma unroll
     for (int par = 0; par < 2; par++) {
         const int c = dch ^ ((4 * par + (drow >> 1)) & 7);
-        const int row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
+        const int row = gw * A_DMA * DMA_ROWS + drow;
         a_voff[par] = (row * pr.lda + c * 8) * 2;
         /* W: load i of wave gw is tile load j = W_DMA gw + i */
         const int cw = dch ^ ((4 * ((par + (W_DMA & 1) * gw) & 1) + (drow >> 1)) & 7);
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      * at each load from scalars chosen by the K step, so the two segments
      * share one load sequence and no registers are held for the second */
     const int nk1 = pr.K / BK;
-    const int dma_row = gw * DMA_PER_WAVE * DMA_ROWS + drow;
+    const int dma_row = gw * A_DMA * DMA_ROWS + drow;
     __amdgpu_buffer_rsrc_t a2_rsrc = a_rsrc, w2_rsrc = w_rsrc;
     if (SEG2) {
         a2_rsrc = __builtin_amdgcn_make_buffer_rsrc((void *)(pr.A2 + (size_t)m0 * pr.lda2), (short)0,
@@ -372,11 +377,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
     }
     /* convolution: the output pixel of each row this lane loads, y << 16 | x;
      * rows past M get y = 0x4000, outside every image */
-    uint32_t pix[DMA_PER_WAVE];
+    uint32_t pix[A_DMA];
     if (CONV) {
 #pragma unroll
-        for (int i = 0; i < DMA_PER_WAVE; i++) {
-            const int m = m0 + gw * DMA_PER_WAVE * DMA_ROWS + i * DMA_ROWS + drow;
+        for (int i = 0; i < A_DMA; i++) {
+            const int m = m0 + gw * A_DMA * DMA_ROWS + i * DMA_ROWS + drow;
             pix[i] = m < pr.M ? ((uint32_t)(m / P.conv_w) << 16) | (uint32_t)(m % P.conv_w) : 0x40000000u;
         }
     }
@@ -397,11 +402,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             const int hin = MODE == 2 ? 2 * P.conv_h : P.conv_h, win = MODE == 2 ? 2 * P.conv_w : P.conv_w;
             constexpr int mul = MODE == 2 ? 2 : 1, off = MODE == 2 ? 1 : 0;
 #pragma unroll
-            for (int i = 0; i < DMA_PER_WAVE; i++) {
+            for (int i = 0; i < A_DMA; i++) {
                 const int yy = (int)(pix[i] >> 16) * mul + dy + off, xx = (int)(pix[i] & 0xffffu) * mul + dx + off;
                 const bool ok = (unsigned)yy < (unsigned)hin && (unsigned)xx < (unsigned)win;
                 const int src = ((((yy >> up) * (win >> up)) + (xx >> up)) << P.conv_cin_bshift) + a_chunk[i & 1];
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * A_DMA + i) * 512), 16,
                                                          ok ? src : (int)0x80000000u, soff, 0, 0);
             }
         } else if (SEG2) {
@@ -410,13 +415,13 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             const int extra = s2 ? dma_row * ((pr.lda2 - pr.lda) * 2) : 0;
             const int step = s2 ? DMA_ROWS * pr.lda2 * 2 : a_step, ks = (s2 ? kt - nk1 : kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < DMA_PER_WAVE; i++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512), 16,
+            for (int i = 0; i < A_DMA; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)(stage + (gw * A_DMA + i) * 512), 16,
                                                          a_voff[i & 1] + extra + i * step, ks, 0, 0);
         } else {
 #pragma unroll
-            for (int i = 0; i < DMA_PER_WAVE; i++)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * DMA_PER_WAVE + i) * 512),
+            for (int i = 0; i < A_DMA; i++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(stage + (gw * A_DMA + i) * 512),
                                                          16, a_voff[i & 1] + i * a_step, kt * BK * 2, 0, 0);
         }
     };
@@ -427,9 +432,9 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             const int extra = s2 ? dma_row * ((pr.ldw2 - pr.ldw) * 2) : 0;
             const int step = s2 ? DMA_ROWS * pr.ldw2 * 2 : w_step, ks = (s2 ? kt - nk1 : kt) * BK * 2;
 #pragma unroll
-            for (int i = 0; i < DMA_PER_WAVE; i++)
+            for (int i = 0; i < W_DMA; i++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(r,
-                                                         (lds_void *)(stage + TILE_ELEMS + (gw * DMA_PER_WAVE + i) * 512),
+                                                         (lds_void *)(stage + TILE_ELEMS + (gw * W_DMA + i) * 512),
                                                          16, w_voff[i & 1] + extra + i * step, ks, 0, 0);
         } else {
 #pragma unroll
@@ -440,9 +445,9 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         }
     };
 
-    f32x4 acc[FM][FNT];
+    f32x4 acc[FMT][FNT];
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+    for (int i = 0; i < FMT; i++)
 #pragma unroll
         for (int j = 0; j < FNT; j++)
 #pragma unroll
@@ -450,7 +455,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
 
     const int nk = (pr.K + (SEG2 ? pr.K2 : 0)) / BK;
     /* fragments of one K-step: two 32-wide slices */
-    bf16x8 a[2][FM], w[2][FNT];
+    bf16x8 a[2][FMT], w[2][FNT];
     auto frags = [&](const uint16_t *stage) {
         const uint16_t *As = stage;
         const uint16_t *Ws = stage + TILE_ELEMS;
@@ -458,14 +463,14 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         for (int kk = 0; kk < 2; kk++) {
             const int ch = kk * 4 + lg;
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++) a[kk][mi] = *(const bf16x8 *)(As + swz(wm * TW_M + mi * 16 + lr, ch));
+            for (int mi = 0; mi < FMT; mi++) a[kk][mi] = *(const bf16x8 *)(As + swz(wm * TWM + mi * 16 + lr, ch));
 #pragma unroll
             for (int ni = 0; ni < FNT; ni++) w[kk][ni] = *(const bf16x8 *)(Ws + swz(wn * TWN + ni * 16 + lr, ch));
         }
     };
     auto mfmas = [&](int kk) {
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++)
+            for (int mi = 0; mi < FMT; mi++)
 #pragma unroll
                 for (int ni = 0; ni < FNT; ni++)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[kk][ni], a[kk][mi], acc[mi][ni], 0, 0, 0);
@@ -507,7 +512,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
         dma_a(nxt, min(kt + 1, nk - 1));
         /* spread the loads over the fragment reads */
 #pragma unroll
-        for (int i = 0; i < DMA_PER_WAVE; i++) {
+        for (int i = 0; i < A_DMA; i++) {
             __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
@@ -564,12 +569,12 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
      *      each 16x16 tile at the 4 consecutive columns lg*4 .. lg*4+3 ---- */
     const int M = pr.M, N = pr.N, ldo = pr.ldo;
     const float *vec = pr.vec;
-    const int rowb = m0 + wm * TW_M + lr;
+    const int rowb = m0 + wm * TWM + lr;
     const int colb = n0 + wn * TWN + lg * 4;
     /* whole tile in range and 4-wide accesses aligned: one 8- or 16-byte
      * access per lane and 16x16 tile */
     const bool aligned = (ldo & 3) == 0 && ((uintptr_t)pr.out & 15) == 0 && ((uintptr_t)vec & 15) == 0;
-    const bool full = m0 + BM <= M && n0 + BNT <= N && aligned;
+    const bool full = m0 + BMT <= M && n0 + BNT <= N && aligned;
     /* GroupNorm statistics of a convolution's output: each lane sums the
      * values it writes per 4-channel chunk (one group: groups are multiples
      * of 4 channels), then the tile's sums per group are formed in a fixed
@@ -594,7 +599,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
             for (int ni = 0; ni < FNT; ni++) {
                 const float4 t = vec ? *(const float4 *)(vec + colb + ni * 16) : make_float4(0, 0, 0, 0);
 #pragma unroll
-                for (int mi = 0; mi < FM; mi++) {
+                for (int mi = 0; mi < FMT; mi++) {
                     gn_add(ni, acc[mi][ni][0] + t.x);
                     gn_add(ni, acc[mi][ni][1] + t.y);
                     gn_add(ni, acc[mi][ni][2] + t.z);
@@ -602,8 +607,8 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 }
             }
         }
-        if (pr.epi == IRIS_EPI_SWIGLU) stage_out<BNT / 2, true, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0 >> 1, wm, wn, TWN);
-        else stage_out<BNT, false, FM, FNT>(acc, lds0, lds1, pr, vec, m0, n0, wm, wn, TWN);
+        if (pr.epi == IRIS_EPI_SWIGLU) stage_out<BNT / 2, true, FMT, FNT>(acc, lds0, lds1, pr, vec, m0, n0 >> 1, wm, wn, TWN);
+        else stage_out<BNT, false, FMT, FNT>(acc, lds0, lds1, pr, vec, m0, n0, wm, wn, TWN);
         if (!gn) return;
         staged = true;
     }
@@ -627,7 +632,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 for (int r = 0; r < 4; r++) v[r] = vec && col + r < N ? vec[col + r] : vdef;
             }
 #pragma unroll
-            for (int mi = 0; mi < FM; mi++) {
+            for (int mi = 0; mi < FMT; mi++) {
                 const int row = rowb + mi * 16;
                 const f32x4 x = acc[mi][ni];
                 const size_t o = (size_t)row * ldo + col;
@@ -687,7 +692,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 for (int h = 0; h < 2; h++) {
                     const int col = ((n0 + wn * TWN + g * 64) >> 1) + h * 16 + lg * 4;
 #pragma unroll
-                    for (int mi = 0; mi < FM; mi++) {
+                    for (int mi = 0; mi < FMT; mi++) {
                         const int row = rowb + mi * 16;
                         const f32x4 gt = acc[mi][4 * g + h], up = acc[mi][4 * g + 2 + h];
                         uint16_t y[4];
@@ -715,7 +720,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                 if (col >= N) continue;
                 const float v = vec ? vec[col] : 0.0f;
 #pragma unroll
-                for (int mi = 0; mi < FM; mi++) {
+                for (int mi = 0; mi < FMT; mi++) {
                     const int row = rowb + mi * 16;
                     if (row < M) ((float *)pr.out)[(size_t)col * ldo + row] = acc[mi][ni][r] + v;
                 }
@@ -753,7 +758,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmParams P) {
                         q += (double)d[1];
                     }
                 }
-                double *dst = P.gn_part + ((size_t)(m0 / BM) * G + n0 / cpg + t) * 2;
+                double *dst = P.gn_part + ((size_t)(m0 / BMT) * G + n0 / cpg + t) * 2;
                 dst[0] = s;
                 dst[1] = q;
             }
@@ -931,9 +936,10 @@ namespace {
  * The tile width does not change any output element's accumulation order.
  * phase1 > 0: the tiles of the first phase1 problems are dispatched before
  * those of the others (a launch whose last problems fill a part-empty last
- * round); bnt > 0 forces the tile width. */
+ * round); bnt > 0 forces the tile width. bmt = 128: 128 x 256 tiles (no
+ * second K segment). */
 int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float *ws, size_t ws_bytes,
-                int phase1 = 0, int force_bnt = 0) {
+                int phase1 = 0, int force_bnt = 0, int bmt = BM) {
     if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm: %d problems (1..%d)", n, MAXP);
     GemmParams P;
     memset(&P, 0, sizeof(P));
@@ -946,7 +952,8 @@ int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float 
         P.chunks[i] = 1;
         if (p.M <= 0 || p.N <= 0) continue;
         if (check_problem(p)) return -1;
-        P.tiles_m[i] = (p.M + BM - 1) / BM;
+        if (bmt != BM && p.K2) return iris_set_error("gemm: 128-row tiles take no second K segment");
+        P.tiles_m[i] = (p.M + bmt - 1) / bmt;
         if (want && want[i] > 1) {
             const int nk = p.K / BK;
             const int kchunk = (nk + want[i] - 1) / want[i] * BK;
@@ -976,7 +983,9 @@ int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float 
     if (t256 == 0) return 0;
     int bnt = BN;
     const int cus = iris_cu_count();
-    if (force_bnt == 224 && !seg2 && !swiglu_tiles) {
+    if (bmt != BM) {
+        bnt = BN;
+    } else if (force_bnt == 224 && !seg2 && !swiglu_tiles) {
         bnt = 224;
     } else if (!force_bnt && !seg2 && !swiglu_tiles && cus > 0) {
         const long long w256 = (t256 + cus - 1) / cus * BN, w224 = (t224 + cus - 1) / cus * 224;
@@ -997,7 +1006,9 @@ int launch_gemm(const iris_gemm_problem_t *probs, int n, const int *want, float 
     }
     P.per_xcd = (total - P.phase_tiles + 7) / 8;
     const dim3 grid(P.phase_blocks + 8 * P.per_xcd);
-    if (bnt == 224)
+    if (bmt != BM)
+        IRIS_LAUNCH((gemm_bf16_kernel<0, 256, 128>), grid, dim3(NT), 0, iris_stream(), P);
+    else if (bnt == 224)
         IRIS_LAUNCH((gemm_bf16_kernel<0, 224>), grid, dim3(NT), 0, iris_stream(), P);
     else if (seg2)
         IRIS_LAUNCH(gemm_bf16_kernel<3>, grid, dim3(NT), 0, iris_stream(), P);
@@ -1150,26 +1161,53 @@ int tail_plan(const iris_gemm_problem_t &p, size_t ws_bytes, iris_gemm_problem_t
 extern "C" int iris_hip_gemm_fill_n(const iris_gemm_problem_t *probs, int n, float *ws, size_t ws_bytes) {
     if (!probs || n < 1 || n > MAXP) return iris_set_error("gemm_fill: %d problems (1..%d)", n, MAXP);
     const int cus = iris_cu_count();
-    long long tiles = 0;
-    size_t per = 0;
-    int min_nk = 1 << 30;
+    long long tiles = 0, tiles128 = 0;
+    size_t per = 0, out_bytes = 0;
+    int min_nk = 1 << 30, max_nk = 0;
     bool seg2 = false;
     for (int i = 0; i < n; i++) {
         const iris_gemm_problem_t &p = probs[i];
         if (p.M <= 0 || p.N <= 0) continue;
         tiles += (long long)((p.M + BM - 1) / BM) * ((p.N + BN - 1) / BN);
+        tiles128 += (long long)((p.M + 127) / 128) * ((p.N + BN - 1) / BN);
         per += (size_t)p.M * (size_t)p.N * sizeof(float);
+        const bool rmw = p.epi == IRIS_EPI_GATED_ADD || p.epi == IRIS_EPI_ADD;
+        const size_t es = p.epi == IRIS_EPI_BF16 ? 2 : p.epi == IRIS_EPI_SWIGLU ? 1 : rmw ? 8 : 4;
+        out_bytes += (size_t)p.M * (size_t)p.N * es;
         min_nk = std::min(min_nk, p.K / BK);
+        max_nk = std::max(max_nk, p.K / BK);
         seg2 = seg2 || p.K2 > 0;
     }
-    /* tiles filling at most half of the CUs and a long K: split K into up to
-     * CUs / tiles chunks of at least 4 K steps, as many as the workspace holds */
+    /* Tiles filling at most half of the CUs and a long K: split K into up to
+     * CUs / tiles chunks of at least 4 K steps, as many as the workspace
+     * holds, on 256 x 256 tiles, or on 128 x 256 tiles where those still fit
+     * one round (twice the tiles, so fewer chunks: less reduce traffic and
+     * shorter f32 partial epilogues) and an estimate of the launch and its
+     * reduce is lower. The estimate (us): K steps per block times the step
+     * time of the tile shape with the chip partly idle, plus a tile's
+     * prologue and partial store, plus the reduce pass's traffic at 4.5 TB/s
+     * and its launch; measured over the encoder, caption, embedder and
+     * 512x512 products, it picks the faster shape in each. */
     if (tiles > 0 && !seg2 && cus > 0 && ws && 2 * tiles <= cus && min_nk >= 8) {
-        int splits = (int)std::min<long long>(cus / tiles, min_nk / 4);
-        while (splits > 1 && (size_t)splits * per > ws_bytes) splits--;
-        if (splits > 1) {
-            int want[MAXP];
-            for (int i = 0; i < n; i++) want[i] = splits;
+        auto fit = [&](long long s) {
+            s = std::max(1LL, std::min<long long>(s, min_nk / 4));
+            while (s > 1 && (size_t)s * per > ws_bytes) s--;
+            return (int)s;
+        };
+        auto est = [&](bool half, int s) {
+            const double step = half ? 0.9 : 1.3, fixed = half ? 8.0 : 14.0;
+            const double red = s > 1 ? ((double)s * per + out_bytes) / 4.5e6 + 6.0 : 0.0;
+            return (double)max_nk / s * step + fixed + red;
+        };
+        const int s256 = fit(cus / tiles);
+        const int s128 = tiles128 <= cus ? fit(cus / tiles128) : 0;
+        int want[MAXP];
+        if (s128 > 0 && est(true, s128) < est(false, s256)) {
+            for (int i = 0; i < n; i++) want[i] = s128;
+            return launch_gemm(probs, n, s128 > 1 ? want : nullptr, ws, ws_bytes, 0, 0, 128);
+        }
+        if (s256 > 1) {
+            for (int i = 0; i < n; i++) want[i] = s256;
             return launch_gemm(probs, n, want, ws, ws_bytes);
         }
     }

@@ -382,15 +382,11 @@ static iris_gemm_problem_t prob(const uint16_t *A, int lda, const uint16_t *W, i
 }
 
 /* At 512 tokens the N 2560 products are 20 tiles of 256x256 and the QKV
- * product 48: K is split so about 256 blocks run, up to what the workspace
- * holds, with at least 8 K-steps per chunk. */
+ * product 48: iris_hip_gemm_fill splits K (on 128-row tiles where that is
+ * faster) up to what the workspace holds; the gate/up product (152 tiles)
+ * runs as one launch. */
 static int gemm(qwen3_model_t *m, const iris_gemm_problem_t *p) {
-    const int tiles = ((p->M + 255) / 256) * ((p->N + 255) / 256);
-    int splits = tiles >= 128 ? 1 : 256 / tiles;
-    if (splits > p->K / 64 / 8) splits = p->K / 64 / 8;
-    while (splits > 1 && (size_t)splits * p->M * p->N * sizeof(float) > m->ws_bytes) splits--;
-    if (splits > 1) return iris_hip_gemm_splitk(p, splits, m->ws, m->ws_bytes);
-    return iris_hip_gemm(p, 1);
+    return iris_hip_gemm_fill(p, m->ws, m->ws_bytes);
 }
 
 static int rms(const qwen3_model_t *m, const float *w, int S) {

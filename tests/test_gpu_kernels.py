@@ -252,6 +252,37 @@ def cu_count(lib):
     return int(lib.iris_hip_device_name().decode().rsplit(",", 1)[1].split()[0])
 
 
+def fill_plan(shapes, cus, ws_bytes):
+    """The plan iris_hip_gemm_fill_n makes for problems on few tiles (host
+    logic, restated): (tile rows, K chunks), or None when it does not split
+    (the plain or leftover-split launch). shapes: (M, N, K, epi) each."""
+    tiles = sum(-(-m // 256) * -(-n // 256) for m, n, k, e in shapes)
+    tiles128 = sum(-(-m // 128) * -(-n // 256) for m, n, k, e in shapes)
+    per = sum(m * n * 4 for m, n, k, e in shapes)
+    es = {EPI_BF16: 2, EPI_SWIGLU: 1, EPI_GATED_ADD: 8, EPI_ADD: 8}
+    out_bytes = sum(m * n * es.get(e, 4) for m, n, k, e in shapes)
+    min_nk, max_nk = min(k // 64 for *_, k, e in shapes), max(k // 64 for *_, k, e in shapes)
+    if not (2 * tiles <= cus and min_nk >= 8):
+        return None
+
+    def fit(sp):
+        sp = max(1, min(sp, min_nk // 4))
+        while sp > 1 and sp * per > ws_bytes:
+            sp -= 1
+        return sp
+
+    def est(half, sp):
+        step, fixed = (0.9, 8.0) if half else (1.3, 14.0)
+        red = (sp * per + out_bytes) / 4.5e6 + 6.0 if sp > 1 else 0.0
+        return max_nk / sp * step + fixed + red
+
+    s256 = fit(cus // tiles)
+    s128 = fit(cus // tiles128) if tiles128 <= cus else 0
+    if s128 > 0 and est(True, s128) < est(False, s256):
+        return 128, s128
+    return (256, s256) if s256 > 1 else None
+
+
 @pytest.mark.parametrize("rows,N,K,epi", [((512, 1024), 3072, 3072, EPI_GATED_ADD),
                                           ((512, 1024), 3072, 9216, EPI_GATED_ADD),
                                           ((1536,), 3072, 12288, EPI_GATED_ADD), ((300, 77), 640, 1024, EPI_F32),
@@ -263,13 +294,15 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
     block (512 + 1024 rows; out projection K 3072, down projection K 9216)
     and the single block's out projection (1536 x 3072 x 12288), split over
     K in one launch of both problems, against float64; bit for bit equal to
-    iris_hip_gemm_splitk of each problem alone with the same chunk count,
-    and repeatable (also under the per-kernel profile, which asserts one
-    reduce launch for a split). Also ragged rows and columns with an output
-    row stride that is not a multiple of 4 (the reduce's one-element path),
-    SwiGLU, bf16 and residual-add epilogues, and a product that fills the
-    chip (4608 rows: the plain launch, equal to iris_hip_gemm bit for
-    bit)."""
+    iris_hip_gemm_splitk of each problem alone with the same chunk count
+    (the tile height, 256 or 128 rows, does not change an element's
+    additions), or to iris_hip_gemm where the plan is one chunk of 128-row
+    tiles, and repeatable (also under the per-kernel profile, which asserts
+    one reduce launch for a split and the 128-row kernel where planned).
+    Also ragged rows and columns with an output row stride that is not a
+    multiple of 4 (the one-element paths), SwiGLU, bf16 and residual-add
+    epilogues, and a product that fills the chip (4608 rows: the plain
+    launch, equal to iris_hip_gemm bit for bit)."""
     rng = np.random.default_rng(sum(rows) + N + K)
     cus = cu_count(lib)
     P = tl.GemmProblem
@@ -282,9 +315,9 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
         ldo = nout + 2 if (epi == EPI_F32 and i == 1) else nout
         x0 = rng.standard_normal((m, ldo), np.float32)
         ins.append((m, a, w, vec, x0, ldo, tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w)), tl.Dev.of(vec)))
-    tiles = sum((m + 255) // 256 for m in rows) * ((N + 255) // 256)
-    splits = min(cus // tiles, K // 64 // 4) if 2 * tiles <= cus else 1
     ws_bytes = 64 << 20
+    plan = fill_plan([(m, N, K, epi) for m in rows], cus, ws_bytes)
+    splits = plan[1] if plan else 1
     ws = tl.Dev(ws_bytes)
     lib.iris_hip_gemm_fill_n.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
     lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
@@ -334,19 +367,20 @@ def test_gemm_fill_n(lib, rows, N, K, epi):
             assert tl.rel_l2(g[:, :N], y + vec) < 1e-5
             assert np.array_equal(g[:, N:], x0[:, N:]), "wrote past N"
     reduce_pass = any("splitk_reduce_kernel" in k for k in kernels)
-    assert reduce_pass == (splits > 1), (splits, kernels)
+    assert reduce_pass == (splits > 1), (plan, kernels)
+    assert any("128>" in k for k in kernels) == (plan is not None and plan[0] == 128), (plan, kernels)
     want = run("alone" if splits > 1 else "plain")
     for g, w_ in zip(got, want):
         assert np.array_equal(g, w_), f"differs from the {'split-K' if splits > 1 else 'plain'} launch"
-    print(f"fill_n {rows} x {N} x {K}: {splits} chunks")
+    print(f"fill_n {rows} x {N} x {K}: plan {plan}")
 
 
 def test_gemm_fill_split_in_graph(lib):
-    """A product split over K into 3 chunks (1536 x 3072 x 3072, gated
-    residual add; the 512x512 single block's shape class) captured into a
-    graph with its reduce launch: each replay, with an eager launch of the
-    same product between replays, equals the eager result bit for bit."""
-    M, N, K = 1536, 3072, 3072
+    """A product split over K into 3 chunks (1536 x 3072 x 12288, gated
+    residual add: the 512x512 single block's output projection) captured
+    into a graph with its reduce launch: each replay, with an eager launch of
+    the same product between replays, equals the eager result bit for bit."""
+    M, N, K = 1536, 3072, 12288
     rng = np.random.default_rng(77)
     A = tl.Dev.of(tl.to_bf16(bf(rng.standard_normal((M, K), np.float32))))
     W = tl.Dev.of(tl.to_bf16(bf(rng.standard_normal((N, K), np.float32) * 0.02)))
