@@ -173,9 +173,9 @@ __device__ __forceinline__ void stage_out(const f32x4 (&acc)[FM_][FNT_], uint16_
     }
 }
 
-/* The two epilogues of MODE 4 (the products of one query block against the
- * keys of one 256-wide tile): per-row statistics of the tile, or the
- * probabilities. Lane l holds row lr of each 16x16 tile at columns
+/* The epilogues of MODES 4 and 5 (the products of one query block against
+ * the keys of one 256-wide tile): per-row statistics of the tile (STATS), or
+ * the probabilities. Lane l holds row lr of each 16x16 tile at columns
  * lg*4 .. lg*4+3; a row's 256 columns are spread over the 4 lanes lr + 16j of
  * a wave and the 2 waves across N. */
 template <bool STATS, int FNT_>
@@ -229,33 +229,33 @@ __device__ __forceinline__ void softmax_epilogue(f32x4 (&acc)[FM][FNT_], const G
         return;
     } else {
 #pragma unroll
-    for (int mi = 0; mi < FM; mi++) {
-        const int row = rowb + mi * 16;
-        const float2 rs = row < M ? P.sm_row[row] : make_float2(0.0f, 0.0f);
+        for (int mi = 0; mi < FM; mi++) {
+            const int row = rowb + mi * 16;
+            const float2 rs = row < M ? P.sm_row[row] : make_float2(0.0f, 0.0f);
 #pragma unroll
-        for (int ni = 0; ni < FNT_; ni++)
+            for (int ni = 0; ni < FNT_; ni++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[mi][ni][r] = __builtin_amdgcn_exp2f(acc[mi][ni][r] - rs.x) * rs.y;
-    }
-    const int ldo = pr.ldo;
-    if (m0 + BM <= M && n0 + BNT_ <= N && (ldo & 7) == 0 && ((uintptr_t)pr.out & 15) == 0) {
-        stage_out<BNT_, false, FM, FNT_>(acc, lds0, lds1, pr, nullptr, m0, n0, wm, wn, TWN_);
-        return;
-    }
-    /* edge tiles element by element, zeros in the padding columns */
+                for (int r = 0; r < 4; r++) acc[mi][ni][r] = __builtin_amdgcn_exp2f(acc[mi][ni][r] - rs.x) * rs.y;
+        }
+        const int ldo = pr.ldo;
+        if (m0 + BM <= M && n0 + BNT_ <= N && (ldo & 7) == 0 && ((uintptr_t)pr.out & 15) == 0) {
+            stage_out<BNT_, false, FM, FNT_>(acc, lds0, lds1, pr, nullptr, m0, n0, wm, wn, TWN_);
+            return;
+        }
+        /* edge tiles element by element, zeros in the padding columns */
 #pragma unroll
-    for (int mi = 0; mi < FM; mi++) {
-        const int row = rowb + mi * 16;
-        if (row >= M) continue;
+        for (int mi = 0; mi < FM; mi++) {
+            const int row = rowb + mi * 16;
+            if (row >= M) continue;
 #pragma unroll
-        for (int ni = 0; ni < FNT_; ni++)
+            for (int ni = 0; ni < FNT_; ni++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int col = colb + ni * 16 + r;
-                if (col < P.sm_pad)
-                    ((uint16_t *)pr.out)[(size_t)row * ldo + col] = col < N ? f2bf_hw(acc[mi][ni][r]) : (uint16_t)0;
-            }
-    }
+                for (int r = 0; r < 4; r++) {
+                    const int col = colb + ni * 16 + r;
+                    if (col < P.sm_pad)
+                        ((uint16_t *)pr.out)[(size_t)row * ldo + col] = col < N ? f2bf_hw(acc[mi][ni][r]) : (uint16_t)0;
+                }
+        }
     }
 }
 
