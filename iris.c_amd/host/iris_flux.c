@@ -878,23 +878,30 @@ static int enqueue_forward(iris_transformer_t *tf) {
     /* timestep MLP (:1366-1379) and the modulation GEMVs on SiLU(t_emb) (:4059-4069,
      * :3787-3797, :4270-4277); the single-block modulation is the same for all
      * 20 blocks and is computed once */
-    CK(iris_hip_gemv(w->tmp, tf->t_fc1, w->tsin, NULL, h, 256, 0));
+    /* The embedders below and the GEMV chain here are independent (token
+     * rows and residual stream vs the time embedding and modulation vector):
+     * the embedders run on the side stream beside the GEMVs, joined before
+     * the first block; one after the other while profiling. */
+    const int side = !iris_hip_profile_enabled();
+    if (side) CK(iris_hip_fork());
+    int rc = iris_hip_gemv(w->tmp, tf->t_fc1, w->tsin, NULL, h, 256, 0);
     /* the CSD style delta is added to temb before its SiLU (iris_transformer_flux.c:3969-3972):
      * the bias of the second time-MLP linear */
-    CK(iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, w->csd_on ? tf->d_csd : NULL, h, h, 1));
+    if (!rc) rc = iris_hip_gemv(w->temb, tf->t_fc2, w->tmp, w->csd_on ? tf->d_csd : NULL, h, h, 1);
     /* the four modulation linears in one GEMV over their stacked rows:
      * mod = dimg 6h | dtxt 6h | single 3h | final 2h */
-    CK(iris_hip_gemv(w->mod, tf->mod_all, w->temb, NULL, 17 * h, h, 1));
+    if (!rc) rc = iris_hip_gemv(w->mod, tf->mod_all, w->temb, NULL, 17 * h, h, 1);
+    iris_hip_side(side);
     /* NCHW -> token rows for the target and each reference (:3986-3993, :4667-4689) */
     size_t off = 0;
-    CK(iris_hip_nchw_to_tokens(w->tok, w->lat, C, I0));
+    if (!rc) rc = iris_hip_nchw_to_tokens(w->tok, w->lat, C, I0);
     off = I0;
-    for (int r = 0; r < w->n_refs; r++) {
+    for (int r = 0; r < w->n_refs && !rc; r++) {
         int rs = w->ref_h[r] * w->ref_w[r];
-        CK(iris_hip_nchw_to_tokens(w->tok + off * C, w->lat + off * C, C, rs));
+        rc = iris_hip_nchw_to_tokens(w->tok + off * C, w->lat + off * C, C, rs);
         off += rs;
     }
-    CK(iris_hip_f32_to_bf16(w->txtb, w->txtf, (size_t)B * T * td));
+    if (!rc) rc = iris_hip_f32_to_bf16(w->txtb, w->txtf, (size_t)B * T * td);
     /* img_in / txt_in into the residual stream rows [T, S) and [0, T) (:4022-4031):
      * the image rows (K = latent channels) in one launch, then each text
      * stream (K = text_dim, few rows) split over K */
@@ -902,12 +909,16 @@ static int enqueue_forward(iris_transformer_t *tf) {
     int n = 0;
     for (int b = 0; b < B; b++)
         p[n++] = prob(w->tok, C, tf->img_in, C, w->x + ((size_t)b * S + T) * h, h, NULL, w->I, h, C, IRIS_EPI_F32);
-    CK(gemm(p, n));
-    for (int b = 0; b < B; b++) {
+    if (!rc) rc = gemm(p, n);
+    for (int b = 0; b < B && !rc; b++) {
         p[0] = prob(w->txtb + (size_t)b * T * td, td, tf->txt_in, td, w->x + (size_t)b * S * h, h, NULL, T, h, td,
                     IRIS_EPI_F32);
-        CK(gemm_fill(tf, p, 1));
+        rc = gemm_fill(tf, p, 1);
     }
+    iris_hip_side(0);
+    /* once forked, the side stream is joined whatever failed after the fork */
+    if (side && iris_hip_join() && !rc) rc = -1;
+    CK(rc);
     for (int i = 0; i < tf->n_double; i++) CK(double_block_forward(tf, i));
     for (int i = 0; i < tf->n_single; i++) CK(single_block_forward(tf, i));
     /* final layer on the target rows: AdaLN with (scale, shift) order, proj_out,
