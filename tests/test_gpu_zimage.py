@@ -185,3 +185,24 @@ def test_full_width_reduced_depth(lib, orc):
     lib.zi_transformer_free(tf)
     orc.orc_zi_free(m)
     assert tl.rel_l2(got, ref) < 1e-2 and tl.cosine(got, ref) > 0.999
+
+
+def test_graph_forward_bitwise(lib):
+    """Z-Image-Turbo widths with two refiner pairs and one main layer, 128x128
+    latent (4096 image tokens) and 512 caption tokens: the captured forward
+    equals the profiled forward (the same launches issued one by one) bit
+    for bit, over repeated replays."""
+    args = (3840, 30, 1, 2, 2560, 16, 2, F(256.0), axes_arr([32, 48, 48]), 10240, 1024, 7)
+    tf = lib.zi_transformer_create_synthetic(*args)
+    assert tf, lib.iris_hip_last_error()
+    tf = ctypes.c_void_p(tf)
+    lat = tl.synth_f32((16, 128, 128), 91)
+    cap = tl.synth_f32((512, 2560), 92)
+    graph = forward(lib, tf, lat, 128, 0.6, cap)
+    assert lib.iris_hip_profile_enable(1) == 0
+    seq = forward(lib, tf, lat, 128, 0.6, cap)
+    assert lib.iris_hip_profile_enable(0) == 0
+    np.testing.assert_array_equal(seq, graph)
+    for _ in range(3):
+        np.testing.assert_array_equal(forward(lib, tf, lat, 128, 0.6, cap), graph)
+    lib.zi_transformer_free(tf)
