@@ -247,6 +247,53 @@ def test_gemm_fill(lib, M, N, K, epi, ws_mb):
     print(f"fill {'split-K' if split else 'plain'}: rel_l2 {tl.rel_l2(outs[0], ref):.2e}")
 
 
+@pytest.mark.parametrize("M", [1, 7, 129, 255, 300])
+@pytest.mark.parametrize("epi", [EPI_F32, EPI_BF16, EPI_GATED_ADD, EPI_SWIGLU, EPI_F32_T, EPI_ADD])
+def test_gemm_tile_heights_bitwise(lib, M, epi):
+    """Products on few rows: iris_hip_gemm runs them on 128-row tiles,
+    iris_hip_gemm_splitk with one chunk on 256-row tiles; every epilogue
+    gives the same bits either way (an element's additions do not depend on
+    the tile height), for ragged row counts and N not a multiple of the tile
+    width, and matches float64."""
+    N, K = (640 if epi == EPI_SWIGLU else 600), 512
+    rng = np.random.default_rng(M * 10 + epi)
+    a = bf(rng.standard_normal((M, K), np.float32))
+    w = bf(rng.standard_normal((N, K), np.float32) * 0.03)
+    vec = rng.standard_normal(N).astype(np.float32)
+    nout = N // 2 if epi == EPI_SWIGLU else N
+    shape = (nout, M) if epi == EPI_F32_T else (M, nout)
+    bf16_out = epi in (EPI_BF16, EPI_SWIGLU)
+    x0 = rng.standard_normal(shape).astype(np.float32)
+    A, W, V = tl.Dev.of(tl.to_bf16(a)), tl.Dev.of(tl.to_bf16(w)), tl.Dev.of(vec)
+    ws = tl.Dev(1 << 20)
+    lib.iris_hip_gemm_splitk.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+    outs, kernels = [], []
+    for mode in ("plain", "splitk1"):
+        o = tl.Dev(M * nout * 2) if bf16_out else tl.Dev.of(x0)
+        ldo = M if epi == EPI_F32_T else nout
+        pr = tl.GemmProblem(A.ptr, W.ptr, o.ptr, None if epi == EPI_SWIGLU else V.ptr, M, N, K, K, K, ldo, epi)
+        call = (lambda: lib.iris_hip_gemm(ctypes.byref(pr), 1)) if mode == "plain" else \
+            (lambda: lib.iris_hip_gemm_splitk(ctypes.byref(pr), 1, ws.ptr, 1 << 20))
+        kernels.append(launched_kernels(lib, call))
+        outs.append(tl.bf16_to_f32(o.get(np.uint16, shape)) if bf16_out else o.get(np.float32, shape))
+    assert any("128>" in k for k in kernels[0]) and not any("128>" in k for k in kernels[1]), kernels
+    assert np.array_equal(outs[0], outs[1]), "tile heights differ"
+    y = a.astype(np.float64) @ w.astype(np.float64).T
+    if epi == EPI_SWIGLU:
+        gt = np.concatenate([y[:, c * 64:c * 64 + 32] for c in range(N // 64)], 1)
+        up = np.concatenate([y[:, c * 64 + 32:c * 64 + 64] for c in range(N // 64)], 1)
+        ref = gt / (1 + np.exp(-gt)) * up
+    elif epi == EPI_GATED_ADD:
+        ref = x0 + vec * y
+    elif epi == EPI_ADD:
+        ref = x0 + y + vec
+    elif epi == EPI_F32_T:
+        ref = (y + vec).T
+    else:
+        ref = y + vec
+    assert tl.rel_l2(outs[0], ref) < (4e-3 if bf16_out else 1e-5)
+
+
 def cu_count(lib):
     lib.iris_hip_device_name.restype = ctypes.c_char_p
     return int(lib.iris_hip_device_name().decode().rsplit(",", 1)[1].split()[0])
