@@ -22,7 +22,10 @@ beside its QKV product and attention); the per-kernel table is
 back_to_back_launch_ms times the same kernel alone over 30 launches on the
 step's resident buffers. `cpu_baseline` times the oracle (C restatement of the reference's
 f32 `make blas` path on OpenBLAS) on one block of each kind at the same shape,
-extrapolated to a step.
+extrapolated to a step. With the default workload the line also carries
+`other_configs`: c2, c3, c4, c5, qwen3 and vae, each run by this script in a
+child process after the default workload is measured (--no-other-configs
+skips them).
 """
 import argparse
 import ctypes
@@ -653,6 +656,8 @@ def main():
     ap.add_argument("--probe", choices=["gemm", "attn", "copy", "rownorm", "kvprep"],
                     help="only launch one kernel class a few times (for counter runs)")
     ap.add_argument("--probe-launches", type=int, default=3)
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="with the default workload, skip measuring the other workloads in child processes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: runs on one GPU; --gpus {args.gpus} is not supported "
@@ -704,9 +709,52 @@ def main():
         # the profiled step: every launch between two events, the launches issued one by one
         result["profiled_step"] = {"kernel_ms": round(sum(r["total_ms"] for r in prof), 3),
                                    "top": prof[:10]}
+    if args.config == "ns" and not args.no_other_configs:
+        result["other_configs"] = other_configs(args)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = {"qwen3": cpu_baseline_qwen3, "vae": cpu_baseline_vae}.get(c["kind"], cpu_baseline)(c)
     print(json.dumps(result))
+
+
+OTHER_CONFIGS = ["c2", "c3", "c4", "c5", "qwen3", "vae"]
+
+
+def other_configs(args):
+    """The other workloads, each measured by this script in a child process
+    (`--config X --no-cpu-baseline`, the same steps and warm-up), one after
+    the other once the default workload's line is complete, so that a failure
+    in one leaves this line and the others intact. Per workload: its metric,
+    value and ms per step, the step's MFMA fraction, the dominant kernel in
+    the step and, where the workload has a committed golden, its parity."""
+    out = {}
+    for name in OTHER_CONFIGS:
+        t0 = time.time()
+        cmd = [sys.executable, os.path.abspath(__file__), "--config", name, "--no-cpu-baseline",
+               "--steps", str(args.steps), "--warmup", str(args.warmup)]
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+            lines = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
+            if p.returncode != 0 or not lines:
+                tail = (p.stderr.strip().splitlines() or [""])[-1]
+                out[name] = {"error": f"exit status {p.returncode}: {tail[:300]}"}
+            else:
+                r = json.loads(lines[-1])
+                rl = r["roofline"]
+                entry = {"value": r["value"], "unit": r["unit"],
+                         "ms_per_step": r["ms_per_step"], "mfma_frac_step": r["mfma_frac_step"],
+                         "workload": r["config"]["workload"],
+                         "roofline": {"kernel": rl["kernel"], "launch_ms": rl["launch_ms"], "frac": rl["frac"]},
+                         "kernels": [{"key": k["key"], "launch_ms": k["launch_ms"], "frac": k["frac"]}
+                                     for k in r["kernels"]]}
+                if r["metric"] != METRIC:
+                    entry = {"metric": r["metric"], **entry}
+                if "parity" in r:
+                    entry["parity"] = r["parity"]
+                out[name] = entry
+        except subprocess.TimeoutExpired:
+            out[name] = {"error": "no result within 300 s"}
+        print(f"bench.py: {name} measured in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
+    return out
 
 
 def cpu_baseline(c):
