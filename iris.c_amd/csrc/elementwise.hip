@@ -38,7 +38,7 @@ __global__ __launch_bounds__(NT) void rownorm_kernel(const iris_norm_args_t a) {
 #pragma unroll
     for (int i = 0; i < V; i++) {
         const int c = t + i * NT;
-        v[i] = c < nv ? ((const float4 *)x)[c] : make_float4(0, 0, 0, 0);
+        v[i] = c < nv ? ld_stream((const float4 *)x + c) : make_float4(0, 0, 0, 0);
     }
     const bool use_b = (a.period ? row % a.period : row) >= a.split;
     const float *shift = use_b ? a.shiftB : a.shiftA;
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
 #pragma unroll
     for (int i = 0; i < V; i++) {
         const int c = t + i * NT;
-        v[i] = c < nv ? ((const float4 *)yr)[c] : make_float4(0, 0, 0, 0);
+        v[i] = c < nv ? ld_stream((const float4 *)yr + c) : make_float4(0, 0, 0, 0);
         q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
     }
     q = wave_sum(q);
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(NT) void gemv_kernel(float *y, const uint16_t *W, c
     if (n < N) {
         const uint16_t *w = W + (size_t)n * K;
         for (int k = l * 8; k < K; k += step) {
-            const u16x8 wv = *(const u16x8 *)(w + k);
+            const u16x8 wv = __builtin_nontemporal_load((const u16x8 *)(w + k));   /* weights: read once */
             float4 xa, xb;
             if constexpr (XLDS) {
                 xa = *(const float4 *)(xl + k);

@@ -803,7 +803,7 @@ __global__ void splitk_reduce_kernel(const ReduceParams R) {
             float4 g = make_float4(0.0f, 0.0f, 0.0f, 0.0f), u = g;
             for (int k = 0; k < splits; k++) {
                 const float *row = ws + k * stride + (size_t)m * p.N;
-                const float4 a = *(const float4 *)(row + gc), b = *(const float4 *)(row + gc + 32);
+                const float4 a = ld_stream((const float4 *)(row + gc)), b = ld_stream((const float4 *)(row + gc + 32));
                 g.x += a.x; g.y += a.y; g.z += a.z; g.w += a.w;
                 u.x += b.x; u.y += b.y; u.z += b.z; u.w += b.w;
             }
@@ -814,7 +814,7 @@ __global__ void splitk_reduce_kernel(const ReduceParams R) {
         }
         float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         for (int k = 0; k < splits; k++) {
-            const float4 a = *(const float4 *)(ws + k * stride + (size_t)m * p.N + c);
+            const float4 a = ld_stream((const float4 *)(ws + k * stride + (size_t)m * p.N + c));
             s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
         }
         const float vd = p.epi == IRIS_EPI_GATED_ADD ? 1.0f : 0.0f;
