@@ -732,7 +732,7 @@ def other_configs(args):
         cmd = [sys.executable, os.path.abspath(__file__), "--config", name, "--no-cpu-baseline",
                "--steps", str(args.steps), "--warmup", str(args.warmup)]
         try:
-            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=150)
             lines = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
             if p.returncode != 0 or not lines:
                 tail = (p.stderr.strip().splitlines() or [""])[-1]
@@ -752,7 +752,7 @@ def other_configs(args):
                     entry["parity"] = r["parity"]
                 out[name] = entry
         except subprocess.TimeoutExpired:
-            out[name] = {"error": "no result within 300 s"}
+            out[name] = {"error": "no result within 150 s"}
         print(f"bench.py: {name} measured in {time.time() - t0:.1f} s", file=sys.stderr, flush=True)
     return out
 

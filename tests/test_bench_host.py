@@ -45,7 +45,7 @@ def test_other_configs_collects_children(monkeypatch):
         assert "--no-cpu-baseline" in c
         assert c[c.index("--steps") + 1] == "3" and c[c.index("--warmup") + 1] == "1"
     assert out["c3"] == {"error": "exit status 1: AssertionError: boom"}
-    assert out["c4"] == {"error": "no result within 300 s"}
+    assert out["c4"] == {"error": "no result within 150 s"}
     assert out["vae"]["error"].startswith("exit status 0")
     # the headline metric text is not repeated for the other Flux workloads
     assert "metric" not in out["c2"] and out["qwen3"]["metric"] == "ms per text encode"
