@@ -136,7 +136,7 @@ __global__ __launch_bounds__(NT) void rms_gated_add_kernel(float *x, const float
     for (int i = 0; i < V; i++) {
         const int c = t + i * NT;
         if (c >= nv) continue;
-        float4 xo = ((float4 *)xr)[c];
+        float4 xo = ld_stream((const float4 *)xr + c);
         const float4 w4 = ((const float4 *)w)[c];
         float4 g4 = make_float4(1, 1, 1, 1);
         if (gate) g4 = ((const float4 *)gate)[c];
@@ -195,7 +195,7 @@ __device__ __forceinline__ void qk_norm_rope_rows(const iris_qkprep_args_t &a, i
             const int head = hb + hq;
             const bool on = head < nh;                        /* uniform per 16-lane group */
             u16x8 raw = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (on) raw = *(const u16x8 *)(src + head * 128);
+            if (on) raw = __builtin_nontemporal_load((const u16x8 *)(src + head * 128));
             float x[8];
             float ss = 0.0f;
 #pragma unroll
@@ -226,8 +226,8 @@ __device__ __forceinline__ void v_transpose_tile(const iris_qkprep_args_t &a, in
         const int ra = r0 + 2 * p;
         const uint16_t *src = a.qkv + (size_t)ra * a.ld_qkv + a.col_v + head * 128 + ch * 8;
         u16x8 va = {0, 0, 0, 0, 0, 0, 0, 0}, vb = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (ra < a.rows) va = *(const u16x8 *)src;
-        if (ra + 1 < a.rows) vb = *(const u16x8 *)(src + a.ld_qkv);
+        if (ra < a.rows) va = __builtin_nontemporal_load((const u16x8 *)src);
+        if (ra + 1 < a.rows) vb = __builtin_nontemporal_load((const u16x8 *)(src + a.ld_qkv));
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int d = ch * 8 + j;
