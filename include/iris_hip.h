@@ -361,6 +361,11 @@ int iris_hip_patchify(uint16_t *d_out, const float *d_latent, int C, int H, int 
 int iris_hip_unpatchify(float *d_latent, const float *d_patches, int C, int H, int W, int ps);
 /* copy one f32 row vector into rows [r0, r1) of a [*, cols] matrix */
 int iris_hip_fill_rows(float *d_x, const float *d_row, int r0, int r1, int cols);
+/* x[r][c0 + j] = tanh(x[r][c0 + j]) for r < rows, j < len ([rows][ld] f32):
+ * the gate columns of Z-Image's modulation vectors once per step (tanh(gate)
+ * of zi_block_forward, iris_transformer_zimage.c:818-836), so the gated
+ * residual adds take them with gate_tanh 0. */
+int iris_hip_tanh_cols(float *d_x, int rows, int ld, int c0, int len);
 /* out[r][c] = table[ids[r]][c] (bf16 table [vocab][cols] -> f32), zeros for
  * ids outside [0, vocab) */
 int iris_hip_embed_rows(float *d_out, const uint16_t *d_table, const int *d_ids, int rows, int cols, int vocab);

@@ -369,6 +369,17 @@ __global__ void fill_rows_kernel(float *x, const float *row, int r0, int r1, int
         x[(size_t)r0 * cols + i] = row[i % cols];
 }
 
+/* x[r][c0 + j] = tanh(x[r][c0 + j]) for j < len: Z-Image's gate columns of
+ * the step's modulation vectors, once per step instead of once per element
+ * of every gated residual add. */
+__global__ void tanh_cols_kernel(float *x, int rows, int ld, int c0, int len) {
+    const size_t n = (size_t)rows * len;
+    for (size_t i = blockIdx.x * (size_t)NT + threadIdx.x; i < n; i += (size_t)gridDim.x * NT) {
+        float *p = x + (i / len) * ld + c0 + i % len;
+        *p = tanhf(*p);
+    }
+}
+
 /* Token embedding lookup (iris_qwen3.c:1080-1091): one block row per token,
  * 8 bf16 per thread per step; ids outside the table give a zero row. */
 __global__ void embed_rows_kernel(float *out, const uint16_t *table, const int *ids, int rows, int cols, int vocab) {
@@ -550,6 +561,14 @@ int iris_hip_fill_rows(float *x, const float *row, int r0, int r1, int cols) {
     size_t n = (size_t)(r1 - r0) * cols;
     IRIS_LAUNCH(fill_rows_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), x, row, r0, r1, cols);
     return iris_launch_check("fill_rows_kernel");
+}
+
+int iris_hip_tanh_cols(float *x, int rows, int ld, int c0, int len) {
+    if (rows <= 0 || len <= 0) return 0;
+    if (c0 < 0 || c0 + len > ld) return iris_set_error("tanh_cols: columns %d..%d outside ld %d", c0, c0 + len, ld);
+    const size_t n = (size_t)rows * len;
+    IRIS_LAUNCH(tanh_cols_kernel, dim3(grid1d(n)), dim3(NT), 0, iris_stream(), x, rows, ld, c0, len);
+    return iris_launch_check("tanh_cols_kernel");
 }
 
 int iris_hip_embed_rows(float *out, const uint16_t *table, const int *ids, int rows, int cols, int vocab) {

@@ -481,7 +481,8 @@ static int rms(zi_transformer_t *tf, const float *x, uint16_t *out, int rows, co
 /* zi_block_forward (:790-870) on rows [r0, r0 + n) of the unified sequence;
  * keys outside [klo0, khi0) U [klo1, khi1) (relative to r0) are padding. mod
  * is NULL for the unmodulated context refiner, else 1+scale_msa | gate_msa |
- * 1+scale_mlp | gate_mlp (gates before tanh). */
+ * 1+scale_mlp | gate_mlp, the gates already through tanh (iris_hip_tanh_cols
+ * after the modulation GEMV). */
 static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const float *mod, int r0, int n,
                             int klo0, int khi0, int klo1, int khi1) {
     zi_work_t *w = &tf->w;
@@ -515,14 +516,14 @@ static int zi_block_forward(zi_transformer_t *tf, const zi_dev_block_t *b, const
     p = zprob(w->attn, d, b->o, w->y, d, NULL, n, d, d, IRIS_EPI_F32);
     CK(zgemm(tf, &p));
     /* x += tanh(gate_msa) * norm2(attn_out) */
-    CK(iris_hip_rms_gated_add(x, w->y, b->n2, mod ? mod + d : NULL, n, d, ZI_EPS, 1));
+    CK(iris_hip_rms_gated_add(x, w->y, b->n2, mod ? mod + d : NULL, n, d, ZI_EPS, 0));
     /* FFN: x += tanh(gate_mlp) * norm2(w2(silu(w1 h) * w3 h)), h = norm1(x) * (1 + scale_mlp) */
     CK(rms(tf, x, w->a, n, b->fn1, mod ? mod + 2 * d : NULL));
     p = zprob(w->a, d, b->w13, w->ffn, f, NULL, n, 2 * f, d, IRIS_EPI_SWIGLU);
     CK(zgemm(tf, &p));
     p = zprob(w->ffn, f, b->w2, w->y, d, NULL, n, d, f, IRIS_EPI_F32);
     CK(zgemm(tf, &p));
-    CK(iris_hip_rms_gated_add(x, w->y, b->fn2, mod ? mod + 3 * d : NULL, n, d, ZI_EPS, 1));
+    CK(iris_hip_rms_gated_add(x, w->y, b->fn2, mod ? mod + 3 * d : NULL, n, d, ZI_EPS, 0));
     return 0;
 }
 
@@ -537,6 +538,9 @@ static int zi_enqueue(zi_transformer_t *tf) {
      * 1 + W SiLU(t_emb) + b (:1563-1574) */
     CK(iris_hip_gemv(w->mods, tf->ada_all_w, w->temb, tf->ada_all_b, (tf->refiners + tf->layers) * 4 * d,
                      tf->adaln_dim, 0));
+    /* tanh of the gate columns ([d, 2d) and [3d, 4d) of each block's 4d),
+     * once: viewed as rows of 2d, the gates are columns [d, 2d) of each */
+    CK(iris_hip_tanh_cols(w->mods, 2 * (tf->refiners + tf->layers), 2 * d, d, d));
     CK(iris_hip_gemv(w->fscale, tf->f_ada_w, w->temb, tf->f_ada_b1, d, tf->adaln_dim, 1));
     /* patchify (ph, pw, c) and embed image rows [0, I); padding rows get x_pad_token */
     CK(iris_hip_patchify(w->patches, w->lat, tf->in_ch, w->lh, w->lw, tf->ps));
@@ -588,6 +592,7 @@ int zi_block_forward_resident(zi_transformer_t *tf, int kind, int idx) {
     const zi_dev_block_t *b = kind == 0 ? &tf->nr[idx] : &tf->ly[idx];
     float *mod = w->mods + (size_t)(kind == 0 ? idx : tf->refiners + idx) * 4 * d;
     if (iris_hip_gemv(mod, b->ada_w, w->temb, b->ada_b, 4 * d, tf->adaln_dim, 0)) return -1;
+    if (iris_hip_tanh_cols(mod, 2, 2 * d, d, d)) return -1;
     if (kind == 0 ? zi_block_forward(tf, b, mod, 0, w->Ip, 0, w->I, 0, 0)
                   : zi_block_forward(tf, b, mod, 0, w->U, 0, w->I, w->Ip, w->Ip + w->cap_len))
         return -1;

@@ -162,6 +162,7 @@ def hip():
         lib.iris_hip_rms_gated_add.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                                ctypes.c_int]
         lib.iris_hip_fill_rows.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        lib.iris_hip_tanh_cols.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         lib.iris_transformer_load_safetensors.restype = vp
         lib.iris_transformer_create_synthetic.restype = vp
         lib.iris_transformer_create_synthetic.argtypes = [ctypes.c_int] * 6 + [ctypes.c_float, ctypes.c_float,

@@ -941,6 +941,33 @@ def test_rms_gated_add(lib, gate_mode):
     assert tl.rel_l2(dx.get(np.float32, (rows, cols)), want) < 1e-6
 
 
+def test_tanh_cols_then_plain_gate(lib):
+    """iris_hip_tanh_cols on Z-Image's modulation layout (gates at [d, 2d)
+    and [3d, 4d) of each block's 4d, taken as columns [d, 2d) of rows of 2d):
+    the other columns untouched, the gates tanh'd, and the gated add with
+    gate_tanh 0 over them gives the bits of gate_tanh 1 over the raw gates."""
+    rng = np.random.default_rng(8)
+    nblk, d, rows = 5, 3840, 33
+    mods = (rng.standard_normal((nblk, 4 * d)) * 2).astype(np.float32)
+    dm = tl.Dev.of(mods)
+    assert lib.iris_hip_tanh_cols(dm.ptr, 2 * nblk, 2 * d, d, d) == 0
+    got = dm.get(np.float32, (nblk, 4 * d))
+    for lo, hi in ((0, d), (2 * d, 3 * d)):
+        assert np.array_equal(got[:, lo:hi], mods[:, lo:hi])
+    for lo, hi in ((d, 2 * d), (3 * d, 4 * d)):
+        assert np.abs(got[:, lo:hi].astype(np.float64) - np.tanh(mods[:, lo:hi].astype(np.float64))).max() < 2e-7
+    x = rng.standard_normal((rows, d), np.float32)
+    y = rng.standard_normal((rows, d), np.float32)
+    w = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    dy, dw = tl.Dev.of(y), tl.Dev.of(w)
+    raw_gate, tanh_gate = tl.Dev.of(mods[2, 3 * d:]), tl.Dev.of(got[2, 3 * d:])
+    dx1, dx0 = tl.Dev.of(x), tl.Dev.of(x)
+    assert lib.iris_hip_rms_gated_add(dx1.ptr, dy.ptr, dw.ptr, raw_gate.ptr, rows, d, 1e-6, 1) == 0
+    assert lib.iris_hip_rms_gated_add(dx0.ptr, dy.ptr, dw.ptr, tanh_gate.ptr, rows, d, 1e-6, 0) == 0
+    assert np.array_equal(dx0.get(np.uint32, (rows, d)), dx1.get(np.uint32, (rows, d)))
+    assert lib.iris_hip_tanh_cols(dm.ptr, 2, 2 * d, d + 1, d) == -1   # columns past ld
+
+
 @pytest.mark.parametrize("ktables", [False, True])
 def test_qk_prepare(lib, ktables):
     """Q/K RMSNorm + rotary; with ktables, K rotates with its own tables
